@@ -1,0 +1,176 @@
+// optim_math.h -- per-element update arithmetic of the three fused optimizers,
+// plus the storage-type conversions the kernels need.
+//
+// Bit-exactness contract. On the MI355X the update of every active replica must
+// be bit-identical to torch's own ROCm fused kernels (`torch._fused_adam_`,
+// `_fused_adamw_`, `_fused_sgd_`, `_fused_adagrad_`). The reference gets that on
+// its GPU by calling ATen's device math verbatim (src/torchstrap/kernels/csrc/
+// cuda/adam.cu:146-157, cuda/adagrad.cu:141-148) or by transcribing it
+// (cuda/sgd.cu:90-132). This file restates the same arithmetic: the order of the
+// operations, the type each intermediate is held in (float vs double) and the
+// point where a double is narrowed to float are the algorithm, so they follow the
+// ROCm headers shipped with torch 2.10.0+rocm7.0:
+//   torch/include/ATen/native/hip/fused_adam_utils.cuh:28-92   (adam_math)
+//   torch/include/ATen/native/hip/fused_adam_utils.cuh:131-139 (bias corrections)
+//   torch/include/ATen/native/hip/fused_adagrad_utils.cuh:16-50, 75-81
+// Multiply-add contraction is left to the compiler (hipcc's default
+// -ffp-contract=fast), exactly as for those headers; float division and sqrt
+// are IEEE correctly rounded (hipcc's default). Do not reassociate or hand-fuse
+// these expressions: each one is checked bit-for-bit against torch on the GPU.
+#pragma once
+
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+
+namespace churten {
+
+// ---------------------------------------------------------------------------
+// Storage types. fp16 is clang's _Float16; bf16 is carried as raw bits with
+// c10::BFloat16's conversions (widen = shift, narrow = round to nearest even,
+// NaN -> quiet NaN).
+// ---------------------------------------------------------------------------
+struct bf16_t {
+  uint16_t bits;
+};
+
+template <typename T> struct op_type { using type = float; };
+template <> struct op_type<double> { using type = double; };
+template <typename T> using op_t = typename op_type<T>::type;
+
+__device__ __forceinline__ float widen(float x) { return x; }
+__device__ __forceinline__ double widen(double x) { return x; }
+__device__ __forceinline__ float widen(_Float16 x) { return static_cast<float>(x); }
+__device__ __forceinline__ float widen(bf16_t x) {
+  return __uint_as_float(static_cast<uint32_t>(x.bits) << 16);
+}
+
+template <typename T> __device__ __forceinline__ T narrow(op_t<T> x);
+template <> __device__ __forceinline__ float narrow<float>(float x) { return x; }
+template <> __device__ __forceinline__ double narrow<double>(double x) { return x; }
+template <> __device__ __forceinline__ _Float16 narrow<_Float16>(float x) {
+  return static_cast<_Float16>(x);
+}
+template <> __device__ __forceinline__ bf16_t narrow<bf16_t>(float x) {
+  bf16_t out;
+  if (x != x) {
+    out.bits = 0x7FC0u;
+  } else {
+    const uint32_t u = __float_as_uint(x);
+    out.bits = static_cast<uint16_t>((u + 0x7FFFu + ((u >> 16) & 1u)) >> 16);
+  }
+  return out;
+}
+
+// ---------------------------------------------------------------------------
+// Adam / AdamW. Hyperparameters are doubles (ATen passes them as
+// `const double&`), so the moment updates and the weight-decay terms are fp64
+// expressions narrowed once to the math type; the bias corrections arrive
+// already narrowed to the math type, as ATen's call narrows them.
+// ---------------------------------------------------------------------------
+struct AdamHyper {
+  double lr, beta1, beta2, weight_decay, eps;
+};
+
+template <typename opmath_t, bool ADAMW, bool AMSGRAD>
+__device__ __forceinline__ void adam_element(
+    opmath_t& param, opmath_t grad, opmath_t& exp_avg, opmath_t& exp_avg_sq,
+    opmath_t& max_exp_avg_sq, const AdamHyper& h, const bool maximize,
+    const opmath_t bias_correction1, const opmath_t bias_correction2_sqrt) {
+  if (maximize) {
+    grad = -grad;
+  }
+  if (h.weight_decay != 0) {
+    if constexpr (ADAMW) {
+      param -= h.lr * h.weight_decay * param;
+    } else {
+      grad += param * h.weight_decay;
+    }
+  }
+  exp_avg = h.beta1 * exp_avg + (1 - h.beta1) * grad;
+  exp_avg_sq = h.beta2 * exp_avg_sq + (1 - h.beta2) * grad * grad;
+  const opmath_t step_size = h.lr / bias_correction1;
+  opmath_t denom;
+  if constexpr (AMSGRAD) {
+    max_exp_avg_sq = ::max(max_exp_avg_sq, exp_avg_sq);
+    denom = (std::sqrt(max_exp_avg_sq) / bias_correction2_sqrt) + h.eps;
+  } else {
+    denom = (std::sqrt(exp_avg_sq) / bias_correction2_sqrt) + h.eps;
+  }
+  param -= step_size * exp_avg / denom;
+}
+
+// Per-replica bias corrections from the (bumped) step count: computed in double
+// with pow(double, double) from the float step, then narrowed to the math type.
+template <typename opmath_t>
+__device__ __forceinline__ void adam_bias_corrections(
+    const double beta1, const double beta2, const float step,
+    opmath_t& bias_correction1, opmath_t& bias_correction2_sqrt) {
+  const double bc1 = 1 - ::pow(beta1, static_cast<double>(step));
+  const double bc2 = 1 - ::pow(beta2, static_cast<double>(step));
+  bias_correction1 = static_cast<opmath_t>(bc1);
+  bias_correction2_sqrt = static_cast<opmath_t>(std::sqrt(bc2));
+}
+
+// ---------------------------------------------------------------------------
+// SGD. `hyper_t` is the type the hyperparameters are carried in inside the
+// element math.
+// ---------------------------------------------------------------------------
+template <typename hyper_t> struct SgdHyper {
+  hyper_t weight_decay, momentum, lr, dampening;
+};
+
+template <typename opmath_t, typename hyper_t, bool HAS_BUF, bool NESTEROV>
+__device__ __forceinline__ void sgd_element(
+    opmath_t& param, opmath_t grad, opmath_t& momentum_buffer,
+    const SgdHyper<hyper_t>& h, const bool maximize, const bool is_first_step) {
+  if (maximize) {
+    grad *= -1.0;
+  }
+  if (h.weight_decay != 0) {
+    grad += h.weight_decay * param;
+  }
+  if constexpr (HAS_BUF) {
+    const auto buf = is_first_step
+        ? grad
+        : (h.momentum * momentum_buffer + (1 - h.dampening) * grad);
+    momentum_buffer = buf;
+    if constexpr (NESTEROV) {
+      grad = grad + h.momentum * buf;
+    } else {
+      grad = buf;
+    }
+  }
+  param -= h.lr * grad;
+}
+
+// ---------------------------------------------------------------------------
+// Adagrad. corrected_lr, weight_decay and eps are doubles, so the weight-decay
+// term and the whole parameter update (including its divide) run in fp64;
+// the state-sum accumulation stays in the math type.
+// ---------------------------------------------------------------------------
+struct AdagradHyper {
+  double corrected_lr, weight_decay, eps;
+};
+
+template <typename opmath_t>
+__device__ __forceinline__ void adagrad_element(
+    opmath_t& param, opmath_t grad, opmath_t& state_sum, const AdagradHyper& h,
+    const bool maximize) {
+  if (maximize) {
+    grad = -grad;
+  }
+  if (h.weight_decay != 0) {
+    grad += param * h.weight_decay;
+  }
+  state_sum += grad * grad;
+  param = param - h.corrected_lr * grad / (std::sqrt(state_sum) + h.eps);
+}
+
+// corrected_lr = lr / (1 + (step - 1) * lr_decay), with `step - 1` in float.
+__device__ __forceinline__ double adagrad_corrected_lr(
+    const double lr, const double lr_decay, const float step) {
+  const auto denom = 1 + (step - 1) * lr_decay;
+  return lr / denom;
+}
+
+}  // namespace churten
