@@ -1,0 +1,373 @@
+"""Benchmark: fused batched optimizer step on one MI355X.
+
+Workload (the north-star configuration): Adam fp32,
+N = 128 replicas x T = 25,171,968 params (12 transformer-block tensors per
+replica), per-replica lr log-uniform in [1e-5, 1e-3], step uniform in
+[1, 10000], active mask Bernoulli(0.9), grads ~ N(0, 1e-3), synthetic seeded
+tensors resident in HBM before timing starts. One "step" is one
+``torch.ops.torchstrap.adam_step_`` call over the whole (N, T) state.
+
+Printed (one JSON line): value = effective HBM GB/s of the whole step (active
+rows x T x 28 B / step time), plus the kernel's roofline (algorithmic bytes of
+one update launch / its average duration, measured with HIP events on the
+launch stream), the reference CPU kernel timed on this host, and the N-instance
+torch.optim Python-loop baseline on the same GPU.
+
+    python bench.py [--gpus 1] [--steps K] [--warmup W] [--config 5]
+"""
+
+from __future__ import annotations
+
+import argparse
+import json
+import math
+import os
+import subprocess
+import sys
+import time
+from pathlib import Path
+
+ROOT = Path(__file__).resolve().parent
+HBM_PEAK_GBS = 8000.0  # MI355X HBM3E
+
+# Per-replica tensor layouts of BASELINE.json's configs.
+MLP_LAYOUT = [(512, 256), (512,), (256, 512), (256,), (10, 256), (10,)]
+CNN_LAYOUT = [(32, 3, 3, 3), (32,), (64, 32, 3, 3), (64,), (128, 4096), (128,),
+              (10, 128), (10,)]
+BLOCK_LAYOUT = [(4096, 1024)] * 4 + [(1024, 4096)] * 2 + [(1024,)] * 6
+
+
+def padded_width(layout) -> int:
+    raw = sum(math.prod(s) for s in layout)
+    return raw + (-raw % 4)
+
+
+CONFIGS = {
+    1: dict(op="adam", N=8, layout=MLP_LAYOUT, amsgrad=False, decoupled=False),
+    2: dict(op="adam", N=100, layout=MLP_LAYOUT, amsgrad=True, decoupled=True),
+    3: dict(op="sgd", N=32, layout=CNN_LAYOUT),
+    4: dict(op="adagrad", N=64, layout=CNN_LAYOUT),
+    5: dict(op="adam", N=128, layout=BLOCK_LAYOUT, amsgrad=False, decoupled=False),
+}
+
+
+def bytes_per_elem(cfg: int) -> int:
+    c = CONFIGS[cfg]
+    if c["op"] == "adam":
+        return 36 if c["amsgrad"] else 28
+    return 20
+
+
+def make_config(cfg: int, device="cuda", seed=None, N=None):
+    """Synthetic state of one BASELINE.json config, as the op's arguments.
+
+    Returns (op_name, args tuple, kwargs dict, algorithmic bytes of one step).
+    """
+    import torch
+
+    c = CONFIGS[cfg]
+    N = N or c["N"]
+    T = padded_width(c["layout"])
+    raw = sum(math.prod(s) for s in c["layout"])
+    dev = torch.device(device)
+    g = torch.Generator(device=dev).manual_seed(1000 + cfg if seed is None else seed)
+    f = dict(device=dev, dtype=torch.float32)
+
+    def normal(std, *shape):
+        return torch.randn(*shape, generator=g, **f).mul_(std)
+
+    def pad0(t):  # the layout's pad lanes are zero
+        if T > raw:
+            t[:, raw:] = 0
+        return t
+
+    def uniform(lo, hi, n):
+        return torch.rand(n, generator=g, **f) * (hi - lo) + lo
+
+    if cfg == 1:
+        p, gr = pad0(normal(0.02, N, T)), pad0(normal(1e-2, N, T))
+        m, v = torch.zeros(N, T, **f), torch.zeros(N, T, **f)
+        steps = torch.full((N,), 1.0, **f)
+        mask = torch.ones(N, dtype=torch.bool, device=dev)
+        hyp = [torch.full((N,), x, **f) for x in (1e-3, 0.9, 0.999, 1e-8, 0.0)]
+        args = (p, gr, m, v, None, steps, *hyp, mask)
+        kw = dict(amsgrad=False, maximize=False, decoupled_weight_decay=False)
+    elif cfg == 2:
+        p, gr = pad0(normal(0.02, N, T)), pad0(normal(1e-2, N, T))
+        m = pad0(normal(1e-3, N, T))
+        v = pad0(normal(1e-4, N, T).abs_())
+        mx = v.clone()
+        steps = torch.randint(1, 1001, (N,), generator=g, device=dev).float()
+        lr = torch.pow(10.0, uniform(-4, -2, N))
+        mask = torch.rand(N, generator=g, device=dev) < 0.75
+        hyp = [lr] + [torch.full((N,), x, **f) for x in (0.9, 0.999, 1e-8, 1e-2)]
+        args = (p, gr, m, v, mx, steps, *hyp, mask)
+        kw = dict(amsgrad=True, maximize=False, decoupled_weight_decay=True)
+    elif cfg == 3:
+        p, gr = pad0(normal(0.02, N, T)), pad0(normal(1e-2, N, T))
+        mb = pad0(normal(1e-2, N, T))
+        choices = torch.tensor([0.0, 0.5, 0.9, 0.99], **f)
+        mom = choices[torch.randint(0, 4, (N,), generator=g, device=dev)]
+        first = torch.rand(N, generator=g, device=dev) < 0.5
+        steps = torch.where(first, torch.zeros(N, **f),
+                            torch.randint(1, 100, (N,), generator=g, device=dev).float())
+        mask = torch.rand(N, generator=g, device=dev) < 0.8
+        args = (p, gr, mb, steps, torch.full((N,), 1e-2, **f), mom,
+                torch.full((N,), 0.1, **f), torch.zeros(N, **f), mask)
+        kw = dict(nesterov=True, maximize=False)
+    elif cfg == 4:
+        p, gr = pad0(normal(0.02, N, T)), pad0(normal(1e-2, N, T))
+        s = normal(1e-3, N, T).abs_().add_(0.1)
+        steps = torch.randint(1, 501, (N,), generator=g, device=dev).float()
+        mask = torch.ones(N, dtype=torch.bool, device=dev)
+        hyp = [torch.full((N,), x, **f) for x in (1e-2, 1e-4, 1e-4, 1e-10)]
+        args = (p, gr, s, steps, *hyp, mask)
+        kw = dict(maximize=False)
+    else:
+        p, gr = normal(0.02, N, T), normal(1e-3, N, T)
+        m, v = torch.zeros(N, T, **f), torch.zeros(N, T, **f)
+        steps = torch.randint(1, 10001, (N,), generator=g, device=dev).float()
+        lr = torch.pow(10.0, uniform(-5, -3, N))
+        mask = torch.rand(N, generator=g, device=dev) < 0.9
+        hyp = [lr] + [torch.full((N,), x, **f) for x in (0.9, 0.999, 1e-8, 0.0)]
+        args = (p, gr, m, v, None, steps, *hyp, mask)
+        kw = dict(amsgrad=False, maximize=False, decoupled_weight_decay=False)
+    active = int(mask.sum().item())
+    return c["op"], args, kw, active * T * bytes_per_elem(cfg)
+
+
+# ---------------------------------------------------------------------------
+# CPU baseline: the reference's CPU kernel (oracle/_ref), in a child process
+# ---------------------------------------------------------------------------
+CPU_SAMPLE_N = 8
+
+
+def cpu_worker(cfg: int, steps: int) -> None:
+    """Child process: time the reference CPU kernel on N = CPU_SAMPLE_N replicas."""
+    import torch
+
+    threads = min(16, len(os.sched_getaffinity(0)))
+    torch.set_num_threads(threads)
+    ref = ROOT / "oracle" / "_ref" / "torchstrap_ref_C.so"
+    kind = "reference"
+    if ref.exists():
+        torch.ops.load_library(str(ref))
+        op_name, args, kw, nbytes = make_config(cfg, device="cpu", N=CPU_SAMPLE_N)
+        fn = getattr(torch.ops.torchstrap, f"{op_name}_step_")
+        run = lambda: fn(*args, **kw)  # noqa: E731
+    else:  # the C restatement (single-threaded port)
+        sys.path.insert(0, str(ROOT))
+        from oracle import oracle as O
+        kind, threads = "port", 1
+        op_name, args, kw, nbytes = make_config(cfg, device="cpu", N=CPU_SAMPLE_N)
+        a = [t.numpy() if t is not None else None for t in args]
+        run = lambda: O.adam_step(O.CPU, *a, **kw)  # noqa: E731
+    run()  # warm
+    t0 = time.perf_counter()
+    for _ in range(steps):
+        run()
+    dt = (time.perf_counter() - t0) / steps
+    print(json.dumps({"value": round(nbytes / dt / 1e9, 3), "unit": "GB/s",
+                      "cores": threads, "kind": kind, "us_per_step": round(dt * 1e6, 1),
+                      "sample": f"config {cfg} at N={CPU_SAMPLE_N} of {CONFIGS[cfg]['N']} "
+                                f"replicas (same T, same per-replica hyperparameters), "
+                                f"{steps} steps after 1 warm-up, effective bytes "
+                                f"{bytes_per_elem(cfg)} B x active elements"}))
+
+
+def cpu_baseline(cfg: int, steps: int):
+    cmd = [sys.executable, str(Path(__file__).resolve()), "--cpu-worker",
+           "--config", str(cfg), "--steps", str(steps)]
+    env = dict(os.environ, HIP_VISIBLE_DEVICES="", CUDA_VISIBLE_DEVICES="")
+    try:
+        out = subprocess.run(cmd, capture_output=True, text=True, timeout=600, env=env)
+        line = [ln for ln in out.stdout.splitlines() if ln.startswith("{")]
+        if out.returncode != 0 or not line:
+            sys.stderr.write(out.stderr[-2000:])
+            return None
+        return json.loads(line[-1])
+    except subprocess.TimeoutExpired:
+        return None
+
+
+# ---------------------------------------------------------------------------
+# GPU measurements
+# ---------------------------------------------------------------------------
+def kernel_only_timing(op_name, args, kw, launches: int) -> float:
+    """Average duration (ms) of the update kernel alone: the C ABI is called
+    without the step bump, bracketed by HIP events on the launch stream."""
+    import ctypes
+
+    import torch
+
+    lib = ctypes.CDLL(str(ROOT / "churten_amd" / "lib" / "libchurten_optim.so"))
+
+    class RtBuf(ctypes.Structure):
+        _fields_ = [("data", ctypes.c_void_p), ("stride_r", ctypes.c_int64),
+                    ("stride_t", ctypes.c_int64)]
+
+    def buf(t):
+        return RtBuf(t.data_ptr(), t.stride(0), t.stride(1)) if t is not None else RtBuf(0, 0, 1)
+
+    stream = torch.cuda.current_stream()
+    vp = lambda t: ctypes.c_void_p(t.data_ptr())  # noqa: E731
+    p, gr = args[0], args[1]
+    R, T = p.shape
+    if op_name == "adam":
+        bufs = (RtBuf * 5)(*[buf(t) for t in args[:5]])
+        flags = (1 if kw["amsgrad"] else 0) | (2 if kw["decoupled_weight_decay"] else 0)
+        call = lambda: lib.ts_adam_step(  # noqa: E731
+            bufs, 0, vp(args[5]), *[vp(t) for t in args[6:11]], vp(args[11]),
+            ctypes.c_int64(R), ctypes.c_int64(T), ctypes.c_uint32(flags),
+            ctypes.c_void_p(0), ctypes.c_void_p(stream.cuda_stream))
+    else:
+        raise ValueError(op_name)
+    for _ in range(3):
+        assert call() == 0
+    e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    e0.record(stream)
+    for _ in range(launches):
+        call()
+    e1.record(stream)
+    torch.cuda.synchronize()
+    return e0.elapsed_time(e1) / launches
+
+
+def loop_baseline(cfg: int, steps: int, fused: bool):
+    """N independent torch.optim.Adam instances stepped in a Python loop
+    (the reference's 'vanilla' baseline, bench_inplace_adam.py:66-96)."""
+    import torch
+
+    c = CONFIGS[cfg]
+    N = c["N"]
+    dev = torch.device("cuda")
+    g = torch.Generator(device=dev).manual_seed(7)
+    opts, params = [], []
+    for _ in range(N):
+        ps = [torch.randn(*s, device=dev, generator=g).mul_(0.02).requires_grad_()
+              for s in c["layout"]]
+        for t in ps:
+            t.grad = torch.randn(t.shape, device=dev, generator=g).mul_(1e-3)
+        params.append(ps)
+        opts.append(torch.optim.Adam(ps, lr=1e-3, fused=fused, foreach=None if fused else True))
+    for o in opts:
+        o.step()
+    torch.cuda.synchronize()
+    t0 = time.perf_counter()
+    for _ in range(steps):
+        for o in opts:
+            o.step()
+    torch.cuda.synchronize()
+    dt = (time.perf_counter() - t0) / steps
+    del opts, params
+    torch.cuda.empty_cache()
+    return dt * 1e3
+
+
+def read_traffic(kernel: str):
+    """HBM bytes per launch from the committed rocprofv3 --pmc summary, if any."""
+    f = ROOT / "profiles" / f"{kernel}_traffic.json"
+    if f.exists():
+        try:
+            return json.loads(f.read_text()).get("bytes_per_launch")
+        except (ValueError, OSError):
+            return None
+    return None
+
+
+def main():
+    ap = argparse.ArgumentParser()
+    ap.add_argument("--gpus", type=int, default=1)
+    ap.add_argument("--steps", type=int, default=20)
+    ap.add_argument("--warmup", type=int, default=5)
+    ap.add_argument("--config", type=int, default=5, choices=sorted(CONFIGS))
+    ap.add_argument("--cpu-steps", type=int, default=5)
+    ap.add_argument("--no-cpu-baseline", action="store_true")
+    ap.add_argument("--no-loop-baseline", action="store_true")
+    ap.add_argument("--cpu-worker", action="store_true", help=argparse.SUPPRESS)
+    args = ap.parse_args()
+
+    if args.cpu_worker:
+        cpu_worker(args.config, args.steps)
+        return
+    world = int(os.environ.get("WORLD_SIZE", "1"))
+    if args.gpus != 1 or world != 1:
+        print("bench.py measures one MI355X: the optimizer step is per-replica "
+              "independent and this build runs on a single GPU; use --gpus 1.",
+              file=sys.stderr)
+        sys.exit(2)
+
+    # CPU baseline first, before this process touches the GPU.
+    cpu = None if args.no_cpu_baseline else cpu_baseline(args.config, args.cpu_steps)
+
+    import torch
+
+    sys.path.insert(0, str(ROOT))
+    import churten_amd.kernels  # noqa: F401  (fails loudly if the HIP build is missing)
+
+    op_name, op_args, kw, nbytes = make_config(args.config)
+    fn = getattr(torch.ops.torchstrap, f"{op_name}_step_")
+    for _ in range(args.warmup):
+        fn(*op_args, **kw)
+    torch.cuda.synchronize()
+
+    stream = torch.cuda.current_stream()
+    e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    t0 = time.perf_counter()
+    e0.record(stream)
+    for _ in range(args.steps):
+        fn(*op_args, **kw)
+    e1.record(stream)
+    torch.cuda.synchronize()
+    wall_ms = (time.perf_counter() - t0) * 1e3 / args.steps
+    step_ms = e0.elapsed_time(e1) / args.steps
+
+    kern_ms = kernel_only_timing(op_name, op_args, kw, max(10, args.steps))
+    achieved = nbytes / (kern_ms * 1e-3) / 1e9
+    kernel = "adam_stream_kernel"
+    del op_args
+    torch.cuda.empty_cache()
+
+    loop = {}
+    if not args.no_loop_baseline and op_name == "adam":
+        loop["fused_ms"] = round(loop_baseline(args.config, 3, fused=True), 3)
+        loop["foreach_ms"] = round(loop_baseline(args.config, 3, fused=False), 3)
+
+    value = nbytes / (step_ms * 1e-3) / 1e9
+    c = CONFIGS[args.config]
+    out = {
+        "metric": "Adam step us + effective HBM GB/s (% of peak) at NxT; speedup vs Python loop",
+        "value": round(value, 1),
+        "unit": "GB/s",
+        "n_gpus": 1,
+        "steps": args.steps,
+        "warmup": args.warmup,
+        "ms_per_step": round(step_ms, 4),
+        "us_per_step": round(step_ms * 1e3, 1),
+        "wall_ms_per_step": round(wall_ms, 4),
+        "pct_of_hbm_peak": round(100 * value / HBM_PEAK_GBS, 1),
+        "higher_is_better": True,
+        "scaling": "weak",
+        "vs_baseline": None,
+        "dtype": "f32",
+        "data": "synthetic (seeded torch generators, resident in HBM)",
+        "config": {"workload": f"BASELINE.json configs[{args.config - 1}]: {c['op']} fp32, "
+                               f"N={c['N']} x T={padded_width(c['layout'])}",
+                   "N": c["N"], "T": padded_width(c["layout"]),
+                   "active_bytes_per_step": nbytes, "bytes_per_elem": bytes_per_elem(args.config),
+                   "parallelism": "single GPU"},
+        "roofline": {"bound": "hbm", "kernel": kernel, "achieved": round(achieved, 1),
+                     "peak": HBM_PEAK_GBS, "unit": "GB/s",
+                     "frac": round(achieved / HBM_PEAK_GBS, 4),
+                     "kernel_avg_ms": round(kern_ms, 4),
+                     "traffic": read_traffic(f"{kernel}_cfg{args.config}")},
+        "cpu_baseline": cpu,
+        "python_loop_baseline": loop or None,
+        "speedup_vs_python_loop": ({k: round(v / step_ms, 2) for k, v in loop.items()}
+                                   if loop else None),
+    }
+    print(json.dumps(out), flush=True)
+
+
+if __name__ == "__main__":
+    main()

@@ -1,0 +1,184 @@
+"""Deterministic parity cases shared by the golden-vector scripts and the tests.
+
+A case is a small dict: the operator, (R, T), its flags, a seed, the
+hyperparameter pattern, the freeze pattern, the starting step and the number of
+steps. ``make_inputs`` expands it with numpy's PCG64 (bit-reproducible on every
+platform) into float32 state, per-replica vectors and one gradient per step;
+the golden files store only the case, a SHA-256 digest of every output array
+and, for small cases, the arrays themselves.
+"""
+
+from __future__ import annotations
+
+import hashlib
+import itertools
+
+import numpy as np
+
+F32 = np.float32
+
+
+def f32(x: float) -> float:
+    return float(np.float32(x))
+
+
+def digest(a: np.ndarray) -> str:
+    return hashlib.sha256(np.ascontiguousarray(a, dtype="<f4").tobytes()).hexdigest()
+
+
+# ---------------------------------------------------------------------------
+# case lists
+# ---------------------------------------------------------------------------
+# T values: 45 (ragged: T % 4 and T % 8 != 0), 52 (T % 4 == 0, AVX2 tail of 4),
+# 64 (no tail anywhere), 1000 (tail of 0 on 8 lanes, > one GPU tile row? no),
+# 16397 (crosses the CPU 16384-element chunk and several GPU tiles, ragged).
+_TS = (45, 52, 64, 1000)
+
+
+def adam_cases():
+    out = []
+    for T, ams, mx, dec, wd in itertools.product(_TS, (False, True), (False, True),
+                                                  (False, True), (0.0, 1e-2)):
+        out.append(dict(op="adam", R=3, T=T, amsgrad=ams, maximize=mx,
+                        decoupled=dec, wd=wd, hypers="distinct", mask="one_frozen",
+                        steps0=0, nsteps=3, seed=len(out)))
+    # step-0 freeze, late steps, big ragged row
+    out.append(dict(op="adam", R=4, T=16397, amsgrad=True, maximize=False, decoupled=True,
+                    wd=1e-2, hypers="distinct", mask="one_frozen", steps0=0, nsteps=2,
+                    seed=1001))
+    out.append(dict(op="adam", R=4, T=45, amsgrad=False, maximize=False, decoupled=False,
+                    wd=1e-2, hypers="distinct", mask="one_frozen", steps0=250, nsteps=2,
+                    seed=1002))
+    return out
+
+
+def sgd_cases():
+    out = []
+    for T, mom, damp, wd, nest, mx in itertools.product(_TS, (0.0, 0.9), (0.0, 0.3),
+                                                        (0.0, 1e-2), (False, True),
+                                                        (False, True)):
+        if nest and (mom == 0.0 or damp != 0.0):
+            continue
+        out.append(dict(op="sgd", R=3, T=T, momentum=mom, dampening=damp, wd=wd,
+                        nesterov=nest, maximize=mx, hypers="uniform", mask="one_frozen",
+                        steps0=0, nsteps=3, seed=2000 + len(out)))
+    # per-replica momentum incl. a momentum-0 replica inside a buffered call
+    out.append(dict(op="sgd", R=4, T=1000, momentum="mixed", dampening=0.1, wd=1e-2,
+                    nesterov=False, maximize=False, hypers="distinct", mask="one_frozen",
+                    steps0=0, nsteps=3, seed=2901))
+    out.append(dict(op="sgd", R=4, T=16397, momentum="mixed", dampening=0.0, wd=0.0,
+                    nesterov=True, maximize=False, hypers="distinct", mask="one_frozen",
+                    steps0=0, nsteps=2, seed=2902))
+    return out
+
+
+def adagrad_cases():
+    out = []
+    for T, lrd, wd, eps, mx in itertools.product(_TS, (0.0, 1e-2), (0.0, 1e-2),
+                                                 (1e-10, 1e-6), (False, True)):
+        out.append(dict(op="adagrad", R=3, T=T, lr_decay=lrd, wd=wd, eps=eps,
+                        maximize=mx, hypers="distinct", mask="one_frozen", steps0=0,
+                        nsteps=3, seed=3000 + len(out)))
+    out.append(dict(op="adagrad", R=4, T=16397, lr_decay=1e-4, wd=1e-4, eps=1e-10,
+                    maximize=False, hypers="distinct", mask="one_frozen", steps0=120,
+                    nsteps=2, seed=3901))
+    return out
+
+
+def all_cases():
+    return adam_cases() + sgd_cases() + adagrad_cases()
+
+
+def case_id(c) -> str:
+    keys = [k for k in c if k not in ("op",)]
+    return c["op"] + "-" + "-".join(f"{k}={c[k]}" for k in keys)
+
+
+# ---------------------------------------------------------------------------
+# inputs
+# ---------------------------------------------------------------------------
+def _mask(c, R):
+    m = np.ones(R, dtype=bool)
+    if c["mask"] == "one_frozen" and R > 1:
+        m[1] = False
+    return m
+
+
+def make_inputs(c):
+    """All inputs of a case as float32 numpy arrays (state is (R, T))."""
+    rng = np.random.Generator(np.random.PCG64(c["seed"]))
+    R, T = c["R"], c["T"]
+
+    def n(*shape, scale=1.0):
+        return (rng.standard_normal(shape) * scale).astype(F32)
+
+    x = {"mask": _mask(c, R), "steps": np.full(R, c["steps0"], dtype=F32)}
+    x["p"] = n(R, T)
+    if c["op"] == "adam":
+        x["m"] = np.abs(n(R, T))
+        x["v"] = np.abs(n(R, T))
+        x["mx"] = np.abs(n(R, T)) if c["amsgrad"] else None
+        if c["hypers"] == "distinct":
+            x["lr"] = np.linspace(1e-3, 5e-2, R, dtype=F32)
+            x["beta1"] = np.linspace(0.80, 0.95, R, dtype=F32)
+            x["beta2"] = np.linspace(0.990, 0.9999, R, dtype=F32)
+            x["eps"] = np.linspace(1e-9, 1e-7, R, dtype=F32)
+        else:
+            x["lr"] = np.full(R, 1e-2, F32)
+            x["beta1"] = np.full(R, 0.9, F32)
+            x["beta2"] = np.full(R, 0.999, F32)
+            x["eps"] = np.full(R, 1e-8, F32)
+        x["wd"] = np.full(R, c["wd"], F32)
+    elif c["op"] == "sgd":
+        mom = c["momentum"]
+        if mom == "mixed":
+            x["momentum"] = np.array([0.0, 0.5, 0.9, 0.99][:R] + [0.9] * max(0, R - 4), F32)
+        else:
+            x["momentum"] = np.full(R, mom, F32)
+        has_buf = bool(np.any(x["momentum"] != 0))
+        x["mb"] = n(R, T) if has_buf else None
+        x["lr"] = (np.linspace(1e-3, 5e-2, R, dtype=F32) if c["hypers"] == "distinct"
+                   else np.full(R, 1e-2, F32))
+        x["dampening"] = np.full(R, c["dampening"], F32)
+        x["wd"] = np.full(R, c["wd"], F32)
+    else:
+        x["s"] = np.abs(n(R, T))
+        x["lr"] = (np.linspace(1e-3, 5e-2, R, dtype=F32) if c["hypers"] == "distinct"
+                   else np.full(R, 1e-2, F32))
+        x["lr_decay"] = np.full(R, c["lr_decay"], F32)
+        x["wd"] = np.full(R, c["wd"], F32)
+        x["eps"] = np.full(R, c["eps"], F32)
+    x["grads"] = [n(R, T) for _ in range(c["nsteps"])]
+    return x
+
+
+def state_names(c, x):
+    if c["op"] == "adam":
+        return ["p", "m", "v"] + (["mx"] if c["amsgrad"] else [])
+    if c["op"] == "sgd":
+        return ["p"] + (["mb"] if x["mb"] is not None else [])
+    return ["p", "s"]
+
+
+def run_oracle(c, form, unit_stride=True):
+    """Runs the case through the C oracle; returns {name: array} incl. steps."""
+    from oracle import oracle as O
+
+    x = make_inputs(c)
+    for g in x["grads"]:
+        if c["op"] == "adam":
+            O.adam_step(form, x["p"], g, x["m"], x["v"], x["mx"], x["steps"], x["lr"],
+                        x["beta1"], x["beta2"], x["eps"], x["wd"], x["mask"],
+                        amsgrad=c["amsgrad"], maximize=c["maximize"],
+                        decoupled_weight_decay=c["decoupled"], unit_stride=unit_stride)
+        elif c["op"] == "sgd":
+            O.sgd_step(form, x["p"], g, x["mb"], x["steps"], x["lr"], x["momentum"],
+                       x["dampening"], x["wd"], x["mask"], nesterov=c["nesterov"],
+                       maximize=c["maximize"], unit_stride=unit_stride)
+        else:
+            O.adagrad_step(form, x["p"], g, x["s"], x["steps"], x["lr"], x["lr_decay"],
+                           x["wd"], x["eps"], x["mask"], maximize=c["maximize"],
+                           unit_stride=unit_stride)
+    out = {k: x[k] for k in state_names(c, x)}
+    out["steps"] = x["steps"]
+    return out
