@@ -1,0 +1,158 @@
+"""The drop-in boundary, checked without a GPU.
+
+* The C ABI library loads and exports every entry point include/churten_optim.h
+  declares; argument validation returns hipErrorInvalidValue before any device
+  call.
+* The operator library registers the three ``torchstrap`` schemas with the
+  reference's exact text (src/torchstrap/kernels/csrc/stubs.cpp:25-72), the
+  fake kernels and the vmap rules (checked on meta tensors).
+* The product never reaches the test oracle.
+"""
+
+from __future__ import annotations
+
+import ctypes
+import re
+from pathlib import Path
+
+import pytest
+import torch
+from torch.func import vmap
+
+ROOT = Path(__file__).resolve().parents[1]
+HEADER = ROOT / "include" / "churten_optim.h"
+LIB = ROOT / "churten_amd" / "lib" / "libchurten_optim.so"
+
+REFERENCE_SCHEMAS = {
+    "adam_step_": "torchstrap::adam_step_(Tensor(a!) params, Tensor grads, Tensor(b!) exp_avgs, "
+                  "Tensor(c!) exp_avg_sqs, Tensor(d!)? max_exp_avg_sqs, Tensor(e!) state_steps, "
+                  "Tensor lr, Tensor beta1, Tensor beta2, Tensor eps, Tensor weight_decay, "
+                  "Tensor active_mask, bool amsgrad, bool maximize, "
+                  "bool decoupled_weight_decay) -> Tensor",
+    "sgd_step_": "torchstrap::sgd_step_(Tensor(a!) params, Tensor grads, Tensor(b!)? "
+                 "momentum_buffers, Tensor(c!) state_steps, Tensor lr, Tensor momentum, "
+                 "Tensor dampening, Tensor weight_decay, Tensor active_mask, bool nesterov, "
+                 "bool maximize) -> Tensor",
+    "adagrad_step_": "torchstrap::adagrad_step_(Tensor(a!) params, Tensor grads, Tensor(b!) "
+                     "state_sums, Tensor(c!) state_steps, Tensor lr, Tensor lr_decay, "
+                     "Tensor weight_decay, Tensor eps, Tensor active_mask, "
+                     "bool maximize) -> Tensor",
+}
+
+
+def declared_symbols():
+    text = HEADER.read_text()
+    return sorted(set(re.findall(r"^\s*int\s+(ts_\w+)\s*\(", text, flags=re.M)))
+
+
+def test_header_declares_the_entry_points():
+    assert declared_symbols() == sorted(
+        ["ts_adagrad_step", "ts_adam_step", "ts_bump_steps", "ts_sgd_step", "ts_version"])
+
+
+def test_library_exports_every_declared_symbol():
+    lib = ctypes.CDLL(str(LIB))
+    for name in declared_symbols():
+        assert hasattr(lib, name), name
+    assert lib.ts_version() == 100
+
+
+def test_invalid_arguments_rejected_before_any_launch():
+    lib = ctypes.CDLL(str(LIB))
+    null = ctypes.c_void_p(0)
+    i64 = ctypes.c_int64
+    # no operand table
+    assert lib.ts_adam_step(null, 0, null, null, null, null, null, null, null, i64(1),
+                            i64(4), ctypes.c_uint32(0), null, null) == 1
+    assert lib.ts_sgd_step(null, 0, null, null, null, null, null, null, i64(1), i64(4),
+                           ctypes.c_uint32(0), null, null) == 1
+    assert lib.ts_adagrad_step(null, 0, null, null, null, null, null, null, i64(1), i64(4),
+                               ctypes.c_uint32(0), null, null) == 1
+    # unknown dtype, negative R
+    assert lib.ts_bump_steps(7, null, null, i64(0), null, null) == 1
+    assert lib.ts_bump_steps(0, null, null, i64(-1), null, null) == 1
+
+
+def test_schemas_match_the_reference_text():
+    import churten_amd.kernels  # noqa: F401
+
+    for name, want in REFERENCE_SCHEMAS.items():
+        got = str(getattr(torch.ops.torchstrap, name).default._schema)
+        assert got == want, name
+
+
+def _meta_adam(R=3, T=8):
+    f = dict(device="meta")
+    return ([torch.empty(R, T, **f) for _ in range(4)] + [None, torch.empty(R, **f)]
+            + [torch.empty(R, **f) for _ in range(5)] + [torch.empty(R, dtype=torch.bool, **f)])
+
+
+def test_fake_kernels_on_meta_tensors():
+    import churten_amd.kernels as K
+
+    out = K.adam_step_(*_meta_adam(), amsgrad=False, maximize=False,
+                       decoupled_weight_decay=True)
+    assert out.shape == () and out.device.type == "meta" and out.dtype == torch.float32
+    m = lambda *s: torch.empty(*s, device="meta")  # noqa: E731
+    mask = torch.empty(3, dtype=torch.bool, device="meta")
+    out = K.sgd_step_(m(3, 8), m(3, 8), None, m(3), m(3), m(3), m(3), m(3), mask,
+                      nesterov=False, maximize=False)
+    assert out.shape == ()
+    out = K.adagrad_step_(m(3, 8), m(3, 8), m(3, 8), m(3), m(3), m(3), m(3), m(3), mask,
+                          maximize=False)
+    assert out.shape == ()
+
+
+def test_vmap_rule_squeezes_replica_dim_on_meta():
+    import churten_amd.kernels as K
+
+    B, T = 4, 10
+    args = _meta_adam(B, T)
+    args[4] = torch.empty(B, T, device="meta")
+
+    def one(p, g, m, v, mx, s, lr, b1, b2, eps, wd, mask):
+        return K.adam_step_(p.unsqueeze(0), g.unsqueeze(0), m.unsqueeze(0), v.unsqueeze(0),
+                            mx.unsqueeze(0), s.view(1), lr.view(1), b1.view(1), b2.view(1),
+                            eps.view(1), wd.view(1), mask.view(1), amsgrad=True,
+                            maximize=False, decoupled_weight_decay=True)
+
+    out = vmap(one)(*args)
+    assert out.shape == ()  # the rule returns an unbatched scalar
+
+
+def test_consolidated_helpers():
+    from churten_amd.kernels._consolidated import hyp, hyp_mask, lead_squeeze
+
+    t = torch.zeros(5, 3, 1, 7)  # batch dim at 2
+    out = lead_squeeze(torch.zeros(7, 1, 5), 2)
+    assert out.shape == (5, 7, 1)
+    out = lead_squeeze(t.movedim(2, 0), 0)
+    assert out.shape == (1, 5, 3, 7)
+    assert lead_squeeze(torch.zeros(4, 1, 9), 0).shape == (4, 9)
+    assert lead_squeeze(torch.zeros(9, 4), 1).shape == (4, 9)
+    assert not lead_squeeze(torch.zeros(9, 4), 1).is_contiguous()
+    assert hyp(torch.tensor(2.0), None, 3).tolist() == [2.0, 2.0, 2.0]
+    assert hyp(torch.tensor([1.0, 2.0]), None, 2).tolist() == [1.0, 2.0]
+    assert hyp_mask(torch.tensor([1.0, 0.0]), 0, 2).dtype == torch.bool
+    assert lead_squeeze(t, None) is t
+
+
+def test_cpu_tensors_have_no_fallback():
+    """GPU tensors go to the HIP kernels; no other device is served silently."""
+    import churten_amd.kernels as K
+
+    R, T = 2, 4
+    args = [torch.zeros(R, T) for _ in range(4)] + [None, torch.zeros(R)] + \
+        [torch.zeros(R) for _ in range(5)] + [torch.ones(R, dtype=torch.bool)]
+    if torch._C._dispatch_has_kernel_for_dispatch_key("torchstrap::adam_step_", "CPU"):
+        pytest.skip("a CPU kernel is registered")
+    with pytest.raises(NotImplementedError):
+        K.adam_step_(*args, amsgrad=False, maximize=False, decoupled_weight_decay=True)
+
+
+def test_product_never_imports_the_oracle():
+    for f in (ROOT / "churten_amd").rglob("*"):
+        if f.suffix in (".py", ".cpp", ".hip", ".h"):
+            text = f.read_text()
+            assert "import oracle" not in text and "from oracle" not in text, f
+            assert "liboracle" not in text and "optim_oracle" not in text, f

@@ -1,0 +1,84 @@
+"""BASELINE.json's five configurations at their real sizes.
+
+Configs 1-4 (up to 64 x 545,100) are checked whole: every element of every
+row, after one step, bit-identical to the oracle's device formulation (frozen
+rows included: they must come back unchanged). Config 5 (128 x 25,171,968,
+52 GB of state) is checked through size-independent properties: frozen rows
+unchanged bit for bit, the step counters, and windows of active rows -- at the
+start, the middle and the very end of the buffers, where element offsets pass
+2^31 -- bit-identical to the oracle run on the same window.
+"""
+
+from __future__ import annotations
+
+import numpy as np
+import pytest
+import torch
+
+import bench
+import churten_amd.kernels  # noqa: F401
+from oracle import oracle as O
+
+pytestmark = pytest.mark.gpu
+
+
+def _np(t):
+    return None if t is None else t.detach().cpu().numpy().copy()
+
+
+def _oracle_call(op, host, kw):
+    if op == "adam":
+        O.adam_step(O.DEVICE, *host, **kw)
+    elif op == "sgd":
+        O.sgd_step(O.DEVICE, *host, **kw)
+    else:
+        O.adagrad_step(O.DEVICE, *host, **kw)
+
+
+@pytest.mark.parametrize("cfg", [1, 2, 3, 4])
+def test_config_one_step_bit_exact(cfg):
+    op, args, kw, _ = bench.make_config(cfg)
+    host = [_np(t) for t in args]
+    getattr(torch.ops.torchstrap, f"{op}_step_")(*args, **kw)
+    torch.cuda.synchronize()
+    _oracle_call(op, host, kw)
+    for i, (t, h) in enumerate(zip(args, host)):
+        if t is None or i == 1:
+            continue
+        got = _np(t)
+        if got.dtype == np.bool_:
+            continue
+        assert np.array_equal(got.view(np.uint32), h.view(np.uint32)), f"config {cfg} arg {i}"
+
+
+def test_config5_properties():
+    op, args, kw, nbytes = bench.make_config(5)
+    p, gr, m, v, _, steps = args[:6]
+    mask = args[11]
+    R, T = p.shape
+    assert (R, T) == (128, 25171968) and R * T > 2**31
+    frozen = (~mask).nonzero().flatten()
+    active = mask.nonzero().flatten().tolist()
+    assert len(frozen) > 0 and len(active) > 0
+    keep = [t[frozen].clone() for t in (p, m, v)]
+    windows = [(active[0], 0), (active[len(active) // 2], T // 2 - 2048),
+               (active[-1], T - 4096)]
+    hyp = [_np(t) for t in args[6:11]]
+    before = []
+    for r, t0 in windows:
+        before.append([_np(t[r : r + 1, t0 : t0 + 4096]) for t in (p, gr, m, v)]
+                      + [_np(steps[r : r + 1])] + [h[r : r + 1].copy() for h in hyp])
+    steps0 = _np(steps)
+    torch.ops.torchstrap.adam_step_(*args, **kw)
+    torch.cuda.synchronize()
+    for t, k in zip((p, m, v), keep):
+        assert torch.equal(t[frozen], k)
+    want_steps = steps0 + _np(mask).astype(np.float32)
+    assert np.array_equal(_np(steps), want_steps)
+    for (r, t0), b in zip(windows, before):
+        pw, gw, mw, vw, sw, *hw = b
+        O.adam_step(O.DEVICE, pw, gw, mw, vw, None, sw, *hw, np.ones(1, bool), **kw)
+        for name, t, want in (("p", p, pw), ("m", m, mw), ("v", v, vw)):
+            got = _np(t[r : r + 1, t0 : t0 + 4096])
+            assert np.array_equal(got.view(np.uint32), want.view(np.uint32)), (
+                f"row {r} window {t0}: {name}")

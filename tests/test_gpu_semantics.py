@@ -1,0 +1,442 @@
+"""Operator semantics on the GPU: freeze/thaw, vmap, layouts, edge cases,
+errors, dtypes and torch.library registration.
+
+Mirrors the reference's tiers 3-5 (test/optimizer/test_inplace_*_masking.py,
+test_inplace_*_vmap.py, test_cpu_cuda_*_parity.py's opcheck) on the MI355X.
+"""
+
+from __future__ import annotations
+
+import numpy as np
+import pytest
+import torch
+from torch.func import vmap
+
+import churten_amd.kernels as K
+from oracle import oracle as O
+
+pytestmark = pytest.mark.gpu
+
+DEV = torch.device("cuda")
+
+
+def full(R, x, dtype=torch.float32):
+    return torch.full((R,), x, device=DEV, dtype=dtype)
+
+
+def adam_args(R, T, amsgrad=False, seed=0, steps=2.0, dtype=torch.float32):
+    g = torch.Generator(device=DEV).manual_seed(seed)
+    rnd = lambda: torch.randn(R, T, device=DEV, generator=g).to(dtype)  # noqa: E731
+    st = [rnd(), rnd(), rnd().abs(), rnd().abs(), rnd().abs() if amsgrad else None]
+    return st + [full(R, steps, dtype), full(R, 1e-2, dtype), full(R, 0.9, dtype),
+                 full(R, 0.999, dtype), full(R, 1e-8, dtype), full(R, 1e-2, dtype)]
+
+
+# ---------------------------------------------------------------------------
+# freeze semantics (reference test_inplace_adam_masking.py:50-111)
+# ---------------------------------------------------------------------------
+@pytest.mark.parametrize("inactive", [[], [2], [0, 3], [0, 1, 2, 3, 4]])
+@pytest.mark.parametrize("amsgrad", [False, True])
+def test_adam_frozen_rows_bit_identical(inactive, amsgrad):
+    R, T = 5, 4 * 6 + 6 + 3 + 3
+    a = adam_args(R, T, amsgrad, seed=7)
+    mask = torch.ones(R, dtype=torch.bool, device=DEV)
+    mask[inactive] = False
+    before = [t.clone() if t is not None else None for t in a]
+    K.adam_step_(*a, mask, amsgrad=amsgrad, maximize=False, decoupled_weight_decay=True)
+    torch.cuda.synchronize()
+    act = mask.nonzero().flatten()
+    frz = (~mask).nonzero().flatten()
+    for i in (0, 2, 3, 4, 5):
+        if a[i] is None:
+            continue
+        assert torch.equal(a[i][frz], before[i][frz]), f"arg {i} frozen rows changed"
+        if len(act) and i != 4:
+            assert not torch.equal(a[i][act], before[i][act]), f"arg {i} active rows unchanged"
+
+
+def test_adam_step0_freeze_never_reads_state():
+    """A replica frozen at step 0 would give 1 - beta^0 = 0 and NaN if computed;
+    its rows (even NaN-filled ones) must stay untouched and NaN-free elsewhere."""
+    R, T = 3, 64
+    a = adam_args(R, T, steps=0.0)
+    a[0][1] = float("nan")
+    mask = torch.tensor([True, False, True], device=DEV)
+    K.adam_step_(*a, mask, amsgrad=False, maximize=False, decoupled_weight_decay=False)
+    torch.cuda.synchronize()
+    assert torch.isnan(a[0][1]).all()
+    assert torch.isfinite(a[0][[0, 2]]).all()
+    assert a[5].tolist() == [1.0, 0.0, 1.0]
+
+
+def test_sgd_frozen_at_step0_then_thawed_gets_buf_equal_grad():
+    """Reference test_inplace_sgd_masking.py:102-140: a replica frozen before its
+    first step keeps a pristine buffer; on thaw its first step has buf == grad."""
+    R, T = 3, 52
+    g = torch.Generator(device=DEV).manual_seed(3)
+    p = torch.randn(R, T, device=DEV, generator=g)
+    mb = torch.randn(R, T, device=DEV, generator=g)
+    steps = torch.zeros(R, device=DEV)
+    hyp = (full(R, 1e-2), full(R, 0.9), full(R, 0.0), full(R, 0.0))
+    mask = torch.tensor([True, False, True], device=DEV)
+    mb_before = mb.clone()
+    for _ in range(2):
+        grad = torch.randn(R, T, device=DEV, generator=g)
+        K.sgd_step_(p, grad, mb, steps, *hyp, mask, nesterov=False, maximize=False)
+    assert torch.equal(mb[1], mb_before[1])
+    assert steps.tolist() == [2.0, 0.0, 2.0]
+    grad = torch.randn(R, T, device=DEV, generator=g)
+    K.sgd_step_(p, grad, mb, steps, *hyp, torch.ones(R, dtype=torch.bool, device=DEV),
+                nesterov=False, maximize=False)
+    torch.cuda.synchronize()
+    assert torch.equal(mb[1], grad[1])
+    assert steps.tolist() == [3.0, 1.0, 3.0]
+
+
+def test_sgd_momentum0_replica_is_plain_sgd():
+    """A momentum-0 replica inside a buffered call: buf = grad, p -= lr * grad."""
+    R, T = 2, 1000
+    g = torch.Generator(device=DEV).manual_seed(4)
+    p = torch.randn(R, T, device=DEV, generator=g)
+    mb = torch.randn(R, T, device=DEV, generator=g)
+    steps = torch.full((R,), 5.0, device=DEV)
+    grad = torch.randn(R, T, device=DEV, generator=g)
+    p0 = p.clone()
+    K.sgd_step_(p, grad, mb, steps, full(R, 0.25), torch.tensor([0.0, 0.9], device=DEV),
+                full(R, 0.0), full(R, 0.0), torch.ones(R, dtype=torch.bool, device=DEV),
+                nesterov=False, maximize=False)
+    torch.cuda.synchronize()
+    assert torch.equal(mb[0], grad[0])
+    assert torch.equal(p[0], p0[0] - 0.25 * grad[0])  # lr a power of 2: exact
+
+
+@pytest.mark.parametrize("lr_decay", [0.0, 0.5])
+def test_adagrad_thawed_step_matches_never_frozen(lr_decay):
+    """Reference test_inplace_adagrad_masking.py:91-131: a frozen replica's clock
+    does not advance (no lr decay while frozen), so its first step after thawing
+    is bit-equal to the first step of a replica that was never frozen."""
+    T = 45
+    g = torch.Generator(device=DEV).manual_seed(6)
+    p_init = torch.randn(T, device=DEV, generator=g)
+    s_init = torch.rand(T, device=DEV, generator=g)
+    grad = torch.randn(T, device=DEV, generator=g)
+    hyp = lambda R: (full(R, 1e-2), full(R, lr_decay), full(R, 1e-2), full(R, 1e-10))  # noqa
+    # never frozen: one replica, one step
+    pa, sa, stepa = p_init.view(1, T).clone(), s_init.view(1, T).clone(), torch.zeros(1, device=DEV)
+    K.adagrad_step_(pa, grad.view(1, T), sa, stepa, *hyp(1),
+                    torch.ones(1, dtype=torch.bool, device=DEV), maximize=False)
+    # replica 1 frozen for three calls while replica 0 trains, then thawed
+    pb = torch.stack([torch.randn(T, device=DEV, generator=g), p_init])
+    sb = torch.stack([torch.rand(T, device=DEV, generator=g), s_init])
+    stepb = torch.zeros(2, device=DEV)
+    for _ in range(3):
+        K.adagrad_step_(pb, torch.randn(2, T, device=DEV, generator=g), sb, stepb, *hyp(2),
+                        torch.tensor([True, False], device=DEV), maximize=False)
+    assert torch.equal(pb[1], p_init) and stepb.tolist() == [3.0, 0.0]
+    K.adagrad_step_(pb, torch.stack([grad, grad]), sb, stepb, *hyp(2),
+                    torch.ones(2, dtype=torch.bool, device=DEV), maximize=False)
+    torch.cuda.synchronize()
+    assert stepb.tolist() == [4.0, 1.0]
+    assert torch.equal(pb[1], pa[0]) and torch.equal(sb[1], sa[0])
+
+
+# ---------------------------------------------------------------------------
+# vmap (reference test_inplace_adam_vmap.py)
+# ---------------------------------------------------------------------------
+@pytest.mark.parametrize("amsgrad", [False, True])
+def test_adam_outer_vmap_matches_direct_call(amsgrad):
+    B, T = 3, 33
+    g = torch.Generator(device=DEV).manual_seed(8)
+    mk = lambda: torch.randn(B, T, device=DEV, generator=g)  # noqa: E731
+    base = [mk(), mk(), mk().abs(), mk().abs(), mk().abs(), torch.zeros(B, device=DEV)]
+    lr = torch.linspace(5e-3, 5e-2, B, device=DEV)
+    hyp = [lr, full(B, 0.9), full(B, 0.999), full(B, 1e-8), full(B, 1e-2)]
+    mask = torch.ones(B, dtype=torch.bool, device=DEV)
+    v_state = [t.clone() for t in base]
+    d_state = [t.clone() for t in base]
+
+    def one(p, gr, m, v, mx, s, lr, b1, b2, eps, wd, msk):
+        return K.adam_step_(p.unsqueeze(0), gr.unsqueeze(0), m.unsqueeze(0), v.unsqueeze(0),
+                            mx.unsqueeze(0) if amsgrad else None, s.view(1), lr.view(1),
+                            b1.view(1), b2.view(1), eps.view(1), wd.view(1),
+                            msk.view(1).to(torch.bool), amsgrad=amsgrad, maximize=False,
+                            decoupled_weight_decay=True)
+
+    vmap(one, in_dims=(0,) * 12)(*v_state, *hyp, mask)
+    K.adam_step_(*d_state[:4], d_state[4] if amsgrad else None, d_state[5], *hyp, mask,
+                 amsgrad=amsgrad, maximize=False, decoupled_weight_decay=True)
+    torch.cuda.synchronize()
+    for a, b in zip(v_state, d_state):
+        assert torch.equal(a, b)
+
+
+def test_sgd_vmap_batch_dim_1_is_strided():
+    """in_dims=1 makes the rule's movedim produce a strided (B, T) view."""
+    B, T = 4, 20
+    g = torch.Generator(device=DEV).manual_seed(9)
+    p_tb = torch.randn(T, B, device=DEV, generator=g)
+    mb_tb = torch.randn(T, B, device=DEV, generator=g)
+    gr_tb = torch.randn(T, B, device=DEV, generator=g)
+    steps = torch.full((B,), 3.0, device=DEV)
+    p_d, mb_d = p_tb.t().contiguous(), mb_tb.t().contiguous()
+    steps_d = steps.clone()
+    hyp = (torch.linspace(1e-3, 1e-2, B, device=DEV), full(B, 0.9), full(B, 0.1),
+           full(B, 1e-2))
+    mask = torch.ones(B, dtype=torch.bool, device=DEV)
+
+    def one(p, gr, mb, s, lr, mom, damp, wd, msk):
+        return K.sgd_step_(p.unsqueeze(0), gr.unsqueeze(0), mb.unsqueeze(0), s.view(1),
+                           lr.view(1), mom.view(1), damp.view(1), wd.view(1),
+                           msk.view(1), nesterov=False, maximize=False)
+
+    vmap(one, in_dims=(1, 1, 1, 0, 0, 0, 0, 0, 0))(p_tb, gr_tb, mb_tb, steps, *hyp, mask)
+    K.sgd_step_(p_d, gr_tb.t().contiguous(), mb_d, steps_d, *hyp, mask, nesterov=False,
+                maximize=False)
+    torch.cuda.synchronize()
+    assert torch.equal(p_tb.t(), p_d) and torch.equal(mb_tb.t(), mb_d)
+    assert torch.equal(steps, steps_d)
+
+
+def test_adagrad_vmap_unbatched_scalar_hypers_broadcast():
+    B, T = 3, 16
+    g = torch.Generator(device=DEV).manual_seed(10)
+    p, s = torch.randn(B, T, device=DEV, generator=g), torch.rand(B, T, device=DEV, generator=g)
+    gr = torch.randn(B, T, device=DEV, generator=g)
+    steps = torch.zeros(B, device=DEV)
+    p2, s2, steps2 = p.clone(), s.clone(), steps.clone()
+    lr = torch.tensor(1e-2, device=DEV)
+
+    def one(p, gr, s, st):
+        return K.adagrad_step_(p.unsqueeze(0), gr.unsqueeze(0), s.unsqueeze(0), st.view(1),
+                               lr, lr * 0, lr * 0, lr * 0 + 1e-10,
+                               torch.ones((), dtype=torch.bool, device=DEV), maximize=False)
+
+    vmap(one)(p, gr, s, steps)
+    K.adagrad_step_(p2, gr, s2, steps2, full(B, 1e-2), full(B, 0.0), full(B, 0.0),
+                    full(B, 1e-10), torch.ones(B, dtype=torch.bool, device=DEV),
+                    maximize=False)
+    torch.cuda.synchronize()
+    assert torch.equal(p, p2) and torch.equal(s, s2) and torch.equal(steps, steps2)
+
+
+# ---------------------------------------------------------------------------
+# edge cases and layouts
+# ---------------------------------------------------------------------------
+def test_return_is_fresh_zero_scalar():
+    a = adam_args(2, 8)
+    out = K.adam_step_(*a, torch.ones(2, dtype=torch.bool, device=DEV), amsgrad=False,
+                       maximize=False, decoupled_weight_decay=True)
+    assert out.shape == () and out.dtype == torch.float32 and out.device.type == "cuda"
+    assert out.item() == 0.0
+    assert all(out.data_ptr() != t.data_ptr() for t in a if t is not None)
+
+
+@pytest.mark.parametrize("R,T", [(0, 16), (3, 0), (0, 0)])
+def test_empty_state_still_bumps_steps(R, T):
+    a = adam_args(R, T)
+    mask = torch.ones(R, dtype=torch.bool, device=DEV)
+    out = K.adam_step_(*a, mask, amsgrad=False, maximize=False, decoupled_weight_decay=True)
+    torch.cuda.synchronize()
+    assert out.item() == 0.0
+    assert a[5].tolist() == [3.0] * R
+    s = torch.zeros(R, device=DEV)
+    K.sgd_step_(torch.zeros(R, T, device=DEV), torch.zeros(R, T, device=DEV), None, s,
+                full(R, 1.0), full(R, 0.0), full(R, 0.0), full(R, 0.0), mask, nesterov=False,
+                maximize=False)
+    K.adagrad_step_(torch.zeros(R, T, device=DEV), torch.zeros(R, T, device=DEV),
+                    torch.zeros(R, T, device=DEV), s, full(R, 1.0), full(R, 0.0),
+                    full(R, 0.0), full(R, 1e-10), mask, maximize=False)
+    assert s.tolist() == [2.0] * R
+
+
+@pytest.mark.parametrize("T", [1, 2, 3, 5, 1023, 1024, 1025, 4097])
+def test_odd_widths_bit_exact_to_oracle(T):
+    R = 3
+    g = torch.Generator(device=DEV).manual_seed(T)
+    a = adam_args(R, T, amsgrad=True, seed=T)
+    mask = torch.tensor([True, False, True], device=DEV)
+    host = [t.cpu().numpy().copy() if t is not None else None for t in a]
+    grad = a[1]
+    K.adam_step_(*a, mask, amsgrad=True, maximize=False, decoupled_weight_decay=True)
+    torch.cuda.synchronize()
+    O.adam_step(O.DEVICE, host[0], host[1], host[2], host[3], host[4], host[5], host[6],
+                host[7], host[8], host[9], host[10], mask.cpu().numpy(), amsgrad=True,
+                decoupled_weight_decay=True)
+    for i in (0, 2, 3, 4, 5):
+        assert np.array_equal(a[i].cpu().numpy().view(np.uint32), host[i].view(np.uint32)), i
+    del g, grad
+
+
+def test_misaligned_row_views_take_element_path_bit_exact():
+    """Rows of a column-slice view are not 16-byte aligned: same bits as contiguous."""
+    R, T = 4, 64
+    big = adam_args(R, T + 1, seed=12)
+    view = [t[:, 1:] if t is not None and t.dim() == 2 else t for t in big]
+    dense = [t.clone().contiguous() if t is not None else None for t in view]
+    dense[5:] = [t.clone() for t in view[5:]]
+    mask = torch.ones(R, dtype=torch.bool, device=DEV)
+    K.adam_step_(*view, mask, amsgrad=False, maximize=True, decoupled_weight_decay=False)
+    K.adam_step_(*dense, mask, amsgrad=False, maximize=True, decoupled_weight_decay=False)
+    torch.cuda.synchronize()
+    for a, b in zip(view[:4], dense[:4]):
+        assert torch.equal(a, b)
+
+
+def test_noncontiguous_and_foreign_dtype_side_inputs():
+    """(R,) inputs may be strided or float64 and steps float64, mask float:
+    normalised like the reference (to the param dtype / bool)."""
+    R, T = 3, 40
+    a = adam_args(R, T, seed=13)
+    b = [t.clone() if t is not None else None for t in a]
+    wide = torch.stack([a[6], a[6]], 1)[:, 0]  # strided lr view
+    assert not wide.is_contiguous()
+    b_steps = b[5].double()
+    K.adam_step_(*a[:6], wide, *a[7:], torch.tensor([1.0, 0.0, 1.0], device=DEV),
+                 amsgrad=False, maximize=False, decoupled_weight_decay=True)
+    K.adam_step_(*b[:5], b_steps, *(t.double() for t in b[6:]),
+                 torch.tensor([True, False, True], device=DEV), amsgrad=False,
+                 maximize=False, decoupled_weight_decay=True)
+    torch.cuda.synchronize()
+    for i in (0, 2, 3):
+        assert torch.equal(a[i], b[i])
+    assert a[5].tolist() == b_steps.tolist() == [3.0, 2.0, 3.0]
+
+
+# ---------------------------------------------------------------------------
+# errors (reference: RuntimeError from TORCH_CHECK)
+# ---------------------------------------------------------------------------
+def test_errors_are_runtime_errors():
+    R, T = 2, 8
+    a = adam_args(R, T)
+    mask = torch.ones(R, dtype=torch.bool, device=DEV)
+    kw = dict(amsgrad=False, maximize=False, decoupled_weight_decay=True)
+    with pytest.raises(RuntimeError, match="2-D"):
+        K.adam_step_(a[0][0], *a[1:], mask, **kw)
+    with pytest.raises(RuntimeError, match="amsgrad=True requires max_exp_avg_sqs"):
+        K.adam_step_(*a, mask, amsgrad=True, maximize=False, decoupled_weight_decay=True)
+    with pytest.raises(RuntimeError, match="grads"):
+        K.adam_step_(a[0], a[1][:, :4], *a[2:], mask, **kw)
+    with pytest.raises(RuntimeError, match="lr"):
+        K.adam_step_(*a[:6], full(R + 1, 1e-3), *a[7:], mask, **kw)
+    with pytest.raises(RuntimeError, match="lr"):
+        K.adam_step_(*a[:6], torch.full((R,), 1e-3), *a[7:], mask, **kw)
+    with pytest.raises(RuntimeError, match="nesterov=True requires momentum_buffers"):
+        K.sgd_step_(a[0], a[1], None, a[5], *a[6:10], mask, nesterov=True, maximize=False)
+    with pytest.raises(RuntimeError, match="65535"):
+        big = torch.zeros(65536, 1, device=DEV)
+        r = torch.zeros(65536, device=DEV)
+        K.sgd_step_(big, big, None, r, r, r, r, r, r.bool(), nesterov=False, maximize=False)
+    with pytest.raises(RuntimeError, match="dtype"):
+        K.adam_step_(a[0], a[1].double(), *a[2:], mask, **kw)
+
+
+# ---------------------------------------------------------------------------
+# registration
+# ---------------------------------------------------------------------------
+def test_opcheck_all_ops():
+    R, T = 3, 8
+    mask = torch.tensor([True, False, True], device=DEV)
+    U = lambda x: full(R, x)  # noqa: E731
+    rn = lambda: torch.randn(R, T, device=DEV)  # noqa: E731
+    torch.library.opcheck(
+        torch.ops.torchstrap.adam_step_.default,
+        (rn(), rn(), rn().abs(), rn().abs(), None, torch.zeros(R, device=DEV), U(1e-2),
+         U(0.9), U(0.999), U(1e-8), U(1e-2), mask),
+        dict(amsgrad=False, maximize=False, decoupled_weight_decay=True))
+    torch.library.opcheck(
+        torch.ops.torchstrap.sgd_step_.default,
+        (rn(), rn(), rn(), torch.zeros(R, device=DEV), U(1e-2), U(0.9), U(0.0), U(0.0), mask),
+        dict(nesterov=True, maximize=False))
+    torch.library.opcheck(
+        torch.ops.torchstrap.sgd_step_.default,
+        (rn(), rn(), None, torch.zeros(R, device=DEV), U(1e-2), U(0.0), U(0.0), U(0.0), mask),
+        dict(nesterov=False, maximize=False))
+    torch.library.opcheck(
+        torch.ops.torchstrap.adagrad_step_.default,
+        (rn(), rn(), rn().abs(), torch.zeros(R, device=DEV), U(1e-2), U(0.0), U(0.0),
+         U(1e-10), mask),
+        dict(maximize=False))
+
+
+# ---------------------------------------------------------------------------
+# other parameter dtypes (the reference dispatches fp32/fp64/fp16/bf16)
+# ---------------------------------------------------------------------------
+@pytest.mark.parametrize("amsgrad", [False, True])
+def test_adam_fp64_bit_exact_to_aten(amsgrad):
+    R, T = 2, 77
+    g = torch.Generator(device=DEV).manual_seed(14)
+    rnd = lambda: torch.randn(R, T, device=DEV, generator=g, dtype=torch.float64)  # noqa
+    p, m, v, mx = rnd(), rnd().abs(), rnd().abs(), rnd().abs()
+    ref = [[t[r].clone() for t in (p, m, v, mx)] for r in range(R)]
+    steps = torch.zeros(R, device=DEV, dtype=torch.float64)
+    lr = torch.tensor([1e-2, 3e-3], device=DEV, dtype=torch.float64)
+    h = [full(R, x, torch.float64) for x in (0.9, 0.999, 1e-8, 1e-2)]
+    mask = torch.ones(R, dtype=torch.bool, device=DEV)
+    for k in range(3):
+        grad = rnd()
+        for r in range(R):
+            torch._fused_adamw_([ref[r][0]], [grad[r].clone()], [ref[r][1]], [ref[r][2]],
+                                [ref[r][3]] if amsgrad else [],
+                                [torch.tensor(float(k + 1), device=DEV)], lr=lr[r].item(),
+                                beta1=0.9, beta2=0.999, weight_decay=1e-2, eps=1e-8,
+                                amsgrad=amsgrad, maximize=False, grad_scale=None,
+                                found_inf=None)
+        K.adam_step_(p, grad, m, v, mx if amsgrad else None, steps, lr, *h, mask,
+                     amsgrad=amsgrad, maximize=False, decoupled_weight_decay=True)
+    torch.cuda.synchronize()
+    for r in range(R):
+        for got, want in zip((p[r], m[r], v[r]), ref[r][:3]):
+            assert torch.equal(got, want)
+
+
+@pytest.mark.parametrize("dtype", [torch.float16, torch.bfloat16])
+def test_adam_16bit_bit_exact_to_aten_with_representable_hypers(dtype):
+    """Hyperparameters are carried in the param dtype (reference to_hyper); with
+    values exact in 16 bits the element math must equal torch's, bit for bit."""
+    R, T = 2, 64
+    g = torch.Generator(device=DEV).manual_seed(15)
+    rnd = lambda: torch.randn(R, T, device=DEV, generator=g).to(dtype)  # noqa: E731
+    p, m, v = rnd(), rnd().abs(), rnd().abs()
+    ref = [[t[r].clone() for t in (p, m, v)] for r in range(R)]
+    lr, b1, b2, eps, wd = 2.0**-7, 0.875, 1 - 2.0**-7, 2.0**-14, 2.0**-6
+    steps = torch.zeros(R, device=DEV, dtype=dtype)
+    mask = torch.ones(R, dtype=torch.bool, device=DEV)
+    for k in range(3):
+        grad = rnd()
+        for r in range(R):
+            torch._fused_adam_([ref[r][0]], [grad[r].clone()], [ref[r][1]], [ref[r][2]], [],
+                               [torch.tensor(float(k + 1), device=DEV)], lr=lr, beta1=b1,
+                               beta2=b2, weight_decay=wd, eps=eps, amsgrad=False,
+                               maximize=False, grad_scale=None, found_inf=None)
+        K.adam_step_(p, grad, m, v, None, steps, *(full(R, x, dtype) for x in (lr, b1, b2, eps, wd)),
+                     mask, amsgrad=False, maximize=False, decoupled_weight_decay=False)
+    torch.cuda.synchronize()
+    for r in range(R):
+        for got, want in zip((p[r], m[r], v[r]), ref[r]):
+            assert torch.equal(got, want)
+
+
+@pytest.mark.parametrize("dtype", [torch.float64, torch.float16, torch.bfloat16])
+def test_sgd_adagrad_other_dtypes_close_to_fp32(dtype):
+    R, T = 2, 100
+    tol = {torch.float64: 1e-6, torch.float16: 2e-3, torch.bfloat16: 2e-2}[dtype]
+    g = torch.Generator(device=DEV).manual_seed(16)
+    base = [torch.randn(R, T, device=DEV, generator=g) for _ in range(3)]
+    for op in ("sgd", "adagrad"):
+        outs = []
+        for dt in (torch.float32, dtype):
+            p, gr, x = (t.to(dt).clone() for t in base)
+            x = x.abs()
+            steps = torch.zeros(R, device=DEV, dtype=dt)
+            mask = torch.ones(R, dtype=torch.bool, device=DEV)
+            if op == "sgd":
+                K.sgd_step_(p, gr, x, steps, full(R, 0.125, dt), full(R, 0.5, dt),
+                            full(R, 0.0, dt), full(R, 0.0, dt), mask, nesterov=True,
+                            maximize=False)
+            else:
+                K.adagrad_step_(p, gr, x, steps, full(R, 0.125, dt), full(R, 0.0, dt),
+                                full(R, 0.0, dt), full(R, 2.0**-14, dt), mask, maximize=False)
+            outs.append((p.float(), x.float()))
+        torch.cuda.synchronize()
+        for a, b in zip(*outs):
+            torch.testing.assert_close(b, a, atol=tol, rtol=tol)
