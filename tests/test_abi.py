@@ -117,7 +117,8 @@ def test_vmap_rule_squeezes_replica_dim_on_meta():
                             maximize=False, decoupled_weight_decay=True)
 
     out = vmap(one)(*args)
-    assert out.shape == ()  # the rule returns an unbatched scalar
+    # the rule returns one unbatched scalar, which vmap broadcasts over B
+    assert out.shape == (B,)
 
 
 def test_consolidated_helpers():
