@@ -275,6 +275,20 @@ def read_traffic(kernel: str):
     return None
 
 
+def calibrate_copy(nbytes: int = 1 << 30, reps: int = 3) -> None:
+    """A plain device copy of known size: the per-dispatch FETCH_SIZE and
+    WRITE_SIZE it produces under rocprofv3 give the counters' scale."""
+    import torch
+
+    src = torch.ones(nbytes // 4, device="cuda")
+    dst = torch.empty_like(src)
+    for _ in range(reps):
+        dst.copy_(src)
+    torch.cuda.synchronize()
+    print(json.dumps({"calibration": "copy", "bytes_read": nbytes, "bytes_written": nbytes,
+                      "dispatches": reps}))
+
+
 def main():
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
@@ -284,11 +298,17 @@ def main():
     ap.add_argument("--cpu-steps", type=int, default=5)
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--no-loop-baseline", action="store_true")
+    ap.add_argument("--calibrate-copy", action="store_true",
+                    help="run only a plain 1 GiB device copy (reads and writes 2^30 B "
+                         "each), to scale rocprofv3 FETCH_SIZE / WRITE_SIZE counters")
     ap.add_argument("--cpu-worker", action="store_true", help=argparse.SUPPRESS)
     args = ap.parse_args()
 
     if args.cpu_worker:
         cpu_worker(args.config, args.steps)
+        return
+    if args.calibrate_copy:
+        calibrate_copy()
         return
     world = int(os.environ.get("WORLD_SIZE", "1"))
     if args.gpus != 1 or world != 1:
