@@ -572,11 +572,14 @@ int launch_bump(void* steps, const uint8_t* mask, int64_t R, void* out_zero,
 }
 
 // Runs the optional bump, then `launch` when there is any work.
+// Empty tensors may carry null data pointers, so operands are only required
+// where they are dereferenced: steps and mask when R > 0, the rest (checked
+// inside `launch`) when there is at least one element.
 template <typename T, typename Launch>
 int run_step(void* steps, const uint8_t* mask, int64_t R, int64_t T_,
              uint32_t flags, void* out_zero, hipStream_t stream,
              Launch&& launch) {
-  if (R < 0 || T_ < 0 || steps == nullptr || mask == nullptr) {
+  if (R < 0 || T_ < 0 || (R > 0 && (steps == nullptr || mask == nullptr))) {
     return kInvalid;
   }
   if ((flags & TS_BUMP_STEPS) != 0 || out_zero != nullptr) {
@@ -605,12 +608,13 @@ int adam_typed(const ts_rt_buf* bufs, void* steps, const void* lr,
                uint32_t flags, void* out_zero, hipStream_t stream) {
   const bool amsgrad = (flags & TS_AMSGRAD) != 0;
   const bool adamw = (flags & TS_ADAMW) != 0;
-  if (bufs == nullptr || lr == nullptr || beta1 == nullptr || beta2 == nullptr ||
-      eps == nullptr || wd == nullptr) {
+  if (bufs == nullptr) {
     return kInvalid;
   }
+  const bool work = R > 0 && T_ > 0;
   AdamArgs<T> a;
-  if (!fill_operands<T>(bufs, amsgrad ? 5 : 4, a.x)) {
+  if (work && (lr == nullptr || beta1 == nullptr || beta2 == nullptr || eps == nullptr ||
+               wd == nullptr || !fill_operands<T>(bufs, amsgrad ? 5 : 4, a.x))) {
     return kInvalid;
   }
   a.steps = static_cast<const T*>(steps);
@@ -648,17 +652,19 @@ int sgd_typed(const ts_rt_buf* bufs, void* steps, const void* lr,
               const void* momentum, const void* dampening, const void* wd,
               const uint8_t* mask, int64_t R, int64_t T_, uint32_t flags,
               void* out_zero, hipStream_t stream) {
-  if (bufs == nullptr || lr == nullptr || momentum == nullptr ||
-      dampening == nullptr || wd == nullptr) {
+  if (bufs == nullptr) {
     return kInvalid;
   }
+  const bool work = R > 0 && T_ > 0;
+  // bufs[2].data == NULL selects the buffer-less (depth-2) form.
   const bool has_buf = bufs[2].data != nullptr;
   const bool nesterov = (flags & TS_NESTEROV) != 0;
-  if (nesterov && !has_buf) {
+  if (work && nesterov && !has_buf) {
     return kInvalid;
   }
   SgdArgs<T> a;
-  if (!fill_operands<T>(bufs, has_buf ? 3 : 2, a.x)) {
+  if (work && (lr == nullptr || momentum == nullptr || dampening == nullptr ||
+               wd == nullptr || !fill_operands<T>(bufs, has_buf ? 3 : 2, a.x))) {
     return kInvalid;
   }
   a.steps = static_cast<const T*>(steps);
@@ -695,12 +701,13 @@ int adagrad_typed(const ts_rt_buf* bufs, void* steps, const void* lr,
                   const void* lr_decay, const void* wd, const void* eps,
                   const uint8_t* mask, int64_t R, int64_t T_, uint32_t flags,
                   void* out_zero, hipStream_t stream) {
-  if (bufs == nullptr || lr == nullptr || lr_decay == nullptr || wd == nullptr ||
-      eps == nullptr) {
+  if (bufs == nullptr) {
     return kInvalid;
   }
+  const bool work = R > 0 && T_ > 0;
   AdagradArgs<T> a;
-  if (!fill_operands<T>(bufs, 3, a.x)) {
+  if (work && (lr == nullptr || lr_decay == nullptr || wd == nullptr || eps == nullptr ||
+               !fill_operands<T>(bufs, 3, a.x))) {
     return kInvalid;
   }
   a.steps = static_cast<const T*>(steps);
