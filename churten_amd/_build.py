@@ -86,6 +86,12 @@ def build_library(verbose: bool = False) -> Path:
     return LIB
 
 
+# The CPU kernels state every fused multiply-add explicitly (std::fma) and
+# must not gain or lose any: -ffp-contract=off. AVX2/FMA as the reference's
+# CPU build (its setup.py:58-60), which the element formulations reproduce.
+CPU_KERNEL_FLAGS = ["-O3", "-mavx2", "-mfma", "-ffp-contract=off", "-fno-math-errno"]
+
+
 def build_extension(verbose: bool = False) -> Path:
     import torch
     from torch.utils import cpp_extension
@@ -93,13 +99,10 @@ def build_extension(verbose: bool = False) -> Path:
     torch_lib = Path(torch.__file__).resolve().parent / "lib"
     incs = [*cpp_extension.include_paths(), sysconfig.get_paths()["include"], "/opt/rocm/include"]
     abi = int(torch._C._GLIBCXX_USE_CXX11_ABI)
-    tmp = EXT.with_suffix(".so.tmp")
-    cmd = [
+    common = [
         "g++",
-        "-O2",
         "-std=c++17",
         "-fPIC",
-        "-shared",
         "-Wall",
         "-Wno-unused-function",
         f"-D_GLIBCXX_USE_CXX11_ABI={abi}",
@@ -107,20 +110,34 @@ def build_extension(verbose: bool = False) -> Path:
         "-DUSE_ROCM=1",
         "-DTORCH_EXTENSION_NAME=_C",
         *[f"-isystem{p}" for p in incs],
-        str(CSRC / "torch_ops.cpp"),
-        "-o",
-        str(tmp),
-        f"-L{LIB_DIR}",
-        "-lchurten_optim",
-        f"-L{torch_lib}",
-        "-lc10",
-        "-lc10_hip",
-        "-ltorch_cpu",
-        "-ltorch",
-        "-Wl,-rpath,$ORIGIN/../lib",
-        f"-Wl,-rpath,{torch_lib}",
     ]
-    _run(cmd, verbose)
+    build_dir = PKG / "_objs"
+    build_dir.mkdir(exist_ok=True)
+    objs = []
+    for src, flags in (("torch_ops.cpp", ["-O2"]), ("cpu_kernels.cpp", CPU_KERNEL_FLAGS)):
+        obj = build_dir / (Path(src).stem + ".o")
+        _run([*common, *flags, "-c", str(CSRC / src), "-o", str(obj)], verbose)
+        objs.append(str(obj))
+    tmp = EXT.with_suffix(".so.tmp")
+    _run(
+        [
+            "g++",
+            "-shared",
+            *objs,
+            "-o",
+            str(tmp),
+            f"-L{LIB_DIR}",
+            "-lchurten_optim",
+            f"-L{torch_lib}",
+            "-lc10",
+            "-lc10_hip",
+            "-ltorch_cpu",
+            "-ltorch",
+            "-Wl,-rpath,$ORIGIN/../lib",
+            f"-Wl,-rpath,{torch_lib}",
+        ],
+        verbose,
+    )
     os.replace(tmp, EXT)
     return EXT
 
