@@ -1,0 +1,53 @@
+"""``Adagrad`` -- a GradientTransformation over the consolidated state.
+
+Restates src/torchstrap/optimizer/adagrad.py:274-346: ``init`` registers the
+``(N,)`` hyperparameters, the step counter and the ``(N, T)`` accumulator,
+filled with ``initial_accumulator_value`` (pad lanes included: they never see
+a gradient, so they never move the pad parameters); ``update`` issues one
+``torchstrap::adagrad_step_`` call.
+"""
+
+from __future__ import annotations
+
+import torch
+
+from churten_amd.kernels.adagrad import adagrad_step_
+from churten_amd.optimizer.grad_transform import GradientTransformation
+from churten_amd.state import State
+
+__all__ = ["Adagrad", "adagrad_step_"]
+
+
+class Adagrad(metaclass=GradientTransformation):
+    @classmethod
+    def init(cls, state: State, *, lr=1e-2, lr_decay=0.0, weight_decay=0.0, eps=1e-10,
+             initial_accumulator_value=0.0, maximize: bool = False) -> State:
+        for key, value in (("lr", lr), ("lr_decay", lr_decay), ("weight_decay", weight_decay),
+                           ("eps", eps), ("state_steps", 0)):
+            state.add_optim_state(key, value)
+        state.add_optim_state("state_sums", per_param=True)
+        sums = state.optimizer_state["state_sums"]
+        if isinstance(initial_accumulator_value, torch.Tensor):
+            sums.copy_(initial_accumulator_value.expand_as(sums))
+        elif initial_accumulator_value != 0.0:
+            sums.fill_(initial_accumulator_value)
+        state.add_optim_meta("maximize", maximize)
+        return state
+
+    @classmethod
+    def update(cls, state: State, maximize: bool = False) -> State:
+        opt = state.optimizer_state
+        maximize = bool(opt.get("maximize", maximize))
+        adagrad_step_(
+            torch.atleast_2d(state.flat_params),
+            torch.atleast_2d(state.flat_grads),
+            torch.atleast_2d(opt["state_sums"]),
+            torch.atleast_1d(opt["state_steps"]),
+            torch.atleast_1d(opt["lr"]),
+            torch.atleast_1d(opt["lr_decay"]),
+            torch.atleast_1d(opt["weight_decay"]),
+            torch.atleast_1d(opt["eps"]),
+            torch.atleast_1d(state.active_mask),
+            maximize=maximize,
+        )
+        return state

@@ -1,0 +1,65 @@
+"""``Adam`` -- a GradientTransformation over the consolidated state.
+
+Restates src/torchstrap/optimizer/adam.py:49-143: ``init`` registers the
+per-replica ``(N,)`` hyperparameters (floats or tensors, stored in the param
+dtype), a zero ``state_steps`` counter, ``(N, T)`` moments (plus
+``max_exp_avg_sqs`` under amsgrad) and the static variant flags; ``update``
+issues one ``torchstrap::adam_step_`` call over the whole ensemble.
+Defaults are the reference's: AdamW-style decoupled decay with
+weight_decay = 1e-2.
+"""
+
+from __future__ import annotations
+
+import torch
+
+from churten_amd.kernels.adam import adam_step_
+from churten_amd.optimizer.grad_transform import GradientTransformation
+from churten_amd.state import State
+
+__all__ = ["Adam", "adam_step_"]
+
+
+class Adam(metaclass=GradientTransformation):
+    @classmethod
+    def init(cls, state: State, *, lr=1e-3, beta1=0.9, beta2=0.999, eps=1e-8,
+             weight_decay=1e-2, amsgrad: bool = False, maximize: bool = False,
+             decoupled_weight_decay: bool = True) -> State:
+        for key, value in (("lr", lr), ("beta1", beta1), ("beta2", beta2), ("eps", eps),
+                           ("weight_decay", weight_decay), ("state_steps", 0)):
+            state.add_optim_state(key, value)
+        state.add_optim_state("exp_avgs", per_param=True)
+        state.add_optim_state("exp_avg_sqs", per_param=True)
+        if amsgrad:
+            state.add_optim_state("max_exp_avg_sqs", per_param=True)
+        state.add_optim_meta("amsgrad", amsgrad)
+        state.add_optim_meta("maximize", maximize)
+        state.add_optim_meta("decoupled_weight_decay", decoupled_weight_decay)
+        return state
+
+    @classmethod
+    def update(cls, state: State, decoupled_weight_decay: bool = True, maximize: bool = False,
+               amsgrad: bool = False) -> State:
+        opt = state.optimizer_state
+        amsgrad = bool(opt.get("amsgrad", amsgrad))
+        maximize = bool(opt.get("maximize", maximize))
+        decoupled_weight_decay = bool(opt.get("decoupled_weight_decay", decoupled_weight_decay))
+        mx = opt.get("max_exp_avg_sqs")
+        adam_step_(
+            torch.atleast_2d(state.flat_params),
+            torch.atleast_2d(state.flat_grads),
+            torch.atleast_2d(opt["exp_avgs"]),
+            torch.atleast_2d(opt["exp_avg_sqs"]),
+            torch.atleast_2d(mx) if mx is not None else None,
+            torch.atleast_1d(opt["state_steps"]),
+            torch.atleast_1d(opt["lr"]),
+            torch.atleast_1d(opt["beta1"]),
+            torch.atleast_1d(opt["beta2"]),
+            torch.atleast_1d(opt["eps"]),
+            torch.atleast_1d(opt["weight_decay"]),
+            torch.atleast_1d(state.active_mask),
+            amsgrad=amsgrad,
+            maximize=maximize,
+            decoupled_weight_decay=decoupled_weight_decay,
+        )
+        return state

@@ -1,0 +1,64 @@
+"""``SGD`` -- a GradientTransformation over the consolidated state.
+
+Restates src/torchstrap/optimizer/sgd.py:168-256: ``init`` applies
+torch.optim.SGD's Nesterov validation across the ensemble (non-zero momentum
+somewhere and no dampening anywhere), registers the ``(N,)``
+hyperparameters and the step counter, and allocates the ``(N, T)`` momentum
+buffers iff any replica has non-zero momentum -- whether the buffer exists is
+one call-level decision, as in ATen, while its value stays per replica. A
+momentum-0 replica in a buffered call runs the momentum recursion with
+momentum 0 (its buffer row is written), as the reference kernels do.
+"""
+
+from __future__ import annotations
+
+import torch
+
+from churten_amd.kernels.sgd import sgd_step_
+from churten_amd.optimizer.grad_transform import GradientTransformation
+from churten_amd.state import State
+
+__all__ = ["SGD", "sgd_step_"]
+
+
+def _any_nonzero(value) -> bool:
+    return bool(torch.as_tensor(value).ne(0).any())
+
+
+class SGD(metaclass=GradientTransformation):
+    @classmethod
+    def init(cls, state: State, *, lr=1e-3, momentum=0.0, dampening=0.0, weight_decay=0.0,
+             nesterov: bool = False, maximize: bool = False) -> State:
+        if nesterov and (not _any_nonzero(momentum) or _any_nonzero(dampening)):
+            raise ValueError("Nesterov momentum requires a non-zero momentum and zero dampening")
+        for key, value in (("lr", lr), ("momentum", momentum), ("dampening", dampening),
+                           ("weight_decay", weight_decay), ("state_steps", 0)):
+            state.add_optim_state(key, value)
+        has_momentum = _any_nonzero(momentum)
+        if has_momentum:
+            state.add_optim_state("momentum_buffers", per_param=True)
+        state.add_optim_meta("nesterov", nesterov)
+        state.add_optim_meta("maximize", maximize)
+        state.add_optim_meta("has_momentum", has_momentum)
+        return state
+
+    @classmethod
+    def update(cls, state: State, nesterov: bool = False, maximize: bool = False) -> State:
+        opt = state.optimizer_state
+        nesterov = bool(opt.get("nesterov", nesterov))
+        maximize = bool(opt.get("maximize", maximize))
+        mb = opt.get("momentum_buffers")
+        sgd_step_(
+            torch.atleast_2d(state.flat_params),
+            torch.atleast_2d(state.flat_grads),
+            torch.atleast_2d(mb) if mb is not None else None,
+            torch.atleast_1d(opt["state_steps"]),
+            torch.atleast_1d(opt["lr"]),
+            torch.atleast_1d(opt["momentum"]),
+            torch.atleast_1d(opt["dampening"]),
+            torch.atleast_1d(opt["weight_decay"]),
+            torch.atleast_1d(state.active_mask),
+            nesterov=nesterov,
+            maximize=maximize,
+        )
+        return state
