@@ -133,7 +133,11 @@ def make_config(cfg: int, device="cuda", seed=None, N=None):
         args = (p, gr, m, v, None, steps, *hyp, mask)
         kw = dict(amsgrad=False, maximize=False, decoupled_weight_decay=False)
     active = int(mask.sum().item())
-    return c["op"], args, kw, active * T * bytes_per_elem(cfg)
+    nbytes = active * T * bytes_per_elem(cfg)
+    if cfg == 3:  # a replica's first step does not read its momentum buffer
+        first_active = int((mask & (steps == 0)).sum().item())
+        nbytes -= first_active * T * 4
+    return c["op"], args, kw, nbytes
 
 
 # ---------------------------------------------------------------------------
@@ -219,6 +223,19 @@ def kernel_only_timing(op_name, args, kw, launches: int) -> float:
         call = lambda: lib.ts_adam_step(  # noqa: E731
             bufs, 0, vp(args[5]), *[vp(t) for t in args[6:11]], vp(args[11]),
             ctypes.c_int64(R), ctypes.c_int64(T), ctypes.c_uint32(flags),
+            ctypes.c_void_p(0), ctypes.c_void_p(stream.cuda_stream))
+    elif op_name == "sgd":
+        bufs = (RtBuf * 3)(*[buf(t) for t in args[:3]])
+        flags = 8 if kw["nesterov"] else 0
+        call = lambda: lib.ts_sgd_step(  # noqa: E731
+            bufs, 0, vp(args[3]), *[vp(t) for t in args[4:8]], vp(args[8]),
+            ctypes.c_int64(R), ctypes.c_int64(T), ctypes.c_uint32(flags),
+            ctypes.c_void_p(0), ctypes.c_void_p(stream.cuda_stream))
+    elif op_name == "adagrad":
+        bufs = (RtBuf * 3)(*[buf(t) for t in args[:3]])
+        call = lambda: lib.ts_adagrad_step(  # noqa: E731
+            bufs, 0, vp(args[3]), *[vp(t) for t in args[4:8]], vp(args[8]),
+            ctypes.c_int64(R), ctypes.c_int64(T), ctypes.c_uint32(0),
             ctypes.c_void_p(0), ctypes.c_void_p(stream.cuda_stream))
     else:
         raise ValueError(op_name)
@@ -344,7 +361,7 @@ def main():
 
     kern_ms = kernel_only_timing(op_name, op_args, kw, max(10, args.steps))
     achieved = nbytes / (kern_ms * 1e-3) / 1e9
-    kernel = "adam_stream_kernel"
+    kernel = f"{op_name}_stream_kernel"
     del op_args
     torch.cuda.empty_cache()
 
