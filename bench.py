@@ -281,6 +281,60 @@ def loop_baseline(cfg: int, steps: int, fused: bool):
     return dt * 1e3
 
 
+def grad_scatter_timing(cfg: int, steps: int):
+    """The training step's gradient hand-off, timed three ways on the same
+    state: the reference pattern (one copy per parameter tensor into the
+    consolidated gradient buffer, grad_transform.py:29, then the update), the
+    fused segmented update that also fills the buffer, and the fused update
+    alone. Per-parameter gradients are (N, *shape) tensors, as vmap returns."""
+    import torch
+
+    c = CONFIGS[cfg]
+    op_name, args, kw, _ = make_config(cfg)
+    if op_name != "adam":
+        return None
+    p, G = args[0], args[1]
+    N = p.shape[0]
+    g = torch.Generator(device="cuda").manual_seed(11)
+    grads, cols, col = [], [], 0
+    for s in c["layout"]:
+        grads.append(torch.randn(N, *s, device="cuda", generator=g).mul_(1e-3))
+        cols.append(col)
+        col += math.prod(s)
+    views = [G[:, o:o + math.prod(s)].view(N, *s) for o, s in zip(cols, c["layout"])]
+    rest = args[2:]
+    seg = torch.ops.churten.adam_step_segments_
+    upd = torch.ops.torchstrap.adam_step_
+
+    def reference():
+        for v, t in zip(views, grads):
+            v.copy_(t)
+        upd(p, G, *rest, **kw)
+
+    variants = {
+        "scatter_then_update_ms": reference,
+        "fused_keep_grads_ms": lambda: seg(p, grads, cols, G, *rest, **kw),
+        "fused_ms": lambda: seg(p, grads, cols, None, *rest, **kw),
+    }
+    stream = torch.cuda.current_stream()
+    out = {}
+    for name, fn in variants.items():
+        fn()
+        torch.cuda.synchronize()
+        e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        e0.record(stream)
+        for _ in range(steps):
+            fn()
+        e1.record(stream)
+        torch.cuda.synchronize()
+        out[name] = round(e0.elapsed_time(e1) / steps, 4)
+    del args, grads, views, rest, p, G
+    torch.cuda.empty_cache()
+    out["speedup_keep_grads"] = round(out["scatter_then_update_ms"] / out["fused_keep_grads_ms"], 3)
+    out["speedup"] = round(out["scatter_then_update_ms"] / out["fused_ms"], 3)
+    return out
+
+
 def read_traffic(kernel: str):
     """HBM bytes per launch from the committed rocprofv3 --pmc summary, if any."""
     f = ROOT / "profiles" / f"{kernel}_traffic.json"
@@ -315,6 +369,8 @@ def main():
     ap.add_argument("--cpu-steps", type=int, default=5)
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--no-loop-baseline", action="store_true")
+    ap.add_argument("--no-grad-scatter", action="store_true",
+                    help="skip the scatter-then-update vs fused segmented timing")
     ap.add_argument("--calibrate-copy", action="store_true",
                     help="run only a plain 1 GiB device copy (reads and writes 2^30 B "
                          "each), to scale rocprofv3 FETCH_SIZE / WRITE_SIZE counters")
@@ -365,6 +421,10 @@ def main():
     del op_args
     torch.cuda.empty_cache()
 
+    scatter = None
+    if not args.no_grad_scatter and op_name == "adam":
+        scatter = grad_scatter_timing(args.config, max(5, args.steps // 2))
+
     loop = {}
     if not args.no_loop_baseline and op_name == "adam":
         loop["fused_ms"] = round(loop_baseline(args.config, 3, fused=True), 3)
@@ -400,6 +460,7 @@ def main():
                      "traffic": read_traffic(f"{kernel}_cfg{args.config}")},
         "cpu_baseline": cpu,
         "python_loop_baseline": loop or None,
+        "grad_scatter_step": scatter,
         "speedup_vs_python_loop": ({k: round(v / step_ms, 2) for k, v in loop.items()}
                                    if loop else None),
     }

@@ -1,29 +1,46 @@
 // optim_kernels.hip -- gfx950 kernels and the extern "C" launchers of
 // include/churten_optim.h.
 //
-// Work decomposition. The consolidated (R, T) state is cut into tiles of
-// kTile = kThreads * kPack * kUnroll consecutive elements of one row; the 1-D
-// grid enumerates (replica, tile) pairs replica-major, so blockIdx.x alone
-// gives both and no grid dimension caps R. A workgroup first reads its
-// replica's active flag: a frozen replica is a workgroup-uniform early exit, so
-// its rows are never read or written (they stay bit-identical, and a replica
-// frozen at step 0 never evaluates 1 - beta^0 = 0). Active workgroups read the
-// replica's hyperparameters once (scalar loads: the address is uniform), derive
-// the per-replica constants, then stream their tile.
+// Structure. Each optimizer is a policy (AdamPolicy, SgdPolicy, AdagradPolicy):
+// its per-replica prologue (hyperparameters, bias corrections, is_first_step,
+// corrected_lr) and its per-element update, both from optim_math.h. Three
+// drivers move the bytes, identically for every policy:
 //
-// Streaming path (unit inner stride, T % 4 == 0, 16-byte aligned rows, which is
-// the layout the consolidation produces): every thread issues kUnroll 16-byte
-// non-temporal loads per buffer before any arithmetic, then computes and issues
-// the non-temporal stores.
-// Element path (any strides, ragged T): the same tile geometry with one element
-// per access; the per-element arithmetic is the same inlined function, so both
-// paths give bit-identical results for the same element.
+//   stream_kernel   the consolidated (R, T) layout `State` produces: unit inner
+//                   stride, 16-byte aligned rows, T % 4 == 0. Non-temporal
+//                   16-byte loads and stores.
+//   element_kernel  any strides, ragged T, misaligned rows: one element per
+//                   access, same tile geometry.
+//   segment_kernel  the gradient arrives as one tensor per parameter (a segment
+//                   table) instead of the consolidated (R, T) gradient buffer:
+//                   the gradient scatter of the training step is fused into the
+//                   update. Optionally the consolidated gradient is written on
+//                   the way through, so `flat_grads` stays what it would have
+//                   been.
+//
+// Operands are ordered [0] param, [1] grad, [2..] optimizer state (Adam:
+// exp_avg, exp_avg_sq, [max_exp_avg_sq]; SGD: [momentum_buffer]; Adagrad:
+// state_sum). The grad is read-only.
+//
+// Work decomposition. Rows are cut into tiles of kTile consecutive elements
+// (segments into tiles of their own); a 1-D grid enumerates (replica, tile)
+// pairs replica-major, so blockIdx.x gives both and no grid dimension caps R.
+// A workgroup first reads its replica's active flag: a frozen replica is a
+// workgroup-uniform early exit, so its rows are never read or written (they stay
+// bit-identical, and a replica frozen at step 0 never evaluates 1 - beta^0 = 0).
+// Active workgroups read the replica's hyperparameters once (uniform address:
+// scalar loads) and derive the per-replica constants, then stream their tile.
+// All drivers inline the same per-element update, so the same element gives
+// the same bits whichever driver processed it.
 //
 // Everything is enqueued on the caller's stream; nothing is allocated.
 
 #include <hip/hip_runtime.h>
 
 #include <stdint.h>
+
+#include <algorithm>
+#include <initializer_list>
 
 #include "../../include/churten_optim.h"
 #include "optim_math.h"
@@ -40,7 +57,8 @@ namespace {
 constexpr int kThreads = 128;
 constexpr int kPack = 4;
 constexpr int kUnroll = 2;
-constexpr int64_t kTile = int64_t(kThreads) * kPack * kUnroll;
+constexpr int kPer = kPack * kUnroll;  // elements per thread per tile
+constexpr int64_t kTile = int64_t(kThreads) * kPer;
 
 template <typename T>
 struct alignas(sizeof(T) * kPack) Pack {
@@ -66,12 +84,22 @@ __device__ __forceinline__ void store_stream(Pack<T>* p, const Pack<T>& v) {
                               reinterpret_cast<PackBits<T>*>(p));
 }
 
-// Up to five (R, T) operands. `data[i]` is element (0, 0) of operand i.
+constexpr int kMaxOperands = 5;
+
+// (R, T) operands. `data[i]` is element (0, 0) of operand i.
 template <typename T>
 struct Operands {
-  T* data[5];
-  int64_t stride_r[5];
-  int64_t stride_t[5];
+  T* data[kMaxOperands];
+  int64_t stride_r[kMaxOperands];
+  int64_t stride_t[kMaxOperands];
+};
+
+// (R,) inputs: the step counter, up to five hyperparameter vectors and the mask.
+template <typename T>
+struct Vectors {
+  const T* steps;
+  const T* h[5];
+  const uint8_t* mask;
 };
 
 struct Grid {
@@ -84,6 +112,443 @@ __device__ __forceinline__ void tile_of_block(const Grid& g, uint32_t& r,
   const uint32_t tile = blockIdx.x;
   r = tile / g.tiles_per_row;
   t0 = int64_t(tile - r * g.tiles_per_row) * kTile;
+}
+
+template <typename T>
+__device__ __forceinline__ double hyper_at(const T* h, uint32_t r) {
+  return static_cast<double>(widen(h[r]));
+}
+
+// ---------------------------------------------------------------------------
+// Policies
+// ---------------------------------------------------------------------------
+// Adam / AdamW: h = {lr, beta1, beta2, eps, weight_decay}.
+template <typename T_, bool ADAMW, bool AMSGRAD>
+struct AdamPolicy {
+  using T = T_;
+  using M = op_t<T>;
+  static constexpr int NS = AMSGRAD ? 3 : 2;
+  struct Rep {
+    AdamHyper h;
+    M bc1, bc2s;
+  };
+  __device__ static void prologue(const Vectors<T>& v, uint32_t r, Rep& rep) {
+    rep.h.lr = hyper_at(v.h[0], r);
+    rep.h.beta1 = hyper_at(v.h[1], r);
+    rep.h.beta2 = hyper_at(v.h[2], r);
+    rep.h.eps = hyper_at(v.h[3], r);
+    rep.h.weight_decay = hyper_at(v.h[4], r);
+    adam_bias_corrections<M>(rep.h.beta1, rep.h.beta2, hyper_at(v.steps, r), rep.bc1,
+                             rep.bc2s);
+  }
+  __device__ static bool reads_state(const Rep&) { return true; }
+  __device__ static void update(M& p, M g, M (&s)[NS], const Rep& rep, bool maximize) {
+    M mx = M(0);
+    if constexpr (AMSGRAD) mx = s[2];
+    adam_element<M, ADAMW, AMSGRAD>(p, g, s[0], s[1], mx, rep.h, maximize, rep.bc1,
+                                    rep.bc2s);
+    if constexpr (AMSGRAD) s[2] = mx;
+  }
+};
+
+// SGD: h = {lr, momentum, dampening, weight_decay}. The hyperparameters are
+// carried as double inside the element math, as torch's ROCm `_fused_sgd_`
+// takes them (checked on the MI355X: carrying them as float instead changes
+// params and buffers by up to a few ulp).
+template <typename T_, bool HAS_BUF, bool NESTEROV>
+struct SgdPolicy {
+  using T = T_;
+  using M = op_t<T>;
+  static constexpr int NS = HAS_BUF ? 1 : 0;
+  struct Rep {
+    SgdHyper<double> h;
+    bool first;
+  };
+  __device__ static void prologue(const Vectors<T>& v, uint32_t r, Rep& rep) {
+    rep.h.lr = hyper_at(v.h[0], r);
+    rep.h.momentum = hyper_at(v.h[1], r);
+    rep.h.dampening = hyper_at(v.h[2], r);
+    rep.h.weight_decay = hyper_at(v.h[3], r);
+    rep.first = widen(v.steps[r]) == M(1);
+  }
+  // On a replica's first step the buffer is overwritten by the gradient
+  // without being read, so it is not fetched.
+  __device__ static bool reads_state(const Rep& rep) { return !rep.first; }
+  __device__ static void update(M& p, M g, M (&s)[NS > 0 ? NS : 1], const Rep& rep,
+                                bool maximize) {
+    M buf = s[0];
+    sgd_element<M, double, HAS_BUF, NESTEROV>(p, g, buf, rep.h, maximize, rep.first);
+    s[0] = buf;
+  }
+};
+
+// Adagrad: h = {lr, lr_decay, weight_decay, eps}.
+template <typename T_>
+struct AdagradPolicy {
+  using T = T_;
+  using M = op_t<T>;
+  static constexpr int NS = 1;
+  struct Rep {
+    AdagradHyper h;
+  };
+  __device__ static void prologue(const Vectors<T>& v, uint32_t r, Rep& rep) {
+    rep.h.weight_decay = hyper_at(v.h[2], r);
+    rep.h.eps = hyper_at(v.h[3], r);
+    rep.h.corrected_lr = adagrad_corrected_lr(hyper_at(v.h[0], r), hyper_at(v.h[1], r),
+                                              static_cast<float>(widen(v.steps[r])));
+  }
+  __device__ static bool reads_state(const Rep&) { return true; }
+  __device__ static void update(M& p, M g, M (&s)[NS], const Rep& rep, bool maximize) {
+    adagrad_element<M>(p, g, s[0], rep.h, maximize);
+  }
+};
+
+template <typename P>
+constexpr int state_slots() {
+  return P::NS > 0 ? P::NS : 1;
+}
+
+template <typename P>
+struct KArgs {
+  Operands<typename P::T> x;
+  Vectors<typename P::T> vec;
+  Grid g;
+  bool maximize;
+};
+
+// One element through the policy: widen, update, narrow. `s_io` holds the
+// state operands' values (unread ones are never used).
+template <typename P>
+__device__ __forceinline__ void apply_element(typename P::T& p_io, typename P::T g_in,
+                                              typename P::T (&s_io)[state_slots<P>()],
+                                              bool load_state, const typename P::Rep& rep,
+                                              bool maximize) {
+  using M = op_t<typename P::T>;
+  M p = widen(p_io);
+  M s[state_slots<P>()];
+#pragma unroll
+  for (int k = 0; k < state_slots<P>(); ++k) {
+    s[k] = (load_state && k < P::NS) ? widen(s_io[k]) : M(0);
+  }
+  P::update(p, widen(g_in), s, rep, maximize);
+  p_io = narrow<typename P::T>(p);
+#pragma unroll
+  for (int k = 0; k < P::NS; ++k) {
+    s_io[k] = narrow<typename P::T>(s[k]);
+  }
+}
+
+// ---------------------------------------------------------------------------
+// Drivers
+// ---------------------------------------------------------------------------
+template <typename P>
+__global__ __launch_bounds__(kThreads) void stream_kernel(KArgs<P> a) {
+  using T = typename P::T;
+  constexpr int NS = P::NS;
+  constexpr int SS = state_slots<P>();
+  uint32_t r;
+  int64_t t0;
+  tile_of_block(a.g, r, t0);
+  if (!a.vec.mask[r]) {
+    return;
+  }
+  typename P::Rep rep;
+  P::prologue(a.vec, r, rep);
+  const bool load_state = P::reads_state(rep);
+
+  Pack<T>* row[2 + SS];
+#pragma unroll
+  for (int b = 0; b < 2 + NS; ++b) {
+    row[b] = reinterpret_cast<Pack<T>*>(a.x.data[b] + int64_t(r) * a.x.stride_r[b] + t0);
+  }
+  const int64_t packs_left = (a.g.T - t0) / kPack;
+
+  Pack<T> v[2 + SS][kUnroll];
+#pragma unroll
+  for (int u = 0; u < kUnroll; ++u) {
+    const int64_t i = int64_t(u) * kThreads + threadIdx.x;
+    if (i < packs_left) {
+      v[0][u] = load_stream(row[0] + i);
+      v[1][u] = load_stream(row[1] + i);
+      if (load_state) {
+#pragma unroll
+        for (int b = 2; b < 2 + NS; ++b) {
+          v[b][u] = load_stream(row[b] + i);
+        }
+      }
+    }
+  }
+#pragma unroll
+  for (int u = 0; u < kUnroll; ++u) {
+    const int64_t i = int64_t(u) * kThreads + threadIdx.x;
+    if (i < packs_left) {
+#pragma unroll
+      for (int k = 0; k < kPack; ++k) {
+        T s[SS];
+#pragma unroll
+        for (int b = 0; b < NS; ++b) s[b] = v[2 + b][u].v[k];
+        apply_element<P>(v[0][u].v[k], v[1][u].v[k], s, load_state, rep, a.maximize);
+#pragma unroll
+        for (int b = 0; b < NS; ++b) v[2 + b][u].v[k] = s[b];
+      }
+      store_stream(row[0] + i, v[0][u]);
+#pragma unroll
+      for (int b = 2; b < 2 + NS; ++b) {
+        store_stream(row[b] + i, v[b][u]);
+      }
+    }
+  }
+}
+
+template <typename P>
+__global__ __launch_bounds__(kThreads) void element_kernel(KArgs<P> a) {
+  using T = typename P::T;
+  constexpr int NS = P::NS;
+  constexpr int SS = state_slots<P>();
+  uint32_t r;
+  int64_t t0;
+  tile_of_block(a.g, r, t0);
+  if (!a.vec.mask[r]) {
+    return;
+  }
+  typename P::Rep rep;
+  P::prologue(a.vec, r, rep);
+  const bool load_state = P::reads_state(rep);
+
+  T* base[2 + SS];
+#pragma unroll
+  for (int b = 0; b < 2 + NS; ++b) {
+    base[b] = a.x.data[b] + int64_t(r) * a.x.stride_r[b];
+  }
+  T v[2 + SS][kPer];
+#pragma unroll
+  for (int u = 0; u < kPer; ++u) {
+    const int64_t t = t0 + int64_t(u) * kThreads + threadIdx.x;
+    if (t < a.g.T) {
+      v[0][u] = base[0][t * a.x.stride_t[0]];
+      v[1][u] = base[1][t * a.x.stride_t[1]];
+      if (load_state) {
+#pragma unroll
+        for (int b = 2; b < 2 + NS; ++b) {
+          v[b][u] = base[b][t * a.x.stride_t[b]];
+        }
+      }
+    }
+  }
+#pragma unroll
+  for (int u = 0; u < kPer; ++u) {
+    const int64_t t = t0 + int64_t(u) * kThreads + threadIdx.x;
+    if (t < a.g.T) {
+      T s[SS];
+#pragma unroll
+      for (int b = 0; b < NS; ++b) s[b] = v[2 + b][u];
+      apply_element<P>(v[0][u], v[1][u], s, load_state, rep, a.maximize);
+      base[0][t * a.x.stride_t[0]] = v[0][u];
+#pragma unroll
+      for (int b = 0; b < NS; ++b) {
+        base[2 + b][t * a.x.stride_t[2 + b]] = s[b];
+      }
+    }
+  }
+}
+
+// ---------------------------------------------------------------------------
+// Segmented gradients
+// ---------------------------------------------------------------------------
+constexpr int kMaxSegments = 64;
+
+// Up to kMaxSegments per-parameter (R, numel) tensors, each mapped onto the
+// columns [col, col + numel) of the (R, T) layout. tile0 is the prefix sum of
+// the segments' tile counts, so a row has tile0[n] tiles; bit s of `vec_ok`
+// says segment s can take 16-byte accesses.
+template <typename T>
+struct Segments {
+  const T* data[kMaxSegments];
+  int64_t stride_r[kMaxSegments];
+  int64_t col[kMaxSegments];
+  int64_t numel[kMaxSegments];
+  uint32_t tile0[kMaxSegments + 1];
+  uint64_t vec_ok;
+  int n;
+};
+
+template <typename P>
+struct SegArgs {
+  KArgs<P> k;  // k.x.data[1]: consolidated gradient to write, or null
+  Segments<typename P::T> seg;
+};
+
+__device__ __forceinline__ int segment_of_tile(const uint32_t* tile0, int n, uint32_t t) {
+  int lo = 0, hi = n - 1;
+  while (lo < hi) {
+    const int mid = (lo + hi + 1) >> 1;
+    if (tile0[mid] <= t) lo = mid;
+    else hi = mid - 1;
+  }
+  return lo;
+}
+
+template <typename P>
+__global__ __launch_bounds__(kThreads) void segment_kernel(SegArgs<P> a) {
+  using T = typename P::T;
+  constexpr int NS = P::NS;
+  constexpr int SS = state_slots<P>();
+  const uint32_t tiles_per_row = a.seg.tile0[a.seg.n];
+  const uint32_t r = blockIdx.x / tiles_per_row;
+  const uint32_t local = blockIdx.x - r * tiles_per_row;
+  const bool write_grad = a.k.x.data[1] != nullptr;
+  const bool active = a.k.vec.mask[r] != 0;
+  const int s = segment_of_tile(a.seg.tile0, a.seg.n, local);
+  // A segment without data is a gap between gradients: its columns take the
+  // gradient already in the consolidated buffer, or zero when there is none.
+  const bool gap = a.seg.data[s] == nullptr;
+  if (!active && (gap || !write_grad)) {
+    return;
+  }
+  const int64_t j0 = int64_t(local - a.seg.tile0[s]) * kTile;
+  const int64_t cnt = min(kTile, a.seg.numel[s] - j0);
+  const int64_t c0 = a.seg.col[s] + j0;
+  T* const g_dst =
+      write_grad ? a.k.x.data[1] + int64_t(r) * a.k.x.stride_r[1] + c0 * a.k.x.stride_t[1]
+                 : nullptr;
+  if (!active) {
+    // A frozen replica's optimizer state is not touched, but the consolidated
+    // gradient is still filled, as the separate scatter would have filled it.
+    const T* g_row = a.seg.data[s] + int64_t(r) * a.seg.stride_r[s] + j0;
+    for (int64_t j = threadIdx.x; j < cnt; j += kThreads) {
+      g_dst[j * a.k.x.stride_t[1]] = g_row[j];
+    }
+    return;
+  }
+
+  typename P::Rep rep;
+  P::prologue(a.k.vec, r, rep);
+  const bool load_state = P::reads_state(rep);
+
+  // Gradient source: the segment's row, or for a gap the consolidated buffer
+  // (null: zero). Only a real segment is stored into the consolidated buffer.
+  const T* g_src = g_dst;
+  int64_t g_stride = write_grad ? a.k.x.stride_t[1] : 0;
+  if (!gap) {
+    g_src = a.seg.data[s] + int64_t(r) * a.seg.stride_r[s] + j0;
+    g_stride = 1;
+  }
+  const bool store_grad = write_grad && !gap;
+  const T zero = narrow<T>(op_t<T>(0));
+
+  T* base[2 + SS];
+#pragma unroll
+  for (int b = 0; b < 2 + NS; ++b) {
+    base[b] = b == 1 ? nullptr
+                     : a.k.x.data[b] + int64_t(r) * a.k.x.stride_r[b] + c0 * a.k.x.stride_t[b];
+  }
+
+  int64_t done = 0;  // leading elements handled by the vector loop
+  if ((a.seg.vec_ok >> s) & 1u) {
+    const int64_t packs = cnt / kPack;
+    Pack<T> v[2 + SS][kUnroll];
+#pragma unroll
+    for (int u = 0; u < kUnroll; ++u) {
+      const int64_t i = int64_t(u) * kThreads + threadIdx.x;
+      if (i < packs) {
+        v[0][u] = load_stream(reinterpret_cast<const Pack<T>*>(base[0]) + i);
+        if (g_src != nullptr) {
+          v[1][u] = load_stream(reinterpret_cast<const Pack<T>*>(g_src) + i);
+        } else {
+#pragma unroll
+          for (int k = 0; k < kPack; ++k) v[1][u].v[k] = zero;
+        }
+        if (load_state) {
+#pragma unroll
+          for (int b = 2; b < 2 + NS; ++b) {
+            v[b][u] = load_stream(reinterpret_cast<const Pack<T>*>(base[b]) + i);
+          }
+        }
+      }
+    }
+#pragma unroll
+    for (int u = 0; u < kUnroll; ++u) {
+      const int64_t i = int64_t(u) * kThreads + threadIdx.x;
+      if (i < packs) {
+        if (store_grad) {
+          store_stream(reinterpret_cast<Pack<T>*>(g_dst) + i, v[1][u]);
+        }
+#pragma unroll
+        for (int k = 0; k < kPack; ++k) {
+          T st[SS];
+#pragma unroll
+          for (int b = 0; b < NS; ++b) st[b] = v[2 + b][u].v[k];
+          apply_element<P>(v[0][u].v[k], v[1][u].v[k], st, load_state, rep, a.k.maximize);
+#pragma unroll
+          for (int b = 0; b < NS; ++b) v[2 + b][u].v[k] = st[b];
+        }
+        store_stream(reinterpret_cast<Pack<T>*>(base[0]) + i, v[0][u]);
+#pragma unroll
+        for (int b = 2; b < 2 + NS; ++b) {
+          store_stream(reinterpret_cast<Pack<T>*>(base[b]) + i, v[b][u]);
+        }
+      }
+    }
+    done = packs * kPack;
+  }
+  // Remaining elements (a partial last pack, or the whole tile of a segment
+  // that cannot take vector accesses), one element per thread and access.
+  for (int64_t j = done + threadIdx.x; j < cnt; j += kThreads) {
+    T p = base[0][j * a.k.x.stride_t[0]];
+    const T g = g_src != nullptr ? g_src[j * g_stride] : zero;
+    T st[SS];
+    if (load_state) {
+#pragma unroll
+      for (int b = 0; b < NS; ++b) st[b] = base[2 + b][j * a.k.x.stride_t[2 + b]];
+    }
+    apply_element<P>(p, g, st, load_state, rep, a.k.maximize);
+    base[0][j * a.k.x.stride_t[0]] = p;
+    if (store_grad) {
+      g_dst[j * a.k.x.stride_t[1]] = g;
+    }
+#pragma unroll
+    for (int b = 0; b < NS; ++b) base[2 + b][j * a.k.x.stride_t[2 + b]] = st[b];
+  }
+}
+
+// Plain gradient scatter: copies every segment into its columns of the (R, T)
+// destination, every row (frozen replicas included, as a copy would).
+template <typename T>
+struct ScatterArgs {
+  T* dst;
+  int64_t dst_stride_r;
+  Segments<T> seg;
+};
+
+template <typename T>
+__global__ __launch_bounds__(kThreads) void scatter_kernel(ScatterArgs<T> a) {
+  const uint32_t tiles_per_row = a.seg.tile0[a.seg.n];
+  const uint32_t r = blockIdx.x / tiles_per_row;
+  const uint32_t local = blockIdx.x - r * tiles_per_row;
+  const int s = segment_of_tile(a.seg.tile0, a.seg.n, local);
+  const int64_t j0 = int64_t(local - a.seg.tile0[s]) * kTile;
+  const int64_t cnt = min(kTile, a.seg.numel[s] - j0);
+  const T* src = a.seg.data[s] + int64_t(r) * a.seg.stride_r[s] + j0;
+  T* dst = a.dst + int64_t(r) * a.dst_stride_r + a.seg.col[s] + j0;
+  int64_t done = 0;
+  if ((a.seg.vec_ok >> s) & 1u) {
+    const int64_t packs = cnt / kPack;
+    Pack<T> v[kUnroll];
+#pragma unroll
+    for (int u = 0; u < kUnroll; ++u) {
+      const int64_t i = int64_t(u) * kThreads + threadIdx.x;
+      if (i < packs) v[u] = load_stream(reinterpret_cast<const Pack<T>*>(src) + i);
+    }
+#pragma unroll
+    for (int u = 0; u < kUnroll; ++u) {
+      const int64_t i = int64_t(u) * kThreads + threadIdx.x;
+      if (i < packs) store_stream(reinterpret_cast<Pack<T>*>(dst) + i, v[u]);
+    }
+    done = packs * kPack;
+  }
+  for (int64_t j = done + threadIdx.x; j < cnt; j += kThreads) {
+    dst[j] = src[j];
+  }
 }
 
 // ---------------------------------------------------------------------------
@@ -104,424 +569,20 @@ __global__ __launch_bounds__(kThreads) void bump_steps_kernel(
 }
 
 // ---------------------------------------------------------------------------
-// Adam / AdamW
-// ---------------------------------------------------------------------------
-template <typename T>
-struct AdamArgs {
-  Operands<T> x;  // param, grad, exp_avg, exp_avg_sq, max_exp_avg_sq
-  const T* steps;
-  const T* lr;
-  const T* beta1;
-  const T* beta2;
-  const T* eps;
-  const T* weight_decay;
-  const uint8_t* mask;
-  Grid g;
-  bool maximize;
-};
-
-template <typename T>
-__device__ __forceinline__ bool adam_prologue(const AdamArgs<T>& a, uint32_t r,
-                                              AdamHyper& h, op_t<T>& bc1,
-                                              op_t<T>& bc2s) {
-  if (!a.mask[r]) {
-    return false;
-  }
-  h.lr = static_cast<double>(widen(a.lr[r]));
-  h.beta1 = static_cast<double>(widen(a.beta1[r]));
-  h.beta2 = static_cast<double>(widen(a.beta2[r]));
-  h.weight_decay = static_cast<double>(widen(a.weight_decay[r]));
-  h.eps = static_cast<double>(widen(a.eps[r]));
-  adam_bias_corrections<op_t<T>>(h.beta1, h.beta2,
-                                 static_cast<double>(widen(a.steps[r])), bc1,
-                                 bc2s);
-  return true;
-}
-
-template <typename T, bool ADAMW, bool AMSGRAD>
-__global__ __launch_bounds__(kThreads) void adam_stream_kernel(AdamArgs<T> a) {
-  using opmath_t = op_t<T>;
-  constexpr int NB = AMSGRAD ? 5 : 4;
-  uint32_t r;
-  int64_t t0;
-  tile_of_block(a.g, r, t0);
-  AdamHyper h;
-  opmath_t bc1, bc2s;
-  if (!adam_prologue(a, r, h, bc1, bc2s)) {
-    return;
-  }
-
-  Pack<T>* row[NB];
-#pragma unroll
-  for (int b = 0; b < NB; ++b) {
-    row[b] = reinterpret_cast<Pack<T>*>(a.x.data[b] + int64_t(r) * a.x.stride_r[b] + t0);
-  }
-  const int64_t packs_left = (a.g.T - t0) / kPack;
-
-  Pack<T> v[NB][kUnroll];
-#pragma unroll
-  for (int u = 0; u < kUnroll; ++u) {
-    const int64_t i = int64_t(u) * kThreads + threadIdx.x;
-    if (i < packs_left) {
-#pragma unroll
-      for (int b = 0; b < NB; ++b) {
-        v[b][u] = load_stream(row[b] + i);
-      }
-    }
-  }
-#pragma unroll
-  for (int u = 0; u < kUnroll; ++u) {
-    const int64_t i = int64_t(u) * kThreads + threadIdx.x;
-    if (i < packs_left) {
-#pragma unroll
-      for (int k = 0; k < kPack; ++k) {
-        opmath_t p = widen(v[0][u].v[k]);
-        opmath_t m = widen(v[2][u].v[k]);
-        opmath_t s = widen(v[3][u].v[k]);
-        opmath_t mx = AMSGRAD ? widen(v[NB - 1][u].v[k]) : opmath_t(0);
-        adam_element<opmath_t, ADAMW, AMSGRAD>(p, widen(v[1][u].v[k]), m, s, mx,
-                                               h, a.maximize, bc1, bc2s);
-        v[0][u].v[k] = narrow<T>(p);
-        v[2][u].v[k] = narrow<T>(m);
-        v[3][u].v[k] = narrow<T>(s);
-        if constexpr (AMSGRAD) {
-          v[NB - 1][u].v[k] = narrow<T>(mx);
-        }
-      }
-#pragma unroll
-      for (int b = 0; b < NB; ++b) {
-        if (b != 1) {
-          store_stream(row[b] + i, v[b][u]);
-        }
-      }
-    }
-  }
-}
-
-template <typename T, bool ADAMW, bool AMSGRAD>
-__global__ __launch_bounds__(kThreads) void adam_element_kernel(AdamArgs<T> a) {
-  using opmath_t = op_t<T>;
-  constexpr int NB = AMSGRAD ? 5 : 4;
-  constexpr int kPer = kPack * kUnroll;
-  uint32_t r;
-  int64_t t0;
-  tile_of_block(a.g, r, t0);
-  AdamHyper h;
-  opmath_t bc1, bc2s;
-  if (!adam_prologue(a, r, h, bc1, bc2s)) {
-    return;
-  }
-
-  T* base[NB];
-#pragma unroll
-  for (int b = 0; b < NB; ++b) {
-    base[b] = a.x.data[b] + int64_t(r) * a.x.stride_r[b];
-  }
-  T v[NB][kPer];
-#pragma unroll
-  for (int u = 0; u < kPer; ++u) {
-    const int64_t t = t0 + int64_t(u) * kThreads + threadIdx.x;
-    if (t < a.g.T) {
-#pragma unroll
-      for (int b = 0; b < NB; ++b) {
-        v[b][u] = base[b][t * a.x.stride_t[b]];
-      }
-    }
-  }
-#pragma unroll
-  for (int u = 0; u < kPer; ++u) {
-    const int64_t t = t0 + int64_t(u) * kThreads + threadIdx.x;
-    if (t < a.g.T) {
-      opmath_t p = widen(v[0][u]);
-      opmath_t m = widen(v[2][u]);
-      opmath_t s = widen(v[3][u]);
-      opmath_t mx = AMSGRAD ? widen(v[NB - 1][u]) : opmath_t(0);
-      adam_element<opmath_t, ADAMW, AMSGRAD>(p, widen(v[1][u]), m, s, mx, h,
-                                             a.maximize, bc1, bc2s);
-      base[0][t * a.x.stride_t[0]] = narrow<T>(p);
-      base[2][t * a.x.stride_t[2]] = narrow<T>(m);
-      base[3][t * a.x.stride_t[3]] = narrow<T>(s);
-      if constexpr (AMSGRAD) {
-        base[NB - 1][t * a.x.stride_t[NB - 1]] = narrow<T>(mx);
-      }
-    }
-  }
-}
-
-// ---------------------------------------------------------------------------
-// SGD. The hyperparameters are carried as double inside the element math, as
-// torch's ROCm `_fused_sgd_` takes them (checked on the MI355X: carrying them
-// as float instead changes params and buffers by up to a few ulp).
-// ---------------------------------------------------------------------------
-using sgd_hyper_t = double;
-
-template <typename T>
-struct SgdArgs {
-  Operands<T> x;  // param, grad, momentum_buffer
-  const T* steps;
-  const T* lr;
-  const T* momentum;
-  const T* dampening;
-  const T* weight_decay;
-  const uint8_t* mask;
-  Grid g;
-  bool maximize;
-};
-
-template <typename T>
-__device__ __forceinline__ bool sgd_prologue(const SgdArgs<T>& a, uint32_t r,
-                                             SgdHyper<sgd_hyper_t>& h,
-                                             bool& is_first_step) {
-  if (!a.mask[r]) {
-    return false;
-  }
-  h.lr = static_cast<sgd_hyper_t>(widen(a.lr[r]));
-  h.momentum = static_cast<sgd_hyper_t>(widen(a.momentum[r]));
-  h.dampening = static_cast<sgd_hyper_t>(widen(a.dampening[r]));
-  h.weight_decay = static_cast<sgd_hyper_t>(widen(a.weight_decay[r]));
-  is_first_step = widen(a.steps[r]) == op_t<T>(1);
-  return true;
-}
-
-template <typename T, bool HAS_BUF, bool NESTEROV>
-__global__ __launch_bounds__(kThreads) void sgd_stream_kernel(SgdArgs<T> a) {
-  using opmath_t = op_t<T>;
-  constexpr int NB = HAS_BUF ? 3 : 2;
-  uint32_t r;
-  int64_t t0;
-  tile_of_block(a.g, r, t0);
-  SgdHyper<sgd_hyper_t> h;
-  bool first;
-  if (!sgd_prologue(a, r, h, first)) {
-    return;
-  }
-
-  Pack<T>* row[NB];
-#pragma unroll
-  for (int b = 0; b < NB; ++b) {
-    row[b] = reinterpret_cast<Pack<T>*>(a.x.data[b] + int64_t(r) * a.x.stride_r[b] + t0);
-  }
-  const int64_t packs_left = (a.g.T - t0) / kPack;
-
-  Pack<T> v[NB][kUnroll];
-#pragma unroll
-  for (int u = 0; u < kUnroll; ++u) {
-    const int64_t i = int64_t(u) * kThreads + threadIdx.x;
-    if (i < packs_left) {
-      v[0][u] = load_stream(row[0] + i);
-      v[1][u] = load_stream(row[1] + i);
-      // On a replica's first step the buffer is overwritten by the gradient
-      // without being read, so it is not fetched.
-      if (HAS_BUF && !first) {
-        v[NB - 1][u] = load_stream(row[NB - 1] + i);
-      }
-    }
-  }
-#pragma unroll
-  for (int u = 0; u < kUnroll; ++u) {
-    const int64_t i = int64_t(u) * kThreads + threadIdx.x;
-    if (i < packs_left) {
-#pragma unroll
-      for (int k = 0; k < kPack; ++k) {
-        opmath_t p = widen(v[0][u].v[k]);
-        opmath_t mb = (HAS_BUF && !first) ? widen(v[NB - 1][u].v[k]) : opmath_t(0);
-        sgd_element<opmath_t, sgd_hyper_t, HAS_BUF, NESTEROV>(
-            p, widen(v[1][u].v[k]), mb, h, a.maximize, first);
-        v[0][u].v[k] = narrow<T>(p);
-        if constexpr (HAS_BUF) {
-          v[NB - 1][u].v[k] = narrow<T>(mb);
-        }
-      }
-      store_stream(row[0] + i, v[0][u]);
-      if constexpr (HAS_BUF) {
-        store_stream(row[NB - 1] + i, v[NB - 1][u]);
-      }
-    }
-  }
-}
-
-template <typename T, bool HAS_BUF, bool NESTEROV>
-__global__ __launch_bounds__(kThreads) void sgd_element_kernel(SgdArgs<T> a) {
-  using opmath_t = op_t<T>;
-  constexpr int NB = HAS_BUF ? 3 : 2;
-  constexpr int kPer = kPack * kUnroll;
-  uint32_t r;
-  int64_t t0;
-  tile_of_block(a.g, r, t0);
-  SgdHyper<sgd_hyper_t> h;
-  bool first;
-  if (!sgd_prologue(a, r, h, first)) {
-    return;
-  }
-
-  T* base[NB];
-#pragma unroll
-  for (int b = 0; b < NB; ++b) {
-    base[b] = a.x.data[b] + int64_t(r) * a.x.stride_r[b];
-  }
-  T v[NB][kPer];
-#pragma unroll
-  for (int u = 0; u < kPer; ++u) {
-    const int64_t t = t0 + int64_t(u) * kThreads + threadIdx.x;
-    if (t < a.g.T) {
-      v[0][u] = base[0][t * a.x.stride_t[0]];
-      v[1][u] = base[1][t * a.x.stride_t[1]];
-      if (HAS_BUF && !first) {
-        v[NB - 1][u] = base[NB - 1][t * a.x.stride_t[NB - 1]];
-      }
-    }
-  }
-#pragma unroll
-  for (int u = 0; u < kPer; ++u) {
-    const int64_t t = t0 + int64_t(u) * kThreads + threadIdx.x;
-    if (t < a.g.T) {
-      opmath_t p = widen(v[0][u]);
-      opmath_t mb = (HAS_BUF && !first) ? widen(v[NB - 1][u]) : opmath_t(0);
-      sgd_element<opmath_t, sgd_hyper_t, HAS_BUF, NESTEROV>(
-          p, widen(v[1][u]), mb, h, a.maximize, first);
-      base[0][t * a.x.stride_t[0]] = narrow<T>(p);
-      if constexpr (HAS_BUF) {
-        base[NB - 1][t * a.x.stride_t[NB - 1]] = narrow<T>(mb);
-      }
-    }
-  }
-}
-
-// ---------------------------------------------------------------------------
-// Adagrad
-// ---------------------------------------------------------------------------
-template <typename T>
-struct AdagradArgs {
-  Operands<T> x;  // param, grad, state_sum
-  const T* steps;
-  const T* lr;
-  const T* lr_decay;
-  const T* weight_decay;
-  const T* eps;
-  const uint8_t* mask;
-  Grid g;
-  bool maximize;
-};
-
-template <typename T>
-__device__ __forceinline__ bool adagrad_prologue(const AdagradArgs<T>& a,
-                                                 uint32_t r, AdagradHyper& h) {
-  if (!a.mask[r]) {
-    return false;
-  }
-  const double lr = static_cast<double>(widen(a.lr[r]));
-  const double lr_decay = static_cast<double>(widen(a.lr_decay[r]));
-  h.weight_decay = static_cast<double>(widen(a.weight_decay[r]));
-  h.eps = static_cast<double>(widen(a.eps[r]));
-  h.corrected_lr = adagrad_corrected_lr(
-      lr, lr_decay, static_cast<float>(widen(a.steps[r])));
-  return true;
-}
-
-template <typename T>
-__global__ __launch_bounds__(kThreads) void adagrad_stream_kernel(AdagradArgs<T> a) {
-  using opmath_t = op_t<T>;
-  constexpr int NB = 3;
-  uint32_t r;
-  int64_t t0;
-  tile_of_block(a.g, r, t0);
-  AdagradHyper h;
-  if (!adagrad_prologue(a, r, h)) {
-    return;
-  }
-
-  Pack<T>* row[NB];
-#pragma unroll
-  for (int b = 0; b < NB; ++b) {
-    row[b] = reinterpret_cast<Pack<T>*>(a.x.data[b] + int64_t(r) * a.x.stride_r[b] + t0);
-  }
-  const int64_t packs_left = (a.g.T - t0) / kPack;
-
-  Pack<T> v[NB][kUnroll];
-#pragma unroll
-  for (int u = 0; u < kUnroll; ++u) {
-    const int64_t i = int64_t(u) * kThreads + threadIdx.x;
-    if (i < packs_left) {
-#pragma unroll
-      for (int b = 0; b < NB; ++b) {
-        v[b][u] = load_stream(row[b] + i);
-      }
-    }
-  }
-#pragma unroll
-  for (int u = 0; u < kUnroll; ++u) {
-    const int64_t i = int64_t(u) * kThreads + threadIdx.x;
-    if (i < packs_left) {
-#pragma unroll
-      for (int k = 0; k < kPack; ++k) {
-        opmath_t p = widen(v[0][u].v[k]);
-        opmath_t s = widen(v[2][u].v[k]);
-        adagrad_element<opmath_t>(p, widen(v[1][u].v[k]), s, h, a.maximize);
-        v[0][u].v[k] = narrow<T>(p);
-        v[2][u].v[k] = narrow<T>(s);
-      }
-      store_stream(row[0] + i, v[0][u]);
-      store_stream(row[2] + i, v[2][u]);
-    }
-  }
-}
-
-template <typename T>
-__global__ __launch_bounds__(kThreads) void adagrad_element_kernel(AdagradArgs<T> a) {
-  using opmath_t = op_t<T>;
-  constexpr int NB = 3;
-  constexpr int kPer = kPack * kUnroll;
-  uint32_t r;
-  int64_t t0;
-  tile_of_block(a.g, r, t0);
-  AdagradHyper h;
-  if (!adagrad_prologue(a, r, h)) {
-    return;
-  }
-
-  T* base[NB];
-#pragma unroll
-  for (int b = 0; b < NB; ++b) {
-    base[b] = a.x.data[b] + int64_t(r) * a.x.stride_r[b];
-  }
-  T v[NB][kPer];
-#pragma unroll
-  for (int u = 0; u < kPer; ++u) {
-    const int64_t t = t0 + int64_t(u) * kThreads + threadIdx.x;
-    if (t < a.g.T) {
-#pragma unroll
-      for (int b = 0; b < NB; ++b) {
-        v[b][u] = base[b][t * a.x.stride_t[b]];
-      }
-    }
-  }
-#pragma unroll
-  for (int u = 0; u < kPer; ++u) {
-    const int64_t t = t0 + int64_t(u) * kThreads + threadIdx.x;
-    if (t < a.g.T) {
-      opmath_t p = widen(v[0][u]);
-      opmath_t s = widen(v[2][u]);
-      adagrad_element<opmath_t>(p, widen(v[1][u]), s, h, a.maximize);
-      base[0][t * a.x.stride_t[0]] = narrow<T>(p);
-      base[2][t * a.x.stride_t[2]] = narrow<T>(s);
-    }
-  }
-}
-
-// ---------------------------------------------------------------------------
 // Host side
 // ---------------------------------------------------------------------------
 constexpr int kInvalid = static_cast<int>(hipErrorInvalidValue);
 
 template <typename T>
-bool fill_operands(const ts_rt_buf* bufs, int n, Operands<T>& x) {
-  for (int b = 0; b < 5; ++b) {
+bool fill_operands(const ts_rt_buf* bufs, int n, Operands<T>& x, bool grad_optional) {
+  for (int b = 0; b < kMaxOperands; ++b) {
     x.data[b] = nullptr;
     x.stride_r[b] = 0;
     x.stride_t[b] = 1;
   }
   for (int b = 0; b < n; ++b) {
     if (bufs[b].data == nullptr) {
+      if (b == 1 && grad_optional) continue;
       return false;
     }
     x.data[b] = static_cast<T*>(bufs[b].data);
@@ -531,14 +592,12 @@ bool fill_operands(const ts_rt_buf* bufs, int n, Operands<T>& x) {
   return true;
 }
 
-// The 16-byte path needs every operand to have unit inner stride and every
-// row start aligned to one pack, and T to be whole packs.
+// The 16-byte path needs unit inner stride and pack-aligned row starts on
+// every (present) operand.
 template <typename T>
-bool streamable(const Operands<T>& x, int n, int64_t T_) {
-  if (T_ % kPack != 0) {
-    return false;
-  }
+bool rows_vectorizable(const Operands<T>& x, int n) {
   for (int b = 0; b < n; ++b) {
+    if (x.data[b] == nullptr) continue;
     if (x.stride_t[b] != 1 || x.stride_r[b] % kPack != 0 ||
         reinterpret_cast<uintptr_t>(x.data[b]) % (sizeof(T) * kPack) != 0) {
       return false;
@@ -571,165 +630,317 @@ int launch_bump(void* steps, const uint8_t* mask, int64_t R, void* out_zero,
   return static_cast<int>(hipGetLastError());
 }
 
-// Runs the optional bump, then `launch` when there is any work.
-// Empty tensors may carry null data pointers, so operands are only required
-// where they are dereferenced: steps and mask when R > 0, the rest (checked
-// inside `launch`) when there is at least one element.
-template <typename T, typename Launch>
-int run_step(void* steps, const uint8_t* mask, int64_t R, int64_t T_,
-             uint32_t flags, void* out_zero, hipStream_t stream,
-             Launch&& launch) {
-  if (R < 0 || T_ < 0 || (R > 0 && (steps == nullptr || mask == nullptr))) {
+// A caller's segment table: in column order, disjoint, inside [0, cols), with
+// data for every non-empty segment (two tiles writing one column would race).
+// One pass, no allocation.
+bool segments_valid(const ts_segment* segs, int n, int64_t cols) {
+  int64_t end = 0;
+  for (int i = 0; i < n; ++i) {
+    const ts_segment& s = segs[i];
+    if (s.numel < 0 || s.col < 0 || s.col > cols - s.numel) return false;
+    if (s.numel == 0) continue;
+    if (s.data == nullptr || s.col < end) return false;
+    end = s.col + s.numel;
+  }
+  return true;
+}
+
+// Walks a valid table in column order, skipping empty segments. With `gaps`,
+// the column ranges no segment covers (between segments and after the last
+// one, up to `cols`) come out as entries without data.
+struct SegmentWalk {
+  const ts_segment* segs;
+  int n;
+  int64_t cols;
+  bool gaps;
+  int i = 0;
+  int64_t at = 0;
+
+  bool next(ts_segment& out) {
+    while (i < n && segs[i].numel == 0) ++i;
+    const int64_t stop = i < n ? segs[i].col : cols;
+    if (gaps && at < stop) {
+      out = ts_segment{nullptr, 0, at, stop - at};
+      at = stop;
+      return true;
+    }
+    if (i == n) return false;
+    out = segs[i++];
+    at = out.col + out.numel;
+    return true;
+  }
+};
+
+// Fills the next launch's table, up to kMaxSegments entries, from the walk;
+// returns the grid size (0 when the walk is done, -1 when it exceeds the 1-D
+// grid). `vec_rows` says whether the (R, T) operands allow vector access.
+template <typename T>
+int64_t next_chunk(SegmentWalk& w, int64_t R, bool vec_rows, Segments<T>& out) {
+  out.n = 0;
+  out.vec_ok = 0;
+  uint64_t tiles = 0;
+  ts_segment s;
+  while (out.n < kMaxSegments && w.next(s)) {
+    const int k = out.n++;
+    out.data[k] = static_cast<const T*>(s.data);
+    out.stride_r[k] = s.stride_r;
+    out.col[k] = s.col;
+    out.numel[k] = s.numel;
+    out.tile0[k] = static_cast<uint32_t>(tiles);
+    tiles += static_cast<uint64_t>((s.numel + kTile - 1) / kTile);
+    if (tiles > UINT32_MAX) return -1;
+    const bool ok = vec_rows && s.col % kPack == 0 && s.stride_r % kPack == 0 &&
+                    reinterpret_cast<uintptr_t>(s.data) % (sizeof(T) * kPack) == 0;
+    out.vec_ok |= (ok ? uint64_t(1) : uint64_t(0)) << k;
+  }
+  out.tile0[out.n] = static_cast<uint32_t>(tiles);
+  const uint64_t blocks = tiles * static_cast<uint64_t>(R);
+  return blocks > INT32_MAX ? -1 : static_cast<int64_t>(blocks);
+}
+
+// Checks that every launch of a walk fits the grid, without launching.
+template <typename T>
+bool walk_fits(SegmentWalk w, int64_t R, bool vec_rows, Segments<T>& scratch) {
+  int64_t blocks;
+  while ((blocks = next_chunk<T>(w, R, vec_rows, scratch)) != 0 || scratch.n > 0) {
+    if (blocks < 0) return false;
+  }
+  return true;
+}
+
+// Launches `kernel` once per chunk of the walk.
+template <typename T, typename Args, typename Kernel>
+int launch_walk(SegmentWalk w, int64_t R, bool vec_rows, Args& a, Segments<T>& seg,
+                Kernel kernel, hipStream_t stream) {
+  int64_t blocks;
+  while ((blocks = next_chunk<T>(w, R, vec_rows, seg)) != 0 || seg.n > 0) {
+    if (blocks < 0) return kInvalid;
+    if (blocks == 0) continue;
+    hipLaunchKernelGGL(kernel, dim3(static_cast<uint32_t>(blocks)), dim3(kThreads), 0, stream,
+                       a);
+    const int err = static_cast<int>(hipGetLastError());
+    if (err != 0) return err;
+  }
+  return 0;
+}
+
+// A call: the (R, T) operand table, the (R,) vectors and the flags.
+struct Call {
+  const ts_rt_buf* bufs;
+  void* steps;
+  const void* h[5];
+  int nh;
+  const uint8_t* mask;
+  int64_t R, T;
+  uint32_t flags;
+  void* out_zero;
+  hipStream_t stream;
+};
+
+template <typename P>
+bool fill_kargs(const Call& c, int nbufs, KArgs<P>& a, bool grad_optional) {
+  using T = typename P::T;
+  if (!fill_operands<T>(c.bufs, nbufs, a.x, grad_optional)) return false;
+  a.vec.steps = static_cast<const T*>(c.steps);
+  for (int i = 0; i < 5; ++i) {
+    a.vec.h[i] = i < c.nh ? static_cast<const T*>(c.h[i]) : nullptr;
+    if (i < c.nh && c.h[i] == nullptr) return false;
+  }
+  a.vec.mask = c.mask;
+  a.maximize = (c.flags & TS_MAXIMIZE) != 0;
+  return true;
+}
+
+// Validation, then the optional bump (which also writes the zero result),
+// then `launch` when there is any work. Every check happens before the first
+// enqueue, so an invalid call changes nothing. Empty tensors may carry null
+// data pointers, so operands are only required where they are dereferenced:
+// steps and mask when R > 0, the rest (checked by `prepare`, which also fills
+// the kernel arguments) when there is at least one element.
+template <typename T, typename Prepare, typename Launch>
+int run_step(const Call& c, Prepare&& prepare, Launch&& launch) {
+  if (c.bufs == nullptr || c.R < 0 || c.T < 0 ||
+      (c.R > 0 && (c.steps == nullptr || c.mask == nullptr))) {
     return kInvalid;
   }
-  if ((flags & TS_BUMP_STEPS) != 0 || out_zero != nullptr) {
-    if ((flags & TS_BUMP_STEPS) != 0 && R > 0) {
-      const int err = launch_bump<T>(steps, mask, R, out_zero, stream);
-      if (err != 0) {
-        return err;
-      }
-    } else if (out_zero != nullptr) {
-      const int err = launch_bump<T>(steps, mask, 0, out_zero, stream);
-      if (err != 0) {
-        return err;
-      }
-    }
+  const bool work = c.R > 0 && c.T > 0;
+  if (work && !prepare()) {
+    return kInvalid;
   }
-  if (R == 0 || T_ == 0) {
+  if ((c.flags & TS_BUMP_STEPS) != 0 && c.R > 0) {
+    const int err = launch_bump<T>(c.steps, c.mask, c.R, c.out_zero, c.stream);
+    if (err != 0) return err;
+  } else if (c.out_zero != nullptr) {
+    const int err = launch_bump<T>(c.steps, c.mask, 0, c.out_zero, c.stream);
+    if (err != 0) return err;
+  }
+  if (!work) {
     return 0;
   }
   return launch();
 }
 
-template <typename T>
-int adam_typed(const ts_rt_buf* bufs, void* steps, const void* lr,
-               const void* beta1, const void* beta2, const void* eps,
-               const void* wd, const uint8_t* mask, int64_t R, int64_t T_,
-               uint32_t flags, void* out_zero, hipStream_t stream) {
+// Consolidated-gradient update with policy P over `nbufs` operands.
+template <typename P>
+int launch_dense(const Call& c, int nbufs) {
+  using T = typename P::T;
+  KArgs<P> a;
+  uint32_t blocks = 0;
+  const auto prepare = [&] {
+    return fill_kargs<P>(c, nbufs, a, false) && make_grid(c.R, c.T, a.g, blocks);
+  };
+  return run_step<T>(c, prepare, [&]() -> int {
+    const dim3 grid(blocks), block(kThreads);
+    if (c.T % kPack == 0 && rows_vectorizable(a.x, nbufs)) {
+      hipLaunchKernelGGL(stream_kernel<P>, grid, block, 0, c.stream, a);
+    } else {
+      hipLaunchKernelGGL(element_kernel<P>, grid, block, 0, c.stream, a);
+    }
+    return static_cast<int>(hipGetLastError());
+  });
+}
+
+// Segmented-gradient update with policy P: one launch per kMaxSegments
+// entries of the walk (their columns are disjoint, so the launches are
+// independent). The gaps make the result that of a scatter followed by the
+// consolidated update in every column.
+template <typename P>
+int launch_segments(const Call& c, int nbufs, const ts_segment* segs, int n_segs) {
+  using T = typename P::T;
+  if (n_segs < 0 || (n_segs > 0 && segs == nullptr)) return kInvalid;
+  SegArgs<P> a;
+  bool vec_rows = false;
+  const SegmentWalk walk{segs, n_segs, c.T, true};
+  const auto prepare = [&] {
+    if (!fill_kargs<P>(c, nbufs, a.k, true) || !segments_valid(segs, n_segs, c.T)) {
+      return false;
+    }
+    vec_rows = rows_vectorizable(a.k.x, nbufs);
+    return walk_fits<T>(walk, c.R, vec_rows, a.seg);
+  };
+  return run_step<T>(c, prepare, [&]() -> int {
+    return launch_walk<T>(walk, c.R, vec_rows, a, a.seg, segment_kernel<P>, c.stream);
+  });
+}
+
+// Runs `launch` with the policy that matches the call's flags and the number
+// of (R, T) operands that policy reads.
+template <typename T, typename Launch>
+int adam_dispatch(uint32_t flags, Launch&& launch) {
   const bool amsgrad = (flags & TS_AMSGRAD) != 0;
   const bool adamw = (flags & TS_ADAMW) != 0;
-  if (bufs == nullptr) {
-    return kInvalid;
+  if (adamw) {
+    if (amsgrad) return launch(AdamPolicy<T, true, true>{}, 5);
+    return launch(AdamPolicy<T, true, false>{}, 4);
   }
-  const bool work = R > 0 && T_ > 0;
-  AdamArgs<T> a;
-  if (work && (lr == nullptr || beta1 == nullptr || beta2 == nullptr || eps == nullptr ||
-               wd == nullptr || !fill_operands<T>(bufs, amsgrad ? 5 : 4, a.x))) {
-    return kInvalid;
-  }
-  a.steps = static_cast<const T*>(steps);
-  a.lr = static_cast<const T*>(lr);
-  a.beta1 = static_cast<const T*>(beta1);
-  a.beta2 = static_cast<const T*>(beta2);
-  a.eps = static_cast<const T*>(eps);
-  a.weight_decay = static_cast<const T*>(wd);
-  a.mask = mask;
-  a.maximize = (flags & TS_MAXIMIZE) != 0;
-  return run_step<T>(steps, mask, R, T_, flags, out_zero, stream, [&]() -> int {
-    uint32_t blocks;
-    if (!make_grid(R, T_, a.g, blocks)) {
-      return kInvalid;
-    }
-    const bool stream_path = streamable(a.x, amsgrad ? 5 : 4, T_);
-    const dim3 grid(blocks), block(kThreads);
-#define CHURTEN_ADAM(W, A)                                                     \
-  if (stream_path)                                                             \
-    hipLaunchKernelGGL((adam_stream_kernel<T, W, A>), grid, block, 0, stream, a); \
-  else                                                                         \
-    hipLaunchKernelGGL((adam_element_kernel<T, W, A>), grid, block, 0, stream, a);
-    if (adamw) {
-      if (amsgrad) { CHURTEN_ADAM(true, true) } else { CHURTEN_ADAM(true, false) }
-    } else {
-      if (amsgrad) { CHURTEN_ADAM(false, true) } else { CHURTEN_ADAM(false, false) }
-    }
-#undef CHURTEN_ADAM
-    return static_cast<int>(hipGetLastError());
-  });
+  if (amsgrad) return launch(AdamPolicy<T, false, true>{}, 5);
+  return launch(AdamPolicy<T, false, false>{}, 4);
 }
 
-template <typename T>
-int sgd_typed(const ts_rt_buf* bufs, void* steps, const void* lr,
-              const void* momentum, const void* dampening, const void* wd,
-              const uint8_t* mask, int64_t R, int64_t T_, uint32_t flags,
-              void* out_zero, hipStream_t stream) {
-  if (bufs == nullptr) {
-    return kInvalid;
-  }
-  const bool work = R > 0 && T_ > 0;
-  // bufs[2].data == NULL selects the buffer-less (depth-2) form.
-  const bool has_buf = bufs[2].data != nullptr;
+template <typename T, typename Launch>
+int sgd_dispatch(uint32_t flags, bool has_buf, Launch&& launch) {
   const bool nesterov = (flags & TS_NESTEROV) != 0;
-  if (work && nesterov && !has_buf) {
-    return kInvalid;
+  if (has_buf) {
+    if (nesterov) return launch(SgdPolicy<T, true, true>{}, 3);
+    return launch(SgdPolicy<T, true, false>{}, 3);
   }
-  SgdArgs<T> a;
-  if (work && (lr == nullptr || momentum == nullptr || dampening == nullptr ||
-               wd == nullptr || !fill_operands<T>(bufs, has_buf ? 3 : 2, a.x))) {
-    return kInvalid;
+  if (nesterov) return kInvalid;
+  return launch(SgdPolicy<T, false, false>{}, 2);
+}
+
+template <typename T, typename Launch>
+int adagrad_dispatch(Launch&& launch) {
+  return launch(AdagradPolicy<T>{}, 3);
+}
+
+template <template <typename> class Body, typename... Args>
+int by_dtype(ts_dtype dtype, Args&&... args) {
+  switch (dtype) {
+    case TS_FLOAT32: return Body<float>::run(args...);
+    case TS_FLOAT64: return Body<double>::run(args...);
+    case TS_FLOAT16: return Body<_Float16>::run(args...);
+    case TS_BFLOAT16: return Body<bf16_t>::run(args...);
   }
-  a.steps = static_cast<const T*>(steps);
-  a.lr = static_cast<const T*>(lr);
-  a.momentum = static_cast<const T*>(momentum);
-  a.dampening = static_cast<const T*>(dampening);
-  a.weight_decay = static_cast<const T*>(wd);
-  a.mask = mask;
-  a.maximize = (flags & TS_MAXIMIZE) != 0;
-  return run_step<T>(steps, mask, R, T_, flags, out_zero, stream, [&]() -> int {
-    uint32_t blocks;
-    if (!make_grid(R, T_, a.g, blocks)) {
-      return kInvalid;
-    }
-    const bool stream_path = streamable(a.x, has_buf ? 3 : 2, T_);
-    const dim3 grid(blocks), block(kThreads);
-#define CHURTEN_SGD(B, N)                                                      \
-  if (stream_path)                                                             \
-    hipLaunchKernelGGL((sgd_stream_kernel<T, B, N>), grid, block, 0, stream, a); \
-  else                                                                         \
-    hipLaunchKernelGGL((sgd_element_kernel<T, B, N>), grid, block, 0, stream, a);
-    if (has_buf) {
-      if (nesterov) { CHURTEN_SGD(true, true) } else { CHURTEN_SGD(true, false) }
-    } else {
-      CHURTEN_SGD(false, false)
-    }
-#undef CHURTEN_SGD
-    return static_cast<int>(hipGetLastError());
-  });
+  return kInvalid;
+}
+
+template <typename P>
+int launch_any(const Call& c, int nbufs, const ts_segment* segs, int n_segs, bool segmented) {
+  return segmented ? launch_segments<P>(c, nbufs, segs, n_segs) : launch_dense<P>(c, nbufs);
 }
 
 template <typename T>
-int adagrad_typed(const ts_rt_buf* bufs, void* steps, const void* lr,
-                  const void* lr_decay, const void* wd, const void* eps,
-                  const uint8_t* mask, int64_t R, int64_t T_, uint32_t flags,
-                  void* out_zero, hipStream_t stream) {
-  if (bufs == nullptr) {
-    return kInvalid;
+struct AdamBody {
+  static int run(const Call& c, const ts_segment* segs, int n_segs, bool segmented) {
+    return adam_dispatch<T>(c.flags, [&](auto policy, int nbufs) {
+      return launch_any<decltype(policy)>(c, nbufs, segs, n_segs, segmented);
+    });
   }
-  const bool work = R > 0 && T_ > 0;
-  AdagradArgs<T> a;
-  if (work && (lr == nullptr || lr_decay == nullptr || wd == nullptr || eps == nullptr ||
-               !fill_operands<T>(bufs, 3, a.x))) {
-    return kInvalid;
+};
+
+template <typename T>
+struct SgdBody {
+  static int run(const Call& c, const ts_segment* segs, int n_segs, bool segmented) {
+    const bool has_buf = c.bufs != nullptr && c.bufs[2].data != nullptr;
+    return sgd_dispatch<T>(c.flags, has_buf, [&](auto policy, int nbufs) {
+      return launch_any<decltype(policy)>(c, nbufs, segs, n_segs, segmented);
+    });
   }
-  a.steps = static_cast<const T*>(steps);
-  a.lr = static_cast<const T*>(lr);
-  a.lr_decay = static_cast<const T*>(lr_decay);
-  a.weight_decay = static_cast<const T*>(wd);
-  a.eps = static_cast<const T*>(eps);
-  a.mask = mask;
-  a.maximize = (flags & TS_MAXIMIZE) != 0;
-  return run_step<T>(steps, mask, R, T_, flags, out_zero, stream, [&]() -> int {
-    uint32_t blocks;
-    if (!make_grid(R, T_, a.g, blocks)) {
-      return kInvalid;
-    }
-    const dim3 grid(blocks), block(kThreads);
-    if (streamable(a.x, 3, T_)) {
-      hipLaunchKernelGGL(adagrad_stream_kernel<T>, grid, block, 0, stream, a);
-    } else {
-      hipLaunchKernelGGL(adagrad_element_kernel<T>, grid, block, 0, stream, a);
-    }
-    return static_cast<int>(hipGetLastError());
-  });
+};
+
+template <typename T>
+struct AdagradBody {
+  static int run(const Call& c, const ts_segment* segs, int n_segs, bool segmented) {
+    return adagrad_dispatch<T>([&](auto policy, int nbufs) {
+      return launch_any<decltype(policy)>(c, nbufs, segs, n_segs, segmented);
+    });
+  }
+};
+
+template <typename T>
+struct ScatterBody {
+  static int run(const ts_segment* segs, int n_segs, void* dst, int64_t dst_stride_r,
+                 int64_t cols, int64_t R, hipStream_t stream) {
+    if (R < 0 || cols < 0 || n_segs < 0 || (n_segs > 0 && segs == nullptr)) return kInvalid;
+    if (!segments_valid(segs, n_segs, cols)) return kInvalid;
+    if (R == 0) return 0;
+    ScatterArgs<T> a;
+    a.dst = static_cast<T*>(dst);
+    a.dst_stride_r = dst_stride_r;
+    const bool vec_rows = dst_stride_r % kPack == 0 &&
+                          reinterpret_cast<uintptr_t>(dst) % (sizeof(T) * kPack) == 0;
+    const SegmentWalk walk{segs, n_segs, cols, false};
+    const bool any = std::any_of(segs, segs + n_segs, [](const ts_segment& s) {
+      return s.numel > 0;
+    });
+    if ((any && dst == nullptr) || !walk_fits<T>(walk, R, vec_rows, a.seg)) return kInvalid;
+    return launch_walk<T>(walk, R, vec_rows, a, a.seg, scatter_kernel<T>, stream);
+  }
+};
+
+template <typename T>
+struct BumpBody {
+  static int run(void* steps, const uint8_t* mask, int64_t R, void* out_zero,
+                 hipStream_t stream) {
+    return launch_bump<T>(steps, mask, R, out_zero, stream);
+  }
+};
+
+Call make_call(const ts_rt_buf* bufs, void* steps, std::initializer_list<const void*> h,
+               const uint8_t* mask, int64_t R, int64_t T, uint32_t flags, void* out_zero,
+               void* stream) {
+  Call c;
+  c.bufs = bufs;
+  c.steps = steps;
+  c.nh = 0;
+  for (const void* p : h) c.h[c.nh++] = p;
+  c.mask = mask;
+  c.R = R;
+  c.T = T;
+  c.flags = flags;
+  c.out_zero = out_zero;
+  c.stream = static_cast<hipStream_t>(stream);
+  return c;
 }
 
 }  // namespace
@@ -738,24 +949,20 @@ int adagrad_typed(const ts_rt_buf* bufs, void* steps, const void* lr,
 // ---------------------------------------------------------------------------
 // C ABI
 // ---------------------------------------------------------------------------
+using churten::by_dtype;
+using churten::make_call;
+
 extern "C" {
 
-int ts_version(void) { return 100; }
+int ts_version(void) { return 110; }
 
 int ts_bump_steps(ts_dtype dtype, void* state_steps, const uint8_t* active_mask,
                   int64_t R, void* out_zero, void* stream) {
-  using namespace churten;
   if (R < 0 || (R > 0 && (state_steps == nullptr || active_mask == nullptr))) {
-    return kInvalid;
+    return churten::kInvalid;
   }
-  auto s = static_cast<hipStream_t>(stream);
-  switch (dtype) {
-    case TS_FLOAT32: return launch_bump<float>(state_steps, active_mask, R, out_zero, s);
-    case TS_FLOAT64: return launch_bump<double>(state_steps, active_mask, R, out_zero, s);
-    case TS_FLOAT16: return launch_bump<_Float16>(state_steps, active_mask, R, out_zero, s);
-    case TS_BFLOAT16: return launch_bump<bf16_t>(state_steps, active_mask, R, out_zero, s);
-  }
-  return kInvalid;
+  return by_dtype<churten::BumpBody>(dtype, state_steps, active_mask, R, out_zero,
+                                     static_cast<hipStream_t>(stream));
 }
 
 int ts_adam_step(const ts_rt_buf* bufs, ts_dtype dtype, void* state_steps,
@@ -763,18 +970,9 @@ int ts_adam_step(const ts_rt_buf* bufs, ts_dtype dtype, void* state_steps,
                  const void* eps, const void* weight_decay,
                  const uint8_t* active_mask, int64_t R, int64_t T,
                  uint32_t flags, void* out_zero, void* stream) {
-  using namespace churten;
-  auto s = static_cast<hipStream_t>(stream);
-#define CHURTEN_CALL(TY) \
-  adam_typed<TY>(bufs, state_steps, lr, beta1, beta2, eps, weight_decay, active_mask, R, T, flags, out_zero, s)
-  switch (dtype) {
-    case TS_FLOAT32: return CHURTEN_CALL(float);
-    case TS_FLOAT64: return CHURTEN_CALL(double);
-    case TS_FLOAT16: return CHURTEN_CALL(_Float16);
-    case TS_BFLOAT16: return CHURTEN_CALL(bf16_t);
-  }
-#undef CHURTEN_CALL
-  return kInvalid;
+  const auto c = make_call(bufs, state_steps, {lr, beta1, beta2, eps, weight_decay},
+                           active_mask, R, T, flags, out_zero, stream);
+  return by_dtype<churten::AdamBody>(dtype, c, nullptr, 0, false);
 }
 
 int ts_sgd_step(const ts_rt_buf* bufs, ts_dtype dtype, void* state_steps,
@@ -782,18 +980,9 @@ int ts_sgd_step(const ts_rt_buf* bufs, ts_dtype dtype, void* state_steps,
                 const void* weight_decay, const uint8_t* active_mask,
                 int64_t R, int64_t T, uint32_t flags, void* out_zero,
                 void* stream) {
-  using namespace churten;
-  auto s = static_cast<hipStream_t>(stream);
-#define CHURTEN_CALL(TY) \
-  sgd_typed<TY>(bufs, state_steps, lr, momentum, dampening, weight_decay, active_mask, R, T, flags, out_zero, s)
-  switch (dtype) {
-    case TS_FLOAT32: return CHURTEN_CALL(float);
-    case TS_FLOAT64: return CHURTEN_CALL(double);
-    case TS_FLOAT16: return CHURTEN_CALL(_Float16);
-    case TS_BFLOAT16: return CHURTEN_CALL(bf16_t);
-  }
-#undef CHURTEN_CALL
-  return kInvalid;
+  const auto c = make_call(bufs, state_steps, {lr, momentum, dampening, weight_decay},
+                           active_mask, R, T, flags, out_zero, stream);
+  return by_dtype<churten::SgdBody>(dtype, c, nullptr, 0, false);
 }
 
 int ts_adagrad_step(const ts_rt_buf* bufs, ts_dtype dtype, void* state_steps,
@@ -801,18 +990,47 @@ int ts_adagrad_step(const ts_rt_buf* bufs, ts_dtype dtype, void* state_steps,
                     const void* weight_decay, const void* eps,
                     const uint8_t* active_mask, int64_t R, int64_t T,
                     uint32_t flags, void* out_zero, void* stream) {
-  using namespace churten;
-  auto s = static_cast<hipStream_t>(stream);
-#define CHURTEN_CALL(TY) \
-  adagrad_typed<TY>(bufs, state_steps, lr, lr_decay, weight_decay, eps, active_mask, R, T, flags, out_zero, s)
-  switch (dtype) {
-    case TS_FLOAT32: return CHURTEN_CALL(float);
-    case TS_FLOAT64: return CHURTEN_CALL(double);
-    case TS_FLOAT16: return CHURTEN_CALL(_Float16);
-    case TS_BFLOAT16: return CHURTEN_CALL(bf16_t);
-  }
-#undef CHURTEN_CALL
-  return kInvalid;
+  const auto c = make_call(bufs, state_steps, {lr, lr_decay, weight_decay, eps},
+                           active_mask, R, T, flags, out_zero, stream);
+  return by_dtype<churten::AdagradBody>(dtype, c, nullptr, 0, false);
+}
+
+int ts_adam_step_segments(const ts_rt_buf* bufs, const ts_segment* grads, int n_grads,
+                          ts_dtype dtype, void* state_steps, const void* lr,
+                          const void* beta1, const void* beta2, const void* eps,
+                          const void* weight_decay, const uint8_t* active_mask,
+                          int64_t R, int64_t T, uint32_t flags, void* out_zero,
+                          void* stream) {
+  const auto c = make_call(bufs, state_steps, {lr, beta1, beta2, eps, weight_decay},
+                           active_mask, R, T, flags, out_zero, stream);
+  return by_dtype<churten::AdamBody>(dtype, c, grads, n_grads, true);
+}
+
+int ts_sgd_step_segments(const ts_rt_buf* bufs, const ts_segment* grads, int n_grads,
+                         ts_dtype dtype, void* state_steps, const void* lr,
+                         const void* momentum, const void* dampening,
+                         const void* weight_decay, const uint8_t* active_mask,
+                         int64_t R, int64_t T, uint32_t flags, void* out_zero,
+                         void* stream) {
+  const auto c = make_call(bufs, state_steps, {lr, momentum, dampening, weight_decay},
+                           active_mask, R, T, flags, out_zero, stream);
+  return by_dtype<churten::SgdBody>(dtype, c, grads, n_grads, true);
+}
+
+int ts_adagrad_step_segments(const ts_rt_buf* bufs, const ts_segment* grads, int n_grads,
+                             ts_dtype dtype, void* state_steps, const void* lr,
+                             const void* lr_decay, const void* weight_decay,
+                             const void* eps, const uint8_t* active_mask, int64_t R,
+                             int64_t T, uint32_t flags, void* out_zero, void* stream) {
+  const auto c = make_call(bufs, state_steps, {lr, lr_decay, weight_decay, eps},
+                           active_mask, R, T, flags, out_zero, stream);
+  return by_dtype<churten::AdagradBody>(dtype, c, grads, n_grads, true);
+}
+
+int ts_scatter_segments(const ts_segment* src, int n_src, ts_dtype dtype, void* dst,
+                        int64_t dst_stride_r, int64_t cols, int64_t R, void* stream) {
+  return by_dtype<churten::ScatterBody>(dtype, src, n_src, dst, dst_stride_r, cols, R,
+                                        static_cast<hipStream_t>(stream));
 }
 
 }  // extern "C"

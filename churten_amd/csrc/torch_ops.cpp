@@ -1,12 +1,20 @@
-// torch_ops.cpp -- the `torchstrap` operator library over the C ABI.
+// torch_ops.cpp -- the operator libraries over the C ABI.
 //
-// Declares the three operator schemas with the reference's exact text
+// `torchstrap`: the three operator schemas with the reference's exact text
 // (src/torchstrap/kernels/csrc/stubs.cpp:25-72), so code that calls
-// torch.ops.torchstrap.{adam,sgd,adagrad}_step_ is served unchanged, and
-// implements the GPU dispatch key by validating the tensors on the host and
-// calling the extern "C" launchers of include/churten_optim.h on the current
-// HIP stream. The module init function makes this file a drop-in for
-// `torchstrap.kernels._C` (stubs.cpp:75-85): importing it registers the ops.
+// torch.ops.torchstrap.{adam,sgd,adagrad}_step_ is served unchanged. The GPU
+// dispatch key validates the tensors on the host and calls the extern "C"
+// launchers of include/churten_optim.h on the current HIP stream. The module
+// init function makes this file a drop-in for `torchstrap.kernels._C`
+// (stubs.cpp:75-85): importing it registers the ops.
+//
+// `churten`: additions with no counterpart in the reference operator set, for
+// the gradient scatter that precedes every update
+// (src/torchstrap/optimizer/grad_transform.py:29): a one-launch scatter
+// (`scatter_grads_`) and the three updates reading per-parameter gradients
+// directly (`*_step_segments_`), optionally materialising the consolidated
+// gradient on the way. Their CPU keys compose the scatter with the CPU
+// kernels.
 //
 // Host-side behaviour kept from the reference operators:
 //   - params must be a 2-D (R, T) buffer; amsgrad needs max_exp_avg_sqs,
@@ -26,12 +34,16 @@
 #include <Python.h>
 
 #include <ATen/ATen.h>
+#include <ATen/core/dispatch/Dispatcher.h>
 #include <c10/core/DeviceGuard.h>
 #include <c10/hip/HIPStream.h>
 #include <torch/library.h>
 
+#include <algorithm>
+#include <numeric>
 #include <optional>
 #include <string>
+#include <vector>
 
 #include "../../include/churten_optim.h"
 
@@ -57,6 +69,8 @@ ts_dtype ts_dtype_of(at::ScalarType t, const char* op) {
 ts_rt_buf rt_buf(const at::Tensor& t) {
   return ts_rt_buf{t.data_ptr(), t.stride(0), t.stride(1)};
 }
+
+constexpr ts_rt_buf kNoBuf{nullptr, 0, 1};
 
 void check_params(const at::Tensor& params, const char* op) {
   TORCH_CHECK(params.dim() == 2, op, ": params must be a 2-D (R, T) buffer");
@@ -91,32 +105,6 @@ at::Tensor hyper(const at::Tensor& t, at::ScalarType dtype) {
   return t.reshape({t.numel()}).to(dtype).contiguous();
 }
 
-// Prepares state_steps and the mask. Returns the steps pointer the kernel
-// reads and adds TS_BUMP_STEPS to `flags` when the bump is left to the
-// launcher (same dtype, contiguous, bool mask).
-struct Steps {
-  at::Tensor steps;  // what the kernel reads (may alias state_steps)
-  at::Tensor mask;
-};
-
-Steps prepare_steps(at::Tensor& state_steps, const at::Tensor& active_mask,
-                    at::ScalarType dtype, uint32_t& flags) {
-  Steps s;
-  const bool fused = state_steps.scalar_type() == dtype &&
-                     state_steps.is_contiguous() &&
-                     active_mask.scalar_type() == at::kBool;
-  if (fused) {
-    s.mask = active_mask.reshape({active_mask.numel()}).contiguous();
-    s.steps = state_steps;
-    flags |= TS_BUMP_STEPS;
-  } else {
-    state_steps.add_(active_mask.to(state_steps.scalar_type()));
-    s.mask = active_mask.reshape({active_mask.numel()}).to(at::kBool).contiguous();
-    s.steps = hyper(state_steps, dtype);
-  }
-  return s;
-}
-
 void check_status(int status, const char* op) {
   TORCH_CHECK(status == 0, op, ": HIP launch failed with error ", status);
 }
@@ -125,142 +113,344 @@ hipStream_t current_stream(const at::Tensor& params) {
   return c10::hip::getCurrentHIPStream(params.device().index()).stream();
 }
 
+// Everything a launcher needs besides the (R, T) operand table: the step
+// counter (bumped by the launcher when TS_BUMP_STEPS is set), the mask, the
+// normalised hyperparameter vectors and the fresh zero result.
+struct Prepared {
+  ts_dtype dtype;
+  uint32_t flags;
+  at::Tensor steps;
+  at::Tensor mask;
+  std::vector<at::Tensor> hyp;
+  at::Tensor out;
+  int64_t R, T;
+  hipStream_t stream;
+
+  const void* h(size_t i) const { return hyp[i].data_ptr(); }
+  const uint8_t* m() const { return static_cast<const uint8_t*>(mask.data_ptr()); }
+};
+
+Prepared prepare(const at::Tensor& params, at::Tensor& state_steps,
+                 const at::Tensor& active_mask, std::initializer_list<const at::Tensor*> hyp,
+                 std::initializer_list<const char*> names, uint32_t flags, const char* op) {
+  check_vec(params, state_steps, op, "state_steps");
+  check_vec(params, active_mask, op, "active_mask");
+  auto name = names.begin();
+  for (const at::Tensor* t : hyp) check_vec(params, *t, op, *name++);
+  Prepared p;
+  const auto dtype = params.scalar_type();
+  p.dtype = ts_dtype_of(dtype, op);
+  p.flags = flags;
+  if (state_steps.scalar_type() == dtype && state_steps.is_contiguous() &&
+      active_mask.scalar_type() == at::kBool) {
+    p.mask = active_mask.reshape({active_mask.numel()}).contiguous();
+    p.steps = state_steps;
+    p.flags |= TS_BUMP_STEPS;
+  } else {
+    state_steps.add_(active_mask.to(state_steps.scalar_type()));
+    p.mask = active_mask.reshape({active_mask.numel()}).to(at::kBool).contiguous();
+    p.steps = hyper(state_steps, dtype);
+  }
+  for (const at::Tensor* t : hyp) p.hyp.push_back(hyper(*t, dtype));
+  p.out = at::empty({}, params.options());
+  p.R = params.size(0);
+  p.T = params.size(1);
+  p.stream = current_stream(params);
+  return p;
+}
+
+// ---------------------------------------------------------------------------
+// Segment tables (per-parameter gradients)
+// ---------------------------------------------------------------------------
+struct SegTable {
+  std::vector<ts_segment> segs;
+  std::vector<at::Tensor> keep;  // (R, numel) views kept alive for the launch
+};
+
+// Each gradient is (R, *shape) and stands for columns [col, col + numel) of
+// params; the table is returned in ascending column order, checked in range
+// and non-overlapping.
+SegTable segments_of(const at::Tensor& params, at::TensorList grads, at::IntArrayRef cols,
+                     const char* op) {
+  TORCH_CHECK(grads.size() == cols.size(), op, ": got ", grads.size(), " gradients but ",
+              cols.size(), " column offsets");
+  const int64_t R = params.size(0), T = params.size(1);
+  std::vector<size_t> order(grads.size());
+  std::iota(order.begin(), order.end(), 0);
+  std::sort(order.begin(), order.end(), [&](size_t a, size_t b) { return cols[a] < cols[b]; });
+  SegTable st;
+  int64_t end = 0;
+  for (size_t i : order) {
+    const at::Tensor& g = grads[i];
+    TORCH_CHECK(g.scalar_type() == params.scalar_type(), op, ": gradient ", i,
+                " must have params' dtype ", params.scalar_type());
+    TORCH_CHECK(g.device() == params.device(), op, ": gradient ", i, " must be on ",
+                params.device());
+    TORCH_CHECK(g.dim() >= 1 && g.size(0) == R, op, ": gradient ", i,
+                " must have the replica count R = ", R, " as its leading dimension");
+    const int64_t numel = R > 0 ? g.numel() / R : 0;
+    TORCH_CHECK(cols[i] >= 0 && cols[i] <= T - numel, op, ": gradient ", i, " (columns ",
+                cols[i], "..", cols[i] + numel, ") lies outside the ", T, " columns");
+    if (R == 0 || numel == 0) continue;
+    TORCH_CHECK(cols[i] >= end, op, ": gradient ", i, " (columns ", cols[i], "..",
+                cols[i] + numel, ") overlaps another gradient");
+    end = cols[i] + numel;
+    at::Tensor g2 = g.reshape({R, numel});
+    if (g2.stride(1) != 1) g2 = g2.contiguous();
+    st.segs.push_back(ts_segment{g2.data_ptr(), g2.stride(0), cols[i], numel});
+    st.keep.push_back(std::move(g2));
+  }
+  return st;
+}
+
+// ---------------------------------------------------------------------------
+// torchstrap::* on the GPU key
+// ---------------------------------------------------------------------------
 at::Tensor adam_step_gpu(at::Tensor params, at::Tensor grads, at::Tensor exp_avgs,
-                         at::Tensor exp_avg_sqs,
-                         std::optional<at::Tensor> max_exp_avg_sqs,
+                         at::Tensor exp_avg_sqs, std::optional<at::Tensor> max_exp_avg_sqs,
                          at::Tensor state_steps, at::Tensor lr, at::Tensor beta1,
-                         at::Tensor beta2, at::Tensor eps,
-                         at::Tensor weight_decay, at::Tensor active_mask,
-                         bool amsgrad, bool maximize,
+                         at::Tensor beta2, at::Tensor eps, at::Tensor weight_decay,
+                         at::Tensor active_mask, bool amsgrad, bool maximize,
                          bool decoupled_weight_decay) {
   constexpr const char* op = "torchstrap::adam_step_";
   check_params(params, op);
-  TORCH_CHECK(!amsgrad || max_exp_avg_sqs.has_value(),
-              "amsgrad=True requires max_exp_avg_sqs");
+  TORCH_CHECK(!amsgrad || max_exp_avg_sqs.has_value(), "amsgrad=True requires max_exp_avg_sqs");
   check_like(params, grads, op, "grads");
   check_like(params, exp_avgs, op, "exp_avgs");
   check_like(params, exp_avg_sqs, op, "exp_avg_sqs");
-  if (amsgrad) {
-    check_like(params, *max_exp_avg_sqs, op, "max_exp_avg_sqs");
-  }
-  check_vec(params, state_steps, op, "state_steps");
-  check_vec(params, lr, op, "lr");
-  check_vec(params, beta1, op, "beta1");
-  check_vec(params, beta2, op, "beta2");
-  check_vec(params, eps, op, "eps");
-  check_vec(params, weight_decay, op, "weight_decay");
-  check_vec(params, active_mask, op, "active_mask");
-
+  if (amsgrad) check_like(params, *max_exp_avg_sqs, op, "max_exp_avg_sqs");
   const c10::DeviceGuard guard(params.device());
-  const auto dtype = params.scalar_type();
-  const ts_dtype td = ts_dtype_of(dtype, op);
-  uint32_t flags = (amsgrad ? TS_AMSGRAD : 0u) |
-                   (decoupled_weight_decay ? TS_ADAMW : 0u) |
-                   (maximize ? TS_MAXIMIZE : 0u);
-  Steps s = prepare_steps(state_steps, active_mask, dtype, flags);
-  const auto lr_c = hyper(lr, dtype);
-  const auto b1_c = hyper(beta1, dtype);
-  const auto b2_c = hyper(beta2, dtype);
-  const auto eps_c = hyper(eps, dtype);
-  const auto wd_c = hyper(weight_decay, dtype);
-
-  ts_rt_buf bufs[5] = {rt_buf(params), rt_buf(grads), rt_buf(exp_avgs),
-                       rt_buf(exp_avg_sqs), ts_rt_buf{nullptr, 0, 1}};
-  if (amsgrad) {
-    bufs[4] = rt_buf(*max_exp_avg_sqs);
-  }
-  at::Tensor out = at::empty({}, params.options());
-  check_status(
-      ts_adam_step(bufs, td, s.steps.data_ptr(), lr_c.data_ptr(), b1_c.data_ptr(),
-                   b2_c.data_ptr(), eps_c.data_ptr(), wd_c.data_ptr(),
-                   static_cast<const uint8_t*>(s.mask.data_ptr()), params.size(0),
-                   params.size(1), flags, out.data_ptr(), current_stream(params)),
+  const Prepared p = prepare(
+      params, state_steps, active_mask, {&lr, &beta1, &beta2, &eps, &weight_decay},
+      {"lr", "beta1", "beta2", "eps", "weight_decay"},
+      (amsgrad ? TS_AMSGRAD : 0u) | (decoupled_weight_decay ? TS_ADAMW : 0u) |
+          (maximize ? TS_MAXIMIZE : 0u),
       op);
-  return out;
+  const ts_rt_buf bufs[5] = {rt_buf(params), rt_buf(grads), rt_buf(exp_avgs),
+                             rt_buf(exp_avg_sqs),
+                             amsgrad ? rt_buf(*max_exp_avg_sqs) : kNoBuf};
+  check_status(ts_adam_step(bufs, p.dtype, p.steps.data_ptr(), p.h(0), p.h(1), p.h(2), p.h(3),
+                            p.h(4), p.m(), p.R, p.T, p.flags, p.out.data_ptr(), p.stream),
+               op);
+  return p.out;
 }
 
 at::Tensor sgd_step_gpu(at::Tensor params, at::Tensor grads,
-                        std::optional<at::Tensor> momentum_buffers,
-                        at::Tensor state_steps, at::Tensor lr,
-                        at::Tensor momentum, at::Tensor dampening,
-                        at::Tensor weight_decay, at::Tensor active_mask,
-                        bool nesterov, bool maximize) {
+                        std::optional<at::Tensor> momentum_buffers, at::Tensor state_steps,
+                        at::Tensor lr, at::Tensor momentum, at::Tensor dampening,
+                        at::Tensor weight_decay, at::Tensor active_mask, bool nesterov,
+                        bool maximize) {
   constexpr const char* op = "torchstrap::sgd_step_";
   check_params(params, op);
-  TORCH_CHECK(!nesterov || momentum_buffers.has_value(),
-              "nesterov=True requires momentum_buffers");
+  TORCH_CHECK(!nesterov || momentum_buffers.has_value(), "nesterov=True requires momentum_buffers");
   check_like(params, grads, op, "grads");
-  const bool has_buf = momentum_buffers.has_value();
-  if (has_buf) {
-    check_like(params, *momentum_buffers, op, "momentum_buffers");
-  }
-  check_vec(params, state_steps, op, "state_steps");
-  check_vec(params, lr, op, "lr");
-  check_vec(params, momentum, op, "momentum");
-  check_vec(params, dampening, op, "dampening");
-  check_vec(params, weight_decay, op, "weight_decay");
-  check_vec(params, active_mask, op, "active_mask");
-
+  if (momentum_buffers.has_value()) check_like(params, *momentum_buffers, op, "momentum_buffers");
   const c10::DeviceGuard guard(params.device());
-  const auto dtype = params.scalar_type();
-  const ts_dtype td = ts_dtype_of(dtype, op);
-  uint32_t flags = (nesterov ? TS_NESTEROV : 0u) | (maximize ? TS_MAXIMIZE : 0u);
-  Steps s = prepare_steps(state_steps, active_mask, dtype, flags);
-  const auto lr_c = hyper(lr, dtype);
-  const auto mom_c = hyper(momentum, dtype);
-  const auto damp_c = hyper(dampening, dtype);
-  const auto wd_c = hyper(weight_decay, dtype);
-
-  ts_rt_buf bufs[3] = {rt_buf(params), rt_buf(grads), ts_rt_buf{nullptr, 0, 1}};
-  if (has_buf) {
-    bufs[2] = rt_buf(*momentum_buffers);
-  }
-  at::Tensor out = at::empty({}, params.options());
-  check_status(
-      ts_sgd_step(bufs, td, s.steps.data_ptr(), lr_c.data_ptr(), mom_c.data_ptr(),
-                  damp_c.data_ptr(), wd_c.data_ptr(),
-                  static_cast<const uint8_t*>(s.mask.data_ptr()), params.size(0),
-                  params.size(1), flags, out.data_ptr(), current_stream(params)),
-      op);
-  return out;
+  const Prepared p = prepare(params, state_steps, active_mask,
+                             {&lr, &momentum, &dampening, &weight_decay},
+                             {"lr", "momentum", "dampening", "weight_decay"},
+                             (nesterov ? TS_NESTEROV : 0u) | (maximize ? TS_MAXIMIZE : 0u), op);
+  const ts_rt_buf bufs[3] = {rt_buf(params), rt_buf(grads),
+                             momentum_buffers.has_value() ? rt_buf(*momentum_buffers) : kNoBuf};
+  check_status(ts_sgd_step(bufs, p.dtype, p.steps.data_ptr(), p.h(0), p.h(1), p.h(2), p.h(3),
+                           p.m(), p.R, p.T, p.flags, p.out.data_ptr(), p.stream),
+               op);
+  return p.out;
 }
 
-at::Tensor adagrad_step_gpu(at::Tensor params, at::Tensor grads,
-                            at::Tensor state_sums, at::Tensor state_steps,
-                            at::Tensor lr, at::Tensor lr_decay,
-                            at::Tensor weight_decay, at::Tensor eps,
-                            at::Tensor active_mask, bool maximize) {
+at::Tensor adagrad_step_gpu(at::Tensor params, at::Tensor grads, at::Tensor state_sums,
+                            at::Tensor state_steps, at::Tensor lr, at::Tensor lr_decay,
+                            at::Tensor weight_decay, at::Tensor eps, at::Tensor active_mask,
+                            bool maximize) {
   constexpr const char* op = "torchstrap::adagrad_step_";
   check_params(params, op);
   check_like(params, grads, op, "grads");
   check_like(params, state_sums, op, "state_sums");
-  check_vec(params, state_steps, op, "state_steps");
-  check_vec(params, lr, op, "lr");
-  check_vec(params, lr_decay, op, "lr_decay");
-  check_vec(params, weight_decay, op, "weight_decay");
-  check_vec(params, eps, op, "eps");
-  check_vec(params, active_mask, op, "active_mask");
-
   const c10::DeviceGuard guard(params.device());
-  const auto dtype = params.scalar_type();
-  const ts_dtype td = ts_dtype_of(dtype, op);
-  uint32_t flags = maximize ? TS_MAXIMIZE : 0u;
-  Steps s = prepare_steps(state_steps, active_mask, dtype, flags);
-  const auto lr_c = hyper(lr, dtype);
-  const auto lrd_c = hyper(lr_decay, dtype);
-  const auto wd_c = hyper(weight_decay, dtype);
-  const auto eps_c = hyper(eps, dtype);
+  const Prepared p = prepare(params, state_steps, active_mask,
+                             {&lr, &lr_decay, &weight_decay, &eps},
+                             {"lr", "lr_decay", "weight_decay", "eps"},
+                             maximize ? TS_MAXIMIZE : 0u, op);
+  const ts_rt_buf bufs[3] = {rt_buf(params), rt_buf(grads), rt_buf(state_sums)};
+  check_status(ts_adagrad_step(bufs, p.dtype, p.steps.data_ptr(), p.h(0), p.h(1), p.h(2),
+                               p.h(3), p.m(), p.R, p.T, p.flags, p.out.data_ptr(), p.stream),
+               op);
+  return p.out;
+}
 
-  ts_rt_buf bufs[3] = {rt_buf(params), rt_buf(grads), rt_buf(state_sums)};
-  at::Tensor out = at::empty({}, params.options());
-  check_status(
-      ts_adagrad_step(bufs, td, s.steps.data_ptr(), lr_c.data_ptr(),
-                      lrd_c.data_ptr(), wd_c.data_ptr(), eps_c.data_ptr(),
-                      static_cast<const uint8_t*>(s.mask.data_ptr()),
-                      params.size(0), params.size(1), flags, out.data_ptr(),
-                      current_stream(params)),
+// ---------------------------------------------------------------------------
+// churten::* on the GPU key
+// ---------------------------------------------------------------------------
+void scatter_grads_gpu(at::Tensor dst, at::TensorList grads, at::IntArrayRef cols) {
+  constexpr const char* op = "churten::scatter_grads_";
+  TORCH_CHECK(dst.dim() == 2 && dst.is_cuda(), op, ": dst must be a 2-D (R, T) GPU buffer");
+  TORCH_CHECK(dst.stride(1) == 1, op, ": dst rows must be contiguous");
+  const c10::DeviceGuard guard(dst.device());
+  const SegTable st = segments_of(dst, grads, cols, op);
+  check_status(ts_scatter_segments(st.segs.data(), static_cast<int>(st.segs.size()),
+                                   ts_dtype_of(dst.scalar_type(), op), dst.data_ptr(),
+                                   dst.stride(0), dst.size(1), dst.size(0),
+                                   current_stream(dst)),
+               op);
+}
+
+at::Tensor adam_step_segments_gpu(at::Tensor params, at::TensorList grads, at::IntArrayRef cols,
+                                  std::optional<at::Tensor> grads_out, at::Tensor exp_avgs,
+                                  at::Tensor exp_avg_sqs,
+                                  std::optional<at::Tensor> max_exp_avg_sqs,
+                                  at::Tensor state_steps, at::Tensor lr, at::Tensor beta1,
+                                  at::Tensor beta2, at::Tensor eps, at::Tensor weight_decay,
+                                  at::Tensor active_mask, bool amsgrad, bool maximize,
+                                  bool decoupled_weight_decay) {
+  constexpr const char* op = "churten::adam_step_segments_";
+  check_params(params, op);
+  TORCH_CHECK(!amsgrad || max_exp_avg_sqs.has_value(), "amsgrad=True requires max_exp_avg_sqs");
+  if (grads_out.has_value()) check_like(params, *grads_out, op, "grads_out");
+  check_like(params, exp_avgs, op, "exp_avgs");
+  check_like(params, exp_avg_sqs, op, "exp_avg_sqs");
+  if (amsgrad) check_like(params, *max_exp_avg_sqs, op, "max_exp_avg_sqs");
+  const c10::DeviceGuard guard(params.device());
+  const SegTable st = segments_of(params, grads, cols, op);
+  const Prepared p = prepare(
+      params, state_steps, active_mask, {&lr, &beta1, &beta2, &eps, &weight_decay},
+      {"lr", "beta1", "beta2", "eps", "weight_decay"},
+      (amsgrad ? TS_AMSGRAD : 0u) | (decoupled_weight_decay ? TS_ADAMW : 0u) |
+          (maximize ? TS_MAXIMIZE : 0u),
       op);
-  return out;
+  const ts_rt_buf bufs[5] = {rt_buf(params), grads_out.has_value() ? rt_buf(*grads_out) : kNoBuf,
+                             rt_buf(exp_avgs), rt_buf(exp_avg_sqs),
+                             amsgrad ? rt_buf(*max_exp_avg_sqs) : kNoBuf};
+  check_status(ts_adam_step_segments(bufs, st.segs.data(), static_cast<int>(st.segs.size()),
+                                     p.dtype, p.steps.data_ptr(), p.h(0), p.h(1), p.h(2),
+                                     p.h(3), p.h(4), p.m(), p.R, p.T, p.flags, p.out.data_ptr(),
+                                     p.stream),
+               op);
+  return p.out;
+}
+
+at::Tensor sgd_step_segments_gpu(at::Tensor params, at::TensorList grads, at::IntArrayRef cols,
+                                 std::optional<at::Tensor> grads_out,
+                                 std::optional<at::Tensor> momentum_buffers,
+                                 at::Tensor state_steps, at::Tensor lr, at::Tensor momentum,
+                                 at::Tensor dampening, at::Tensor weight_decay,
+                                 at::Tensor active_mask, bool nesterov, bool maximize) {
+  constexpr const char* op = "churten::sgd_step_segments_";
+  check_params(params, op);
+  TORCH_CHECK(!nesterov || momentum_buffers.has_value(), "nesterov=True requires momentum_buffers");
+  if (grads_out.has_value()) check_like(params, *grads_out, op, "grads_out");
+  if (momentum_buffers.has_value()) check_like(params, *momentum_buffers, op, "momentum_buffers");
+  const c10::DeviceGuard guard(params.device());
+  const SegTable st = segments_of(params, grads, cols, op);
+  const Prepared p = prepare(params, state_steps, active_mask,
+                             {&lr, &momentum, &dampening, &weight_decay},
+                             {"lr", "momentum", "dampening", "weight_decay"},
+                             (nesterov ? TS_NESTEROV : 0u) | (maximize ? TS_MAXIMIZE : 0u), op);
+  const ts_rt_buf bufs[3] = {rt_buf(params), grads_out.has_value() ? rt_buf(*grads_out) : kNoBuf,
+                             momentum_buffers.has_value() ? rt_buf(*momentum_buffers) : kNoBuf};
+  check_status(ts_sgd_step_segments(bufs, st.segs.data(), static_cast<int>(st.segs.size()),
+                                    p.dtype, p.steps.data_ptr(), p.h(0), p.h(1), p.h(2), p.h(3),
+                                    p.m(), p.R, p.T, p.flags, p.out.data_ptr(), p.stream),
+               op);
+  return p.out;
+}
+
+at::Tensor adagrad_step_segments_gpu(at::Tensor params, at::TensorList grads,
+                                     at::IntArrayRef cols, std::optional<at::Tensor> grads_out,
+                                     at::Tensor state_sums, at::Tensor state_steps,
+                                     at::Tensor lr, at::Tensor lr_decay,
+                                     at::Tensor weight_decay, at::Tensor eps,
+                                     at::Tensor active_mask, bool maximize) {
+  constexpr const char* op = "churten::adagrad_step_segments_";
+  check_params(params, op);
+  if (grads_out.has_value()) check_like(params, *grads_out, op, "grads_out");
+  check_like(params, state_sums, op, "state_sums");
+  const c10::DeviceGuard guard(params.device());
+  const SegTable st = segments_of(params, grads, cols, op);
+  const Prepared p = prepare(params, state_steps, active_mask,
+                             {&lr, &lr_decay, &weight_decay, &eps},
+                             {"lr", "lr_decay", "weight_decay", "eps"},
+                             maximize ? TS_MAXIMIZE : 0u, op);
+  const ts_rt_buf bufs[3] = {rt_buf(params), grads_out.has_value() ? rt_buf(*grads_out) : kNoBuf,
+                             rt_buf(state_sums)};
+  check_status(ts_adagrad_step_segments(bufs, st.segs.data(), static_cast<int>(st.segs.size()),
+                                        p.dtype, p.steps.data_ptr(), p.h(0), p.h(1), p.h(2),
+                                        p.h(3), p.m(), p.R, p.T, p.flags, p.out.data_ptr(),
+                                        p.stream),
+               op);
+  return p.out;
+}
+
+// ---------------------------------------------------------------------------
+// churten::* on the CPU key: the scatter into a consolidated gradient (the
+// caller's grads_out, or a zero buffer), then the torchstrap CPU kernel.
+// ---------------------------------------------------------------------------
+void scatter_grads_cpu(at::Tensor dst, at::TensorList grads, at::IntArrayRef cols) {
+  constexpr const char* op = "churten::scatter_grads_";
+  TORCH_CHECK(dst.dim() == 2, op, ": dst must be a 2-D (R, T) buffer");
+  const SegTable st = segments_of(dst, grads, cols, op);
+  for (size_t i = 0; i < st.segs.size(); ++i) {
+    dst.narrow(1, st.segs[i].col, st.segs[i].numel).copy_(st.keep[i]);
+  }
+}
+
+at::Tensor consolidated(const at::Tensor& params, const std::optional<at::Tensor>& grads_out,
+                        at::TensorList grads, at::IntArrayRef cols) {
+  at::Tensor dst = grads_out.has_value() ? *grads_out : at::zeros_like(params);
+  scatter_grads_cpu(dst, grads, cols);
+  return dst;
+}
+
+at::Tensor adam_step_segments_cpu(at::Tensor params, at::TensorList grads, at::IntArrayRef cols,
+                                  std::optional<at::Tensor> grads_out, at::Tensor exp_avgs,
+                                  at::Tensor exp_avg_sqs,
+                                  std::optional<at::Tensor> max_exp_avg_sqs,
+                                  at::Tensor state_steps, at::Tensor lr, at::Tensor beta1,
+                                  at::Tensor beta2, at::Tensor eps, at::Tensor weight_decay,
+                                  at::Tensor active_mask, bool amsgrad, bool maximize,
+                                  bool decoupled_weight_decay) {
+  static auto step = c10::Dispatcher::singleton()
+                         .findSchemaOrThrow("torchstrap::adam_step_", "")
+                         .typed<at::Tensor(at::Tensor, at::Tensor, at::Tensor, at::Tensor,
+                                           std::optional<at::Tensor>, at::Tensor, at::Tensor,
+                                           at::Tensor, at::Tensor, at::Tensor, at::Tensor,
+                                           at::Tensor, bool, bool, bool)>();
+  TORCH_CHECK(params.dim() == 2, "churten::adam_step_segments_: params must be 2-D");
+  return step.call(params, consolidated(params, grads_out, grads, cols), exp_avgs, exp_avg_sqs,
+                   max_exp_avg_sqs, state_steps, lr, beta1, beta2, eps, weight_decay,
+                   active_mask, amsgrad, maximize, decoupled_weight_decay);
+}
+
+at::Tensor sgd_step_segments_cpu(at::Tensor params, at::TensorList grads, at::IntArrayRef cols,
+                                 std::optional<at::Tensor> grads_out,
+                                 std::optional<at::Tensor> momentum_buffers,
+                                 at::Tensor state_steps, at::Tensor lr, at::Tensor momentum,
+                                 at::Tensor dampening, at::Tensor weight_decay,
+                                 at::Tensor active_mask, bool nesterov, bool maximize) {
+  static auto step = c10::Dispatcher::singleton()
+                         .findSchemaOrThrow("torchstrap::sgd_step_", "")
+                         .typed<at::Tensor(at::Tensor, at::Tensor, std::optional<at::Tensor>,
+                                           at::Tensor, at::Tensor, at::Tensor, at::Tensor,
+                                           at::Tensor, at::Tensor, bool, bool)>();
+  TORCH_CHECK(params.dim() == 2, "churten::sgd_step_segments_: params must be 2-D");
+  return step.call(params, consolidated(params, grads_out, grads, cols), momentum_buffers,
+                   state_steps, lr, momentum, dampening, weight_decay, active_mask, nesterov,
+                   maximize);
+}
+
+at::Tensor adagrad_step_segments_cpu(at::Tensor params, at::TensorList grads,
+                                     at::IntArrayRef cols, std::optional<at::Tensor> grads_out,
+                                     at::Tensor state_sums, at::Tensor state_steps,
+                                     at::Tensor lr, at::Tensor lr_decay,
+                                     at::Tensor weight_decay, at::Tensor eps,
+                                     at::Tensor active_mask, bool maximize) {
+  static auto step = c10::Dispatcher::singleton()
+                         .findSchemaOrThrow("torchstrap::adagrad_step_", "")
+                         .typed<at::Tensor(at::Tensor, at::Tensor, at::Tensor, at::Tensor,
+                                           at::Tensor, at::Tensor, at::Tensor, at::Tensor,
+                                           at::Tensor, bool)>();
+  TORCH_CHECK(params.dim() == 2, "churten::adagrad_step_segments_: params must be 2-D");
+  return step.call(params, consolidated(params, grads_out, grads, cols), state_sums,
+                   state_steps, lr, lr_decay, weight_decay, eps, active_mask, maximize);
 }
 
 }  // namespace
@@ -318,6 +508,37 @@ TORCH_LIBRARY_IMPL(torchstrap, CUDA, m) {
   m.impl("adam_step_", &adam_step_gpu);
   m.impl("sgd_step_", &sgd_step_gpu);
   m.impl("adagrad_step_", &adagrad_step_gpu);
+}
+
+TORCH_LIBRARY(churten, m) {
+  m.def("scatter_grads_(Tensor(a!) dst, Tensor[] grads, int[] cols) -> ()");
+  m.def("adam_step_segments_(Tensor(a!) params, Tensor[] grads, int[] cols, "
+        "Tensor(b!)? grads_out, Tensor(c!) exp_avgs, Tensor(d!) exp_avg_sqs, "
+        "Tensor(e!)? max_exp_avg_sqs, Tensor(f!) state_steps, Tensor lr, Tensor beta1, "
+        "Tensor beta2, Tensor eps, Tensor weight_decay, Tensor active_mask, bool amsgrad, "
+        "bool maximize, bool decoupled_weight_decay) -> Tensor");
+  m.def("sgd_step_segments_(Tensor(a!) params, Tensor[] grads, int[] cols, "
+        "Tensor(b!)? grads_out, Tensor(c!)? momentum_buffers, Tensor(d!) state_steps, "
+        "Tensor lr, Tensor momentum, Tensor dampening, Tensor weight_decay, "
+        "Tensor active_mask, bool nesterov, bool maximize) -> Tensor");
+  m.def("adagrad_step_segments_(Tensor(a!) params, Tensor[] grads, int[] cols, "
+        "Tensor(b!)? grads_out, Tensor(c!) state_sums, Tensor(d!) state_steps, Tensor lr, "
+        "Tensor lr_decay, Tensor weight_decay, Tensor eps, Tensor active_mask, "
+        "bool maximize) -> Tensor");
+}
+
+TORCH_LIBRARY_IMPL(churten, CUDA, m) {
+  m.impl("scatter_grads_", &scatter_grads_gpu);
+  m.impl("adam_step_segments_", &adam_step_segments_gpu);
+  m.impl("sgd_step_segments_", &sgd_step_segments_gpu);
+  m.impl("adagrad_step_segments_", &adagrad_step_segments_gpu);
+}
+
+TORCH_LIBRARY_IMPL(churten, CPU, m) {
+  m.impl("scatter_grads_", &scatter_grads_cpu);
+  m.impl("adam_step_segments_", &adam_step_segments_cpu);
+  m.impl("sgd_step_segments_", &sgd_step_segments_cpu);
+  m.impl("adagrad_step_segments_", &adagrad_step_segments_cpu);
 }
 
 }  // namespace churten

@@ -12,6 +12,7 @@ from __future__ import annotations
 import torch
 
 from churten_amd.kernels.adagrad import adagrad_step_
+from churten_amd.kernels.segments import adagrad_step_segments_
 from churten_amd.optimizer.grad_transform import GradientTransformation
 from churten_amd.state import State
 
@@ -35,12 +36,9 @@ class Adagrad(metaclass=GradientTransformation):
         return state
 
     @classmethod
-    def update(cls, state: State, maximize: bool = False) -> State:
+    def _state_args(cls, state: State, maximize=False):
         opt = state.optimizer_state
-        maximize = bool(opt.get("maximize", maximize))
-        adagrad_step_(
-            torch.atleast_2d(state.flat_params),
-            torch.atleast_2d(state.flat_grads),
+        args = (
             torch.atleast_2d(opt["state_sums"]),
             torch.atleast_1d(opt["state_steps"]),
             torch.atleast_1d(opt["lr"]),
@@ -48,6 +46,22 @@ class Adagrad(metaclass=GradientTransformation):
             torch.atleast_1d(opt["weight_decay"]),
             torch.atleast_1d(opt["eps"]),
             torch.atleast_1d(state.active_mask),
-            maximize=maximize,
         )
+        return args, dict(maximize=bool(opt.get("maximize", maximize)))
+
+    @classmethod
+    def update(cls, state: State, maximize: bool = False) -> State:
+        args, flags = cls._state_args(state, maximize)
+        adagrad_step_(torch.atleast_2d(state.flat_params), torch.atleast_2d(state.flat_grads),
+                      *args, **flags)
+        return state
+
+    @classmethod
+    def update_segments(cls, state: State, grads, cols, grads_out) -> State:
+        """``update`` with the gradient read from the per-parameter tensors
+        (``churten::adagrad_step_segments_``); ``grads_out`` receives the
+        consolidated gradient unless it is None."""
+        args, flags = cls._state_args(state)
+        adagrad_step_segments_(torch.atleast_2d(state.flat_params), grads, cols, grads_out,
+                               *args, **flags)
         return state

@@ -4,7 +4,8 @@ Restates src/torchstrap/optimizer/adam.py:49-143: ``init`` registers the
 per-replica ``(N,)`` hyperparameters (floats or tensors, stored in the param
 dtype), a zero ``state_steps`` counter, ``(N, T)`` moments (plus
 ``max_exp_avg_sqs`` under amsgrad) and the static variant flags; ``update``
-issues one ``torchstrap::adam_step_`` call over the whole ensemble.
+issues one ``torchstrap::adam_step_`` call over the whole ensemble, and
+``update_segments`` the same step with the gradient scatter fused in.
 Defaults are the reference's: AdamW-style decoupled decay with
 weight_decay = 1e-2.
 """
@@ -14,6 +15,7 @@ from __future__ import annotations
 import torch
 
 from churten_amd.kernels.adam import adam_step_
+from churten_amd.kernels.segments import adam_step_segments_
 from churten_amd.optimizer.grad_transform import GradientTransformation
 from churten_amd.state import State
 
@@ -38,16 +40,11 @@ class Adam(metaclass=GradientTransformation):
         return state
 
     @classmethod
-    def update(cls, state: State, decoupled_weight_decay: bool = True, maximize: bool = False,
-               amsgrad: bool = False) -> State:
+    def _state_args(cls, state: State, decoupled_weight_decay=True, maximize=False,
+                    amsgrad=False):
         opt = state.optimizer_state
-        amsgrad = bool(opt.get("amsgrad", amsgrad))
-        maximize = bool(opt.get("maximize", maximize))
-        decoupled_weight_decay = bool(opt.get("decoupled_weight_decay", decoupled_weight_decay))
         mx = opt.get("max_exp_avg_sqs")
-        adam_step_(
-            torch.atleast_2d(state.flat_params),
-            torch.atleast_2d(state.flat_grads),
+        args = (
             torch.atleast_2d(opt["exp_avgs"]),
             torch.atleast_2d(opt["exp_avg_sqs"]),
             torch.atleast_2d(mx) if mx is not None else None,
@@ -58,8 +55,29 @@ class Adam(metaclass=GradientTransformation):
             torch.atleast_1d(opt["eps"]),
             torch.atleast_1d(opt["weight_decay"]),
             torch.atleast_1d(state.active_mask),
-            amsgrad=amsgrad,
-            maximize=maximize,
-            decoupled_weight_decay=decoupled_weight_decay,
         )
+        flags = dict(
+            amsgrad=bool(opt.get("amsgrad", amsgrad)),
+            maximize=bool(opt.get("maximize", maximize)),
+            decoupled_weight_decay=bool(opt.get("decoupled_weight_decay",
+                                                decoupled_weight_decay)),
+        )
+        return args, flags
+
+    @classmethod
+    def update(cls, state: State, decoupled_weight_decay: bool = True, maximize: bool = False,
+               amsgrad: bool = False) -> State:
+        args, flags = cls._state_args(state, decoupled_weight_decay, maximize, amsgrad)
+        adam_step_(torch.atleast_2d(state.flat_params), torch.atleast_2d(state.flat_grads),
+                   *args, **flags)
+        return state
+
+    @classmethod
+    def update_segments(cls, state: State, grads, cols, grads_out) -> State:
+        """``update`` with the gradient read from the per-parameter tensors
+        (``churten::adam_step_segments_``); ``grads_out`` receives the
+        consolidated gradient unless it is None."""
+        args, flags = cls._state_args(state)
+        adam_step_segments_(torch.atleast_2d(state.flat_params), grads, cols, grads_out,
+                            *args, **flags)
         return state

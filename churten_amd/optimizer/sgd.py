@@ -14,6 +14,7 @@ from __future__ import annotations
 
 import torch
 
+from churten_amd.kernels.segments import sgd_step_segments_
 from churten_amd.kernels.sgd import sgd_step_
 from churten_amd.optimizer.grad_transform import GradientTransformation
 from churten_amd.state import State
@@ -43,22 +44,34 @@ class SGD(metaclass=GradientTransformation):
         return state
 
     @classmethod
-    def update(cls, state: State, nesterov: bool = False, maximize: bool = False) -> State:
+    def _state_args(cls, state: State, nesterov=False, maximize=False):
         opt = state.optimizer_state
-        nesterov = bool(opt.get("nesterov", nesterov))
-        maximize = bool(opt.get("maximize", maximize))
         mb = opt.get("momentum_buffers")
-        sgd_step_(
-            torch.atleast_2d(state.flat_params),
-            torch.atleast_2d(state.flat_grads),
-            torch.atleast_2d(mb) if mb is not None else None,
+        args = (
             torch.atleast_1d(opt["state_steps"]),
             torch.atleast_1d(opt["lr"]),
             torch.atleast_1d(opt["momentum"]),
             torch.atleast_1d(opt["dampening"]),
             torch.atleast_1d(opt["weight_decay"]),
             torch.atleast_1d(state.active_mask),
-            nesterov=nesterov,
-            maximize=maximize,
         )
+        flags = dict(nesterov=bool(opt.get("nesterov", nesterov)),
+                     maximize=bool(opt.get("maximize", maximize)))
+        return torch.atleast_2d(mb) if mb is not None else None, args, flags
+
+    @classmethod
+    def update(cls, state: State, nesterov: bool = False, maximize: bool = False) -> State:
+        mb, args, flags = cls._state_args(state, nesterov, maximize)
+        sgd_step_(torch.atleast_2d(state.flat_params), torch.atleast_2d(state.flat_grads), mb,
+                  *args, **flags)
+        return state
+
+    @classmethod
+    def update_segments(cls, state: State, grads, cols, grads_out) -> State:
+        """``update`` with the gradient read from the per-parameter tensors
+        (``churten::sgd_step_segments_``); ``grads_out`` receives the
+        consolidated gradient unless it is None."""
+        mb, args, flags = cls._state_args(state)
+        sgd_step_segments_(torch.atleast_2d(state.flat_params), grads, cols, grads_out, mb,
+                           *args, **flags)
         return state

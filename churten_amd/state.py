@@ -98,10 +98,15 @@ def consolidated_dict_view(tcons: torch.Tensor, metadata) -> dict[str, torch.Ten
 
 class _GradScatter:
     """The gradient buffer seen through per-name views; ``update_`` writes a
-    per-name gradient dict into the consolidated ``(N, T)`` buffer."""
+    per-name gradient dict into the consolidated ``(N, T)`` buffer -- in one
+    ``churten::scatter_grads_`` launch when every gradient is exactly
+    ``(N, *shape)`` in the buffer's dtype and device, else one ``copy_`` per
+    name (which also broadcasts and converts, as the views' ``copy_`` would)."""
 
-    def __init__(self, views: dict[str, torch.Tensor]):
-        self._views = views
+    def __init__(self, buffer: torch.Tensor, metadata):
+        self._buffer = buffer
+        self._meta = {name: (shape, off, n) for name, shape, off, n in metadata}
+        self._views = consolidated_dict_view(buffer, metadata)
 
     def keys(self):
         return self._views.keys()
@@ -109,10 +114,32 @@ class _GradScatter:
     def __getitem__(self, k):
         return self._views[k]
 
+    def segments(self, grads: dict[str, torch.Tensor]):
+        """``(tensors, cols)`` for the fused scatter, or None when some
+        gradient needs the per-name path (unknown name, other shape, dtype or
+        device)."""
+        buf = self._buffer
+        tensors, cols = [], []
+        for name, g in grads.items():
+            meta = self._meta.get(name)
+            # meta[0] is the stacked (N, *shape)
+            if (meta is None or not isinstance(g, torch.Tensor) or g.dtype != buf.dtype
+                    or g.device != buf.device or tuple(g.shape) != tuple(meta[0])):
+                return None
+            tensors.append(g.detach())
+            cols.append(meta[1])
+        return tensors, cols
+
     def update_(self, grads: dict[str, torch.Tensor]) -> "_GradScatter":
         with torch.no_grad():
-            for name, g in grads.items():
-                self._views[name].copy_(g)
+            segs = self.segments(grads) if self._buffer.dim() == 2 else None
+            if segs is not None:
+                from churten_amd.kernels.segments import scatter_grads_
+
+                scatter_grads_(self._buffer, *segs)
+            else:
+                for name, g in grads.items():
+                    self._views[name].copy_(g)
         return self
 
 
@@ -164,7 +191,7 @@ class State:
 
     @property
     def _consolidated_grads(self) -> _GradScatter:
-        return _GradScatter(consolidated_dict_view(self.grads, self.param_meta))
+        return _GradScatter(self.grads, self.param_meta)
 
     # -- optimizer state ---------------------------------------------------
     def add_optim_state(self, key: str, value: Any = None, per_param: bool = False) -> None:

@@ -15,6 +15,11 @@
  *   ts_adagrad_step <- torchstrap::adagrad_step_  (stubs.cpp:61-72, csrc/cuda/adagrad.cu:238-283)
  *   ts_bump_steps   <- the `state_steps.add_(active_mask.to(...))` every op
  *                      runs first (adam.cu:277, sgd.cu:317, adagrad.cu:256)
+ *   ts_*_step_segments, ts_scatter_segments
+ *                   <- the gradient scatter `state._consolidated_grads.update_(grads)`
+ *                      (src/torchstrap/optimizer/grad_transform.py:29) that precedes
+ *                      every update: one copy per parameter tensor there; fused
+ *                      into the update (or one launch) here
  *
  * Contract shared by every entry point:
  *   - All pointers are device pointers on the device that is current for the
@@ -69,6 +74,17 @@ typedef enum ts_dtype {
 #define TS_NESTEROV 0x8u    /* SGD: Nesterov momentum (needs a buffer) */
 #define TS_BUMP_STEPS 0x10u /* all: state_steps += active_mask first */
 
+/* A per-parameter gradient: an (R, numel) tensor with element (r, j) at
+ * data + r*stride_r + j, standing for columns [col, col + numel) of the
+ * consolidated (R, T) layout. Tables of segments are in ascending `col` order
+ * and do not overlap. */
+typedef struct ts_segment {
+  const void* data;
+  int64_t stride_r;
+  int64_t col;
+  int64_t numel;
+} ts_segment;
+
 /* state_steps[r] += active_mask[r] for r < R (in `dtype`), and *out_zero = 0
  * if out_zero is not NULL. One tiny launch. */
 int ts_bump_steps(ts_dtype dtype, void* state_steps, const uint8_t* active_mask,
@@ -106,6 +122,41 @@ int ts_adagrad_step(const ts_rt_buf* bufs, ts_dtype dtype, void* state_steps,
                     const void* weight_decay, const void* eps,
                     const uint8_t* active_mask, int64_t R, int64_t T,
                     uint32_t flags, void* out_zero, void* stream);
+
+/* Segmented-gradient forms of the three updates: the gradient of the columns
+ * a segment covers is read from the per-parameter tensors `grads[0..n_grads)`.
+ * bufs[1].data may be NULL; if it is not, those gradients are also written
+ * into that consolidated (R, T) buffer on the way through (all rows, frozen
+ * replicas included, as the separate scatter would), and the columns no
+ * segment covers take their gradient from it; with NULL they take zero. Element
+ * math and flags as the consolidated forms, so every column ends up identical
+ * to ts_scatter_segments into bufs[1] (or into a zeroed buffer) followed by
+ * ts_*_step. One launch per 64 table entries (segments and the gaps between
+ * them), plus the bump. */
+int ts_adam_step_segments(const ts_rt_buf* bufs, const ts_segment* grads, int n_grads,
+                          ts_dtype dtype, void* state_steps, const void* lr,
+                          const void* beta1, const void* beta2, const void* eps,
+                          const void* weight_decay, const uint8_t* active_mask,
+                          int64_t R, int64_t T, uint32_t flags, void* out_zero,
+                          void* stream);
+int ts_sgd_step_segments(const ts_rt_buf* bufs, const ts_segment* grads, int n_grads,
+                         ts_dtype dtype, void* state_steps, const void* lr,
+                         const void* momentum, const void* dampening,
+                         const void* weight_decay, const uint8_t* active_mask,
+                         int64_t R, int64_t T, uint32_t flags, void* out_zero,
+                         void* stream);
+int ts_adagrad_step_segments(const ts_rt_buf* bufs, const ts_segment* grads, int n_grads,
+                             ts_dtype dtype, void* state_steps, const void* lr,
+                             const void* lr_decay, const void* weight_decay,
+                             const void* eps, const uint8_t* active_mask, int64_t R,
+                             int64_t T, uint32_t flags, void* out_zero, void* stream);
+
+/* Gradient scatter in one launch per 64 segments: copies every segment, all R
+ * rows, into its columns of the (R, cols) buffer dst (row stride dst_stride_r,
+ * unit column stride); other columns are not written. Replaces the
+ * per-parameter copies of grad_transform.py:29. */
+int ts_scatter_segments(const ts_segment* src, int n_src, ts_dtype dtype, void* dst,
+                        int64_t dst_stride_r, int64_t cols, int64_t R, void* stream);
 
 /* Library version, for INTEGRATION checks: major*10000 + minor*100 + patch. */
 int ts_version(void);

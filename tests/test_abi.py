@@ -47,14 +47,16 @@ def declared_symbols():
 
 def test_header_declares_the_entry_points():
     assert declared_symbols() == sorted(
-        ["ts_adagrad_step", "ts_adam_step", "ts_bump_steps", "ts_sgd_step", "ts_version"])
+        ["ts_adagrad_step", "ts_adam_step", "ts_bump_steps", "ts_sgd_step", "ts_version",
+         "ts_adam_step_segments", "ts_sgd_step_segments", "ts_adagrad_step_segments",
+         "ts_scatter_segments"])
 
 
 def test_library_exports_every_declared_symbol():
     lib = ctypes.CDLL(str(LIB))
     for name in declared_symbols():
         assert hasattr(lib, name), name
-    assert lib.ts_version() == 100
+    assert lib.ts_version() == 110
 
 
 def test_invalid_arguments_rejected_before_any_launch():
@@ -71,6 +73,55 @@ def test_invalid_arguments_rejected_before_any_launch():
     # unknown dtype, negative R
     assert lib.ts_bump_steps(7, null, null, i64(0), null, null) == 1
     assert lib.ts_bump_steps(0, null, null, i64(-1), null, null) == 1
+
+
+class Segment(ctypes.Structure):
+    _fields_ = [("data", ctypes.c_void_p), ("stride_r", ctypes.c_int64),
+                ("col", ctypes.c_int64), ("numel", ctypes.c_int64)]
+
+
+class RTBuf(ctypes.Structure):
+    _fields_ = [("data", ctypes.c_void_p), ("stride_r", ctypes.c_int64),
+                ("stride_t", ctypes.c_int64)]
+
+
+@pytest.mark.parametrize("segs", [
+    [(0x1000, 16, 8, 8), (0x2000, 16, 0, 12)],   # out of order / overlapping
+    [(0x1000, 16, 0, 8), (0x2000, 16, 6, 4)],    # overlapping
+    [(0x1000, 16, 12, 8)],                       # past the last column
+    [(0x1000, 16, -4, 4)],                       # negative column
+    [(0, 16, 0, 4)],                             # no data for a non-empty segment
+])
+def test_bad_segment_tables_rejected_before_any_launch(segs):
+    """Every check runs before the first enqueue: with the (fake, never
+    dereferenced) device pointers below, a call that got as far as a launch
+    would fault or fail differently; these return hipErrorInvalidValue."""
+    lib = ctypes.CDLL(str(LIB))
+    fake = ctypes.c_void_p(0x10000)
+    bufs = (RTBuf * 5)(*[RTBuf(0x10000 * (i + 1), 16, 1) for i in range(5)])
+    table = (Segment * len(segs))(*[Segment(*s) for s in segs])
+    R, T = ctypes.c_int64(2), ctypes.c_int64(16)
+    flags = ctypes.c_uint32(0x10)
+    assert lib.ts_adam_step_segments(bufs, table, len(segs), 0, fake, fake, fake, fake, fake,
+                                     fake, fake, R, T, flags, None, None) == 1
+    assert lib.ts_sgd_step_segments(bufs, table, len(segs), 0, fake, fake, fake, fake, fake,
+                                    fake, R, T, flags, None, None) == 1
+    assert lib.ts_adagrad_step_segments(bufs, table, len(segs), 0, fake, fake, fake, fake,
+                                        fake, fake, R, T, flags, None, None) == 1
+    assert lib.ts_scatter_segments(table, len(segs), 0, fake, ctypes.c_int64(16), T, R,
+                                   None) == 1
+
+
+def test_segmented_calls_reject_a_missing_table_and_nesterov_without_buffer():
+    lib = ctypes.CDLL(str(LIB))
+    fake = ctypes.c_void_p(0x10000)
+    bufs = (RTBuf * 5)(*[RTBuf(0x10000 * (i + 1), 16, 1) for i in range(5)])
+    R, T = ctypes.c_int64(2), ctypes.c_int64(16)
+    assert lib.ts_adam_step_segments(bufs, None, 3, 0, fake, fake, fake, fake, fake, fake,
+                                     fake, R, T, ctypes.c_uint32(0), None, None) == 1
+    bufs[2] = RTBuf(0, 0, 1)
+    assert lib.ts_sgd_step_segments(bufs, None, 0, 0, fake, fake, fake, fake, fake, fake, R,
+                                    T, ctypes.c_uint32(0x8), None, None) == 1
 
 
 def test_schemas_match_the_reference_text():
@@ -143,8 +194,9 @@ def test_only_cpu_and_gpu_keys_are_served():
     other device raises from the dispatcher -- there is no catch-all kernel."""
     import churten_amd.kernels  # noqa: F401
 
-    for op in ("adam_step_", "sgd_step_", "adagrad_step_"):
-        name = f"torchstrap::{op}"
+    for name in ["torchstrap::adam_step_", "torchstrap::sgd_step_", "torchstrap::adagrad_step_",
+                 "churten::scatter_grads_", "churten::adam_step_segments_",
+                 "churten::sgd_step_segments_", "churten::adagrad_step_segments_"]:
         assert torch._C._dispatch_has_kernel_for_dispatch_key(name, "CPU")
         assert torch._C._dispatch_has_kernel_for_dispatch_key(name, "CUDA")
         assert not torch._C._dispatch_has_kernel_for_dispatch_key(name, "CompositeImplicitAutograd")
