@@ -10,8 +10,9 @@ tensors resident in HBM before timing starts. One "step" is one
 Printed (one JSON line): value = effective HBM GB/s of the whole step (active
 rows x T x 28 B / step time), plus the kernel's roofline (algorithmic bytes of
 one update launch / its average duration, measured with HIP events on the
-launch stream), the reference CPU kernel timed on this host, and the N-instance
-torch.optim Python-loop baseline on the same GPU.
+launch stream), the reference CPU kernel timed on this host, the N-instance
+torch.optim Python-loop baseline on the same GPU, and the training step's
+gradient hand-off (per-parameter scatter then update, vs the fused segmented update).
 
     python bench.py [--gpus 1] [--steps K] [--warmup W] [--config 5]
 """
@@ -363,8 +364,8 @@ def calibrate_copy(nbytes: int = 1 << 30, reps: int = 3) -> None:
 def main():
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
-    ap.add_argument("--steps", type=int, default=20)
-    ap.add_argument("--warmup", type=int, default=5)
+    ap.add_argument("--steps", type=int, default=100)
+    ap.add_argument("--warmup", type=int, default=10)
     ap.add_argument("--config", type=int, default=5, choices=sorted(CONFIGS))
     ap.add_argument("--cpu-steps", type=int, default=5)
     ap.add_argument("--no-cpu-baseline", action="store_true")
@@ -404,16 +405,20 @@ def main():
         fn(*op_args, **kw)
     torch.cuda.synchronize()
 
+    # K steps bracketed by events on the launch stream, plus one event between
+    # consecutive steps for the per-step median.
     stream = torch.cuda.current_stream()
-    e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    ev = [torch.cuda.Event(enable_timing=True) for _ in range(args.steps + 1)]
     t0 = time.perf_counter()
-    e0.record(stream)
-    for _ in range(args.steps):
+    ev[0].record(stream)
+    for i in range(args.steps):
         fn(*op_args, **kw)
-    e1.record(stream)
+        ev[i + 1].record(stream)
     torch.cuda.synchronize()
     wall_ms = (time.perf_counter() - t0) * 1e3 / args.steps
-    step_ms = e0.elapsed_time(e1) / args.steps
+    step_ms = ev[0].elapsed_time(ev[-1]) / args.steps
+    per_step = sorted(ev[i].elapsed_time(ev[i + 1]) for i in range(args.steps))
+    median_ms = per_step[len(per_step) // 2]
 
     kern_ms = kernel_only_timing(op_name, op_args, kw, max(10, args.steps))
     achieved = nbytes / (kern_ms * 1e-3) / 1e9
@@ -441,6 +446,7 @@ def main():
         "warmup": args.warmup,
         "ms_per_step": round(step_ms, 4),
         "us_per_step": round(step_ms * 1e3, 1),
+        "median_us_per_step": round(median_ms * 1e3, 1),
         "wall_ms_per_step": round(wall_ms, 4),
         "pct_of_hbm_peak": round(100 * value / HBM_PEAK_GBS, 1),
         "higher_is_better": True,
