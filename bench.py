@@ -422,7 +422,13 @@ def main():
 
     kern_ms = kernel_only_timing(op_name, op_args, kw, max(10, args.steps))
     achieved = nbytes / (kern_ms * 1e-3) / 1e9
-    kernel = f"{op_name}_stream_kernel"
+    policy = {"adam": "AdamPolicy<float, %s, %s>" % (str(kw.get("decoupled_weight_decay")).lower(),
+                                                     str(kw.get("amsgrad")).lower()),
+              "sgd": "SgdPolicy<float, %s, %s>" % ("true" if op_args[2] is not None else "false",
+                                                   str(kw.get("nesterov")).lower()),
+              "adagrad": "AdagradPolicy<float>"}[op_name]
+    kernel = f"stream_kernel<{policy}>"
+    profile_key = f"{op_name}_stream_kernel_cfg{args.config}"
     del op_args
     torch.cuda.empty_cache()
 
@@ -463,7 +469,7 @@ def main():
                      "peak": HBM_PEAK_GBS, "unit": "GB/s",
                      "frac": round(achieved / HBM_PEAK_GBS, 4),
                      "kernel_avg_ms": round(kern_ms, 4),
-                     "traffic": read_traffic(f"{kernel}_cfg{args.config}")},
+                     "traffic": read_traffic(profile_key)},
         "cpu_baseline": cpu,
         "python_loop_baseline": loop or None,
         "grad_scatter_step": scatter,
