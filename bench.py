@@ -198,7 +198,7 @@ def cpu_baseline(cfg: int, steps: int):
 # ---------------------------------------------------------------------------
 # GPU measurements
 # ---------------------------------------------------------------------------
-def kernel_only_timing(op_name, args, kw, launches: int) -> float:
+def kernel_only_timing(op_name, args, kw, launches: int, extra_flags: int = 0) -> float:
     """Average duration (ms) of the update kernel alone: the C ABI is called
     without the step bump, bracketed by HIP events on the launch stream."""
     import ctypes
@@ -220,14 +220,15 @@ def kernel_only_timing(op_name, args, kw, launches: int) -> float:
     R, T = p.shape
     if op_name == "adam":
         bufs = (RtBuf * 5)(*[buf(t) for t in args[:5]])
-        flags = (1 if kw["amsgrad"] else 0) | (2 if kw["decoupled_weight_decay"] else 0)
+        flags = ((1 if kw["amsgrad"] else 0) | (2 if kw["decoupled_weight_decay"] else 0)
+                 | extra_flags)
         call = lambda: lib.ts_adam_step(  # noqa: E731
             bufs, 0, vp(args[5]), *[vp(t) for t in args[6:11]], vp(args[11]),
             ctypes.c_int64(R), ctypes.c_int64(T), ctypes.c_uint32(flags),
             ctypes.c_void_p(0), ctypes.c_void_p(stream.cuda_stream))
     elif op_name == "sgd":
         bufs = (RtBuf * 3)(*[buf(t) for t in args[:3]])
-        flags = 8 if kw["nesterov"] else 0
+        flags = (8 if kw["nesterov"] else 0) | extra_flags
         call = lambda: lib.ts_sgd_step(  # noqa: E731
             bufs, 0, vp(args[3]), *[vp(t) for t in args[4:8]], vp(args[8]),
             ctypes.c_int64(R), ctypes.c_int64(T), ctypes.c_uint32(flags),
@@ -236,7 +237,7 @@ def kernel_only_timing(op_name, args, kw, launches: int) -> float:
         bufs = (RtBuf * 3)(*[buf(t) for t in args[:3]])
         call = lambda: lib.ts_adagrad_step(  # noqa: E731
             bufs, 0, vp(args[3]), *[vp(t) for t in args[4:8]], vp(args[8]),
-            ctypes.c_int64(R), ctypes.c_int64(T), ctypes.c_uint32(0),
+            ctypes.c_int64(R), ctypes.c_int64(T), ctypes.c_uint32(extra_flags),
             ctypes.c_void_p(0), ctypes.c_void_p(stream.cuda_stream))
     else:
         raise ValueError(op_name)
@@ -336,6 +337,37 @@ def grad_scatter_timing(cfg: int, steps: int):
     return out
 
 
+TS_STATE_BF16 = 0x20
+
+
+def bf16_state_timing(cfg: int, launches: int):
+    """The same update with the optimizer state (moments / buffers / sums) in
+    bfloat16 next to float32 params: kernel-only time and effective GB/s over
+    the bytes it moves (params and grads 4 B, each state buffer 2 B). Not run
+    for config 3, whose first-step replicas skip the buffer read."""
+    import torch
+
+    op_name, args, kw, _ = make_config(cfg)
+    args = list(args)
+    state_idx = {"adam": [2, 3, 4], "sgd": [2], "adagrad": [2]}[op_name]
+    for i in state_idx:
+        if args[i] is not None:
+            args[i] = args[i].to(torch.bfloat16)
+    mask = args[-1]
+    n_state = sum(args[i] is not None for i in state_idx)
+    per_elem = 4 + 4 + 2 * n_state + 4 + 2 * n_state  # read p, g, state; write p, state
+    active = int(mask.sum().item())
+    T = args[0].shape[1]
+    nbytes = active * T * per_elem
+    ms = kernel_only_timing(op_name, tuple(args), kw, launches, extra_flags=TS_STATE_BF16)
+    del args
+    torch.cuda.empty_cache()
+    return {"kernel_avg_ms": round(ms, 4), "bytes_per_elem": per_elem,
+            "achieved_GBs": round(nbytes / (ms * 1e-3) / 1e9, 1),
+            "frac": round(nbytes / (ms * 1e-3) / 1e9 / HBM_PEAK_GBS, 4),
+            "step_equivalent_GBs": round(active * T * bytes_per_elem(cfg) / (ms * 1e-3) / 1e9, 1)}
+
+
 def read_traffic(kernel: str):
     """HBM bytes per launch from the committed rocprofv3 --pmc summary, if any."""
     f = ROOT / "profiles" / f"{kernel}_traffic.json"
@@ -370,6 +402,8 @@ def main():
     ap.add_argument("--cpu-steps", type=int, default=5)
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--no-loop-baseline", action="store_true")
+    ap.add_argument("--no-bf16-state", action="store_true",
+                    help="skip the bfloat16-optimizer-state timing")
     ap.add_argument("--no-grad-scatter", action="store_true",
                     help="skip the scatter-then-update vs fused segmented timing")
     ap.add_argument("--calibrate-copy", action="store_true",
@@ -432,6 +466,10 @@ def main():
     del op_args
     torch.cuda.empty_cache()
 
+    bf16 = None
+    if not args.no_bf16_state and args.config != 3:
+        bf16 = bf16_state_timing(args.config, max(10, args.steps // 2))
+
     scatter = None
     if not args.no_grad_scatter and op_name == "adam":
         scatter = grad_scatter_timing(args.config, max(5, args.steps // 2))
@@ -473,6 +511,7 @@ def main():
         "cpu_baseline": cpu,
         "python_loop_baseline": loop or None,
         "grad_scatter_step": scatter,
+        "bf16_state": bf16,
         "speedup_vs_python_loop": ({k: round(v / step_ms, 2) for k, v in loop.items()}
                                    if loop else None),
     }

@@ -394,6 +394,30 @@ at::Tensor mask_of(const at::Tensor& m) {
   return m.reshape({m.numel()}).to(at::kBool).contiguous();
 }
 
+// bfloat16 optimizer state next to float32 params (an extension; the
+// reference rejects mixed dtypes): the float32 kernel runs on widened copies of
+// the state, which is then rounded back to nearest-even bfloat16.
+bool bf16_state(const at::Tensor& params, const at::Tensor& state) {
+  return params.scalar_type() == at::kFloat && state.scalar_type() == at::kBFloat16;
+}
+
+// Rounds the active rows of a widened state copy back into the bfloat16
+// buffer; frozen rows keep their bits.
+void store_active_rows(at::Tensor& dst, const at::Tensor& src, const at::Tensor& active_mask) {
+  const at::Tensor rows = active_mask.reshape({-1}).to(at::kBool).nonzero().reshape({-1});
+  dst.index_copy_(0, rows, src.index_select(0, rows).to(dst.scalar_type()));
+}
+
+void check_bf16_state(const at::Tensor& params, const at::Tensor& t, const char* op,
+                      const char* name) {
+  TORCH_CHECK(t.dim() == 2 && t.sizes() == params.sizes(), op, ": ", name,
+              " must have params' shape ", params.sizes(), ", got ", t.sizes());
+  TORCH_CHECK(t.scalar_type() == at::kBFloat16, op, ": ", name,
+              " must be bfloat16 like the other state buffers");
+  TORCH_CHECK(t.device() == params.device(), op, ": ", name, " must be on ",
+              params.device());
+}
+
 at::Tensor adam_step_cpu(at::Tensor params, at::Tensor grads, at::Tensor exp_avgs,
                          at::Tensor exp_avg_sqs, std::optional<at::Tensor> max_exp_avg_sqs,
                          at::Tensor state_steps, at::Tensor lr, at::Tensor beta1,
@@ -403,6 +427,21 @@ at::Tensor adam_step_cpu(at::Tensor params, at::Tensor grads, at::Tensor exp_avg
   constexpr const char* op = "torchstrap::adam_step_";
   TORCH_CHECK(params.dim() == 2, op, ": params must be a 2-D (R, T) buffer");
   TORCH_CHECK(!amsgrad || max_exp_avg_sqs.has_value(), "amsgrad=True requires max_exp_avg_sqs");
+  if (bf16_state(params, exp_avgs)) {
+    check_bf16_state(params, exp_avgs, op, "exp_avgs");
+    check_bf16_state(params, exp_avg_sqs, op, "exp_avg_sqs");
+    if (amsgrad) check_bf16_state(params, *max_exp_avg_sqs, op, "max_exp_avg_sqs");
+    at::Tensor m = exp_avgs.to(at::kFloat), v = exp_avg_sqs.to(at::kFloat);
+    std::optional<at::Tensor> mx;
+    if (amsgrad) mx = max_exp_avg_sqs->to(at::kFloat);
+    at::Tensor out = adam_step_cpu(params, grads, m, v, mx, state_steps, lr, beta1, beta2, eps,
+                                   weight_decay, active_mask, amsgrad, maximize,
+                                   decoupled_weight_decay);
+    store_active_rows(exp_avgs, m, active_mask);
+    store_active_rows(exp_avg_sqs, v, active_mask);
+    if (amsgrad) store_active_rows(*max_exp_avg_sqs, *mx, active_mask);
+    return out;
+  }
   check_rt(params, grads, op, "grads");
   check_rt(params, exp_avgs, op, "exp_avgs");
   check_rt(params, exp_avg_sqs, op, "exp_avg_sqs");
@@ -440,6 +479,14 @@ at::Tensor sgd_step_cpu(at::Tensor params, at::Tensor grads,
   constexpr const char* op = "torchstrap::sgd_step_";
   TORCH_CHECK(params.dim() == 2, op, ": params must be a 2-D (R, T) buffer");
   TORCH_CHECK(!nesterov || momentum_buffers.has_value(), "nesterov=True requires momentum_buffers");
+  if (momentum_buffers.has_value() && bf16_state(params, *momentum_buffers)) {
+    check_bf16_state(params, *momentum_buffers, op, "momentum_buffers");
+    std::optional<at::Tensor> mb = momentum_buffers->to(at::kFloat);
+    at::Tensor out = sgd_step_cpu(params, grads, mb, state_steps, lr, momentum, dampening,
+                                  weight_decay, active_mask, nesterov, maximize);
+    store_active_rows(*momentum_buffers, *mb, active_mask);
+    return out;
+  }
   check_rt(params, grads, op, "grads");
   const bool has_buf = momentum_buffers.has_value();
   if (has_buf) check_rt(params, *momentum_buffers, op, "momentum_buffers");
@@ -469,6 +516,14 @@ at::Tensor adagrad_step_cpu(at::Tensor params, at::Tensor grads, at::Tensor stat
                             bool maximize) {
   constexpr const char* op = "torchstrap::adagrad_step_";
   TORCH_CHECK(params.dim() == 2, op, ": params must be a 2-D (R, T) buffer");
+  if (bf16_state(params, state_sums)) {
+    check_bf16_state(params, state_sums, op, "state_sums");
+    at::Tensor s32 = state_sums.to(at::kFloat);
+    at::Tensor out = adagrad_step_cpu(params, grads, s32, state_steps, lr, lr_decay,
+                                      weight_decay, eps, active_mask, maximize);
+    store_active_rows(state_sums, s32, active_mask);
+    return out;
+  }
   check_rt(params, grads, op, "grads");
   check_rt(params, state_sums, op, "state_sums");
   for (auto* p : {&state_steps, &lr, &lr_decay, &weight_decay, &eps, &active_mask})

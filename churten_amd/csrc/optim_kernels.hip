@@ -41,6 +41,7 @@
 
 #include <algorithm>
 #include <initializer_list>
+#include <type_traits>
 
 #include "../../include/churten_optim.h"
 #include "optim_math.h"
@@ -122,10 +123,17 @@ __device__ __forceinline__ double hyper_at(const T* h, uint32_t r) {
 // ---------------------------------------------------------------------------
 // Policies
 // ---------------------------------------------------------------------------
+// Every policy has a parameter/gradient type T and an optimizer-state type S:
+// S == T is the reference's contract; S = bf16_t with T = float keeps the
+// moments (momentum buffers, sums) in bfloat16 while the element math and the
+// parameters stay in float32 (the state is widened on load and rounded to
+// nearest-even on store).
+
 // Adam / AdamW: h = {lr, beta1, beta2, eps, weight_decay}.
-template <typename T_, bool ADAMW, bool AMSGRAD>
+template <typename T_, bool ADAMW, bool AMSGRAD, typename S_ = T_>
 struct AdamPolicy {
   using T = T_;
+  using S = S_;
   using M = op_t<T>;
   static constexpr int NS = AMSGRAD ? 3 : 2;
   struct Rep {
@@ -155,9 +163,10 @@ struct AdamPolicy {
 // carried as double inside the element math, as torch's ROCm `_fused_sgd_`
 // takes them (checked on the MI355X: carrying them as float instead changes
 // params and buffers by up to a few ulp).
-template <typename T_, bool HAS_BUF, bool NESTEROV>
+template <typename T_, bool HAS_BUF, bool NESTEROV, typename S_ = T_>
 struct SgdPolicy {
   using T = T_;
+  using S = S_;
   using M = op_t<T>;
   static constexpr int NS = HAS_BUF ? 1 : 0;
   struct Rep {
@@ -183,9 +192,10 @@ struct SgdPolicy {
 };
 
 // Adagrad: h = {lr, lr_decay, weight_decay, eps}.
-template <typename T_>
+template <typename T_, typename S_ = T_>
 struct AdagradPolicy {
   using T = T_;
+  using S = S_;
   using M = op_t<T>;
   static constexpr int NS = 1;
   struct Rep {
@@ -220,22 +230,34 @@ struct KArgs {
 // state operands' values (unread ones are never used).
 template <typename P>
 __device__ __forceinline__ void apply_element(typename P::T& p_io, typename P::T g_in,
-                                              typename P::T (&s_io)[state_slots<P>()],
+                                              typename P::S (&s_io)[state_slots<P>()],
                                               bool load_state, const typename P::Rep& rep,
                                               bool maximize) {
-  using M = op_t<typename P::T>;
+  using M = typename P::M;
   M p = widen(p_io);
   M s[state_slots<P>()];
 #pragma unroll
   for (int k = 0; k < state_slots<P>(); ++k) {
-    s[k] = (load_state && k < P::NS) ? widen(s_io[k]) : M(0);
+    s[k] = (load_state && k < P::NS) ? M(widen(s_io[k])) : M(0);
   }
   P::update(p, widen(g_in), s, rep, maximize);
   p_io = narrow<typename P::T>(p);
 #pragma unroll
   for (int k = 0; k < P::NS; ++k) {
-    s_io[k] = narrow<typename P::T>(s[k]);
+    s_io[k] = narrow<typename P::S>(s[k]);
   }
+}
+
+// Row r of (R, T) operand b, as the parameter type (b < 2) or the state type.
+template <typename P>
+__device__ __forceinline__ typename P::T* pg_row(const Operands<typename P::T>& x, int b,
+                                                 uint32_t r) {
+  return x.data[b] + int64_t(r) * x.stride_r[b];
+}
+template <typename P>
+__device__ __forceinline__ typename P::S* state_row(const Operands<typename P::T>& x, int b,
+                                                    uint32_t r) {
+  return reinterpret_cast<typename P::S*>(x.data[b]) + int64_t(r) * x.stride_r[b];
 }
 
 // ---------------------------------------------------------------------------
@@ -244,6 +266,7 @@ __device__ __forceinline__ void apply_element(typename P::T& p_io, typename P::T
 template <typename P>
 __global__ __launch_bounds__(kThreads) void stream_kernel(KArgs<P> a) {
   using T = typename P::T;
+  using S = typename P::S;
   constexpr int NS = P::NS;
   constexpr int SS = state_slots<P>();
   uint32_t r;
@@ -256,24 +279,27 @@ __global__ __launch_bounds__(kThreads) void stream_kernel(KArgs<P> a) {
   P::prologue(a.vec, r, rep);
   const bool load_state = P::reads_state(rep);
 
-  Pack<T>* row[2 + SS];
+  Pack<T>* prow = reinterpret_cast<Pack<T>*>(pg_row<P>(a.x, 0, r) + t0);
+  const Pack<T>* grow = reinterpret_cast<const Pack<T>*>(pg_row<P>(a.x, 1, r) + t0);
+  Pack<S>* srow[SS];
 #pragma unroll
-  for (int b = 0; b < 2 + NS; ++b) {
-    row[b] = reinterpret_cast<Pack<T>*>(a.x.data[b] + int64_t(r) * a.x.stride_r[b] + t0);
+  for (int b = 0; b < NS; ++b) {
+    srow[b] = reinterpret_cast<Pack<S>*>(state_row<P>(a.x, 2 + b, r) + t0);
   }
   const int64_t packs_left = (a.g.T - t0) / kPack;
 
-  Pack<T> v[2 + SS][kUnroll];
+  Pack<T> vp[kUnroll], vg[kUnroll];
+  Pack<S> vs[SS][kUnroll];
 #pragma unroll
   for (int u = 0; u < kUnroll; ++u) {
     const int64_t i = int64_t(u) * kThreads + threadIdx.x;
     if (i < packs_left) {
-      v[0][u] = load_stream(row[0] + i);
-      v[1][u] = load_stream(row[1] + i);
+      vp[u] = load_stream(prow + i);
+      vg[u] = load_stream(grow + i);
       if (load_state) {
 #pragma unroll
-        for (int b = 2; b < 2 + NS; ++b) {
-          v[b][u] = load_stream(row[b] + i);
+        for (int b = 0; b < NS; ++b) {
+          vs[b][u] = load_stream(srow[b] + i);
         }
       }
     }
@@ -284,17 +310,17 @@ __global__ __launch_bounds__(kThreads) void stream_kernel(KArgs<P> a) {
     if (i < packs_left) {
 #pragma unroll
       for (int k = 0; k < kPack; ++k) {
-        T s[SS];
+        S st[SS];
 #pragma unroll
-        for (int b = 0; b < NS; ++b) s[b] = v[2 + b][u].v[k];
-        apply_element<P>(v[0][u].v[k], v[1][u].v[k], s, load_state, rep, a.maximize);
+        for (int b = 0; b < NS; ++b) st[b] = vs[b][u].v[k];
+        apply_element<P>(vp[u].v[k], vg[u].v[k], st, load_state, rep, a.maximize);
 #pragma unroll
-        for (int b = 0; b < NS; ++b) v[2 + b][u].v[k] = s[b];
+        for (int b = 0; b < NS; ++b) vs[b][u].v[k] = st[b];
       }
-      store_stream(row[0] + i, v[0][u]);
+      store_stream(prow + i, vp[u]);
 #pragma unroll
-      for (int b = 2; b < 2 + NS; ++b) {
-        store_stream(row[b] + i, v[b][u]);
+      for (int b = 0; b < NS; ++b) {
+        store_stream(srow[b] + i, vs[b][u]);
       }
     }
   }
@@ -303,6 +329,7 @@ __global__ __launch_bounds__(kThreads) void stream_kernel(KArgs<P> a) {
 template <typename P>
 __global__ __launch_bounds__(kThreads) void element_kernel(KArgs<P> a) {
   using T = typename P::T;
+  using S = typename P::S;
   constexpr int NS = P::NS;
   constexpr int SS = state_slots<P>();
   uint32_t r;
@@ -315,22 +342,23 @@ __global__ __launch_bounds__(kThreads) void element_kernel(KArgs<P> a) {
   P::prologue(a.vec, r, rep);
   const bool load_state = P::reads_state(rep);
 
-  T* base[2 + SS];
+  T* const prow = pg_row<P>(a.x, 0, r);
+  const T* const grow = pg_row<P>(a.x, 1, r);
+  S* srow[SS];
 #pragma unroll
-  for (int b = 0; b < 2 + NS; ++b) {
-    base[b] = a.x.data[b] + int64_t(r) * a.x.stride_r[b];
-  }
-  T v[2 + SS][kPer];
+  for (int b = 0; b < NS; ++b) srow[b] = state_row<P>(a.x, 2 + b, r);
+  T vp[kPer], vg[kPer];
+  S vs[SS][kPer];
 #pragma unroll
   for (int u = 0; u < kPer; ++u) {
     const int64_t t = t0 + int64_t(u) * kThreads + threadIdx.x;
     if (t < a.g.T) {
-      v[0][u] = base[0][t * a.x.stride_t[0]];
-      v[1][u] = base[1][t * a.x.stride_t[1]];
+      vp[u] = prow[t * a.x.stride_t[0]];
+      vg[u] = grow[t * a.x.stride_t[1]];
       if (load_state) {
 #pragma unroll
-        for (int b = 2; b < 2 + NS; ++b) {
-          v[b][u] = base[b][t * a.x.stride_t[b]];
+        for (int b = 0; b < NS; ++b) {
+          vs[b][u] = srow[b][t * a.x.stride_t[2 + b]];
         }
       }
     }
@@ -339,14 +367,14 @@ __global__ __launch_bounds__(kThreads) void element_kernel(KArgs<P> a) {
   for (int u = 0; u < kPer; ++u) {
     const int64_t t = t0 + int64_t(u) * kThreads + threadIdx.x;
     if (t < a.g.T) {
-      T s[SS];
+      S st[SS];
 #pragma unroll
-      for (int b = 0; b < NS; ++b) s[b] = v[2 + b][u];
-      apply_element<P>(v[0][u], v[1][u], s, load_state, rep, a.maximize);
-      base[0][t * a.x.stride_t[0]] = v[0][u];
+      for (int b = 0; b < NS; ++b) st[b] = vs[b][u];
+      apply_element<P>(vp[u], vg[u], st, load_state, rep, a.maximize);
+      prow[t * a.x.stride_t[0]] = vp[u];
 #pragma unroll
       for (int b = 0; b < NS; ++b) {
-        base[2 + b][t * a.x.stride_t[2 + b]] = s[b];
+        srow[b][t * a.x.stride_t[2 + b]] = st[b];
       }
     }
   }
@@ -391,6 +419,7 @@ __device__ __forceinline__ int segment_of_tile(const uint32_t* tile0, int n, uin
 template <typename P>
 __global__ __launch_bounds__(kThreads) void segment_kernel(SegArgs<P> a) {
   using T = typename P::T;
+  using S = typename P::S;
   constexpr int NS = P::NS;
   constexpr int SS = state_slots<P>();
   const uint32_t tiles_per_row = a.seg.tile0[a.seg.n];
@@ -436,32 +465,33 @@ __global__ __launch_bounds__(kThreads) void segment_kernel(SegArgs<P> a) {
   const bool store_grad = write_grad && !gap;
   const T zero = narrow<T>(op_t<T>(0));
 
-  T* base[2 + SS];
+  T* const prow = pg_row<P>(a.k.x, 0, r) + c0 * a.k.x.stride_t[0];
+  S* srow[SS];
 #pragma unroll
-  for (int b = 0; b < 2 + NS; ++b) {
-    base[b] = b == 1 ? nullptr
-                     : a.k.x.data[b] + int64_t(r) * a.k.x.stride_r[b] + c0 * a.k.x.stride_t[b];
+  for (int b = 0; b < NS; ++b) {
+    srow[b] = state_row<P>(a.k.x, 2 + b, r) + c0 * a.k.x.stride_t[2 + b];
   }
 
   int64_t done = 0;  // leading elements handled by the vector loop
   if ((a.seg.vec_ok >> s) & 1u) {
     const int64_t packs = cnt / kPack;
-    Pack<T> v[2 + SS][kUnroll];
+    Pack<T> vp[kUnroll], vg[kUnroll];
+    Pack<S> vs[SS][kUnroll];
 #pragma unroll
     for (int u = 0; u < kUnroll; ++u) {
       const int64_t i = int64_t(u) * kThreads + threadIdx.x;
       if (i < packs) {
-        v[0][u] = load_stream(reinterpret_cast<const Pack<T>*>(base[0]) + i);
+        vp[u] = load_stream(reinterpret_cast<const Pack<T>*>(prow) + i);
         if (g_src != nullptr) {
-          v[1][u] = load_stream(reinterpret_cast<const Pack<T>*>(g_src) + i);
+          vg[u] = load_stream(reinterpret_cast<const Pack<T>*>(g_src) + i);
         } else {
 #pragma unroll
-          for (int k = 0; k < kPack; ++k) v[1][u].v[k] = zero;
+          for (int k = 0; k < kPack; ++k) vg[u].v[k] = zero;
         }
         if (load_state) {
 #pragma unroll
-          for (int b = 2; b < 2 + NS; ++b) {
-            v[b][u] = load_stream(reinterpret_cast<const Pack<T>*>(base[b]) + i);
+          for (int b = 0; b < NS; ++b) {
+            vs[b][u] = load_stream(reinterpret_cast<const Pack<S>*>(srow[b]) + i);
           }
         }
       }
@@ -471,21 +501,21 @@ __global__ __launch_bounds__(kThreads) void segment_kernel(SegArgs<P> a) {
       const int64_t i = int64_t(u) * kThreads + threadIdx.x;
       if (i < packs) {
         if (store_grad) {
-          store_stream(reinterpret_cast<Pack<T>*>(g_dst) + i, v[1][u]);
+          store_stream(reinterpret_cast<Pack<T>*>(g_dst) + i, vg[u]);
         }
 #pragma unroll
         for (int k = 0; k < kPack; ++k) {
-          T st[SS];
+          S st[SS];
 #pragma unroll
-          for (int b = 0; b < NS; ++b) st[b] = v[2 + b][u].v[k];
-          apply_element<P>(v[0][u].v[k], v[1][u].v[k], st, load_state, rep, a.k.maximize);
+          for (int b = 0; b < NS; ++b) st[b] = vs[b][u].v[k];
+          apply_element<P>(vp[u].v[k], vg[u].v[k], st, load_state, rep, a.k.maximize);
 #pragma unroll
-          for (int b = 0; b < NS; ++b) v[2 + b][u].v[k] = st[b];
+          for (int b = 0; b < NS; ++b) vs[b][u].v[k] = st[b];
         }
-        store_stream(reinterpret_cast<Pack<T>*>(base[0]) + i, v[0][u]);
+        store_stream(reinterpret_cast<Pack<T>*>(prow) + i, vp[u]);
 #pragma unroll
-        for (int b = 2; b < 2 + NS; ++b) {
-          store_stream(reinterpret_cast<Pack<T>*>(base[b]) + i, v[b][u]);
+        for (int b = 0; b < NS; ++b) {
+          store_stream(reinterpret_cast<Pack<S>*>(srow[b]) + i, vs[b][u]);
         }
       }
     }
@@ -494,20 +524,20 @@ __global__ __launch_bounds__(kThreads) void segment_kernel(SegArgs<P> a) {
   // Remaining elements (a partial last pack, or the whole tile of a segment
   // that cannot take vector accesses), one element per thread and access.
   for (int64_t j = done + threadIdx.x; j < cnt; j += kThreads) {
-    T p = base[0][j * a.k.x.stride_t[0]];
+    T p = prow[j * a.k.x.stride_t[0]];
     const T g = g_src != nullptr ? g_src[j * g_stride] : zero;
-    T st[SS];
+    S st[SS];
     if (load_state) {
 #pragma unroll
-      for (int b = 0; b < NS; ++b) st[b] = base[2 + b][j * a.k.x.stride_t[2 + b]];
+      for (int b = 0; b < NS; ++b) st[b] = srow[b][j * a.k.x.stride_t[2 + b]];
     }
     apply_element<P>(p, g, st, load_state, rep, a.k.maximize);
-    base[0][j * a.k.x.stride_t[0]] = p;
+    prow[j * a.k.x.stride_t[0]] = p;
     if (store_grad) {
       g_dst[j * a.k.x.stride_t[1]] = g;
     }
 #pragma unroll
-    for (int b = 0; b < NS; ++b) base[2 + b][j * a.k.x.stride_t[2 + b]] = st[b];
+    for (int b = 0; b < NS; ++b) srow[b][j * a.k.x.stride_t[2 + b]] = st[b];
   }
 }
 
@@ -592,14 +622,15 @@ bool fill_operands(const ts_rt_buf* bufs, int n, Operands<T>& x, bool grad_optio
   return true;
 }
 
-// The 16-byte path needs unit inner stride and pack-aligned row starts on
-// every (present) operand.
-template <typename T>
-bool rows_vectorizable(const Operands<T>& x, int n) {
+// The vector path needs unit inner stride and pack-aligned row starts on
+// every (present) operand; operands 0 and 1 hold P::T, the rest P::S.
+template <typename P>
+bool rows_vectorizable(const Operands<typename P::T>& x, int n) {
   for (int b = 0; b < n; ++b) {
     if (x.data[b] == nullptr) continue;
+    const size_t elem = b < 2 ? sizeof(typename P::T) : sizeof(typename P::S);
     if (x.stride_t[b] != 1 || x.stride_r[b] % kPack != 0 ||
-        reinterpret_cast<uintptr_t>(x.data[b]) % (sizeof(T) * kPack) != 0) {
+        reinterpret_cast<uintptr_t>(x.data[b]) % (elem * kPack) != 0) {
       return false;
     }
   }
@@ -791,7 +822,7 @@ int launch_dense(const Call& c, int nbufs) {
   };
   return run_step<T>(c, prepare, [&]() -> int {
     const dim3 grid(blocks), block(kThreads);
-    if (c.T % kPack == 0 && rows_vectorizable(a.x, nbufs)) {
+    if (c.T % kPack == 0 && rows_vectorizable<P>(a.x, nbufs)) {
       hipLaunchKernelGGL(stream_kernel<P>, grid, block, 0, c.stream, a);
     } else {
       hipLaunchKernelGGL(element_kernel<P>, grid, block, 0, c.stream, a);
@@ -815,7 +846,7 @@ int launch_segments(const Call& c, int nbufs, const ts_segment* segs, int n_segs
     if (!fill_kargs<P>(c, nbufs, a.k, true) || !segments_valid(segs, n_segs, c.T)) {
       return false;
     }
-    vec_rows = rows_vectorizable(a.k.x, nbufs);
+    vec_rows = rows_vectorizable<P>(a.k.x, nbufs);
     return walk_fits<T>(walk, c.R, vec_rows, a.seg);
   };
   return run_step<T>(c, prepare, [&]() -> int {
@@ -825,32 +856,49 @@ int launch_segments(const Call& c, int nbufs, const ts_segment* segs, int n_segs
 
 // Runs `launch` with the policy that matches the call's flags and the number
 // of (R, T) operands that policy reads.
-template <typename T, typename Launch>
+template <typename T, typename S, typename Launch>
 int adam_dispatch(uint32_t flags, Launch&& launch) {
   const bool amsgrad = (flags & TS_AMSGRAD) != 0;
   const bool adamw = (flags & TS_ADAMW) != 0;
   if (adamw) {
-    if (amsgrad) return launch(AdamPolicy<T, true, true>{}, 5);
-    return launch(AdamPolicy<T, true, false>{}, 4);
+    if (amsgrad) return launch(AdamPolicy<T, true, true, S>{}, 5);
+    return launch(AdamPolicy<T, true, false, S>{}, 4);
   }
-  if (amsgrad) return launch(AdamPolicy<T, false, true>{}, 5);
-  return launch(AdamPolicy<T, false, false>{}, 4);
+  if (amsgrad) return launch(AdamPolicy<T, false, true, S>{}, 5);
+  return launch(AdamPolicy<T, false, false, S>{}, 4);
 }
 
-template <typename T, typename Launch>
+template <typename T, typename S, typename Launch>
 int sgd_dispatch(uint32_t flags, bool has_buf, Launch&& launch) {
   const bool nesterov = (flags & TS_NESTEROV) != 0;
   if (has_buf) {
-    if (nesterov) return launch(SgdPolicy<T, true, true>{}, 3);
-    return launch(SgdPolicy<T, true, false>{}, 3);
+    if (nesterov) return launch(SgdPolicy<T, true, true, S>{}, 3);
+    return launch(SgdPolicy<T, true, false, S>{}, 3);
   }
   if (nesterov) return kInvalid;
-  return launch(SgdPolicy<T, false, false>{}, 2);
+  return launch(SgdPolicy<T, false, false, S>{}, 2);
 }
 
-template <typename T, typename Launch>
+template <typename T, typename S, typename Launch>
 int adagrad_dispatch(Launch&& launch) {
-  return launch(AdagradPolicy<T>{}, 3);
+  return launch(AdagradPolicy<T, S>{}, 3);
+}
+
+template <typename U>
+struct type_tag {
+  using type = U;
+};
+
+// The optimizer-state type of a call: the parameter type, or bfloat16 under
+// TS_STATE_BF16 (float32 parameters only).
+template <typename T, typename Launch>
+int with_state_type(uint32_t flags, Launch&& launch) {
+  if ((flags & TS_STATE_BF16) == 0) return launch(type_tag<T>{});
+  if constexpr (std::is_same<T, float>::value) {
+    return launch(type_tag<bf16_t>{});
+  } else {
+    return kInvalid;
+  }
 }
 
 template <template <typename> class Body, typename... Args>
@@ -872,8 +920,11 @@ int launch_any(const Call& c, int nbufs, const ts_segment* segs, int n_segs, boo
 template <typename T>
 struct AdamBody {
   static int run(const Call& c, const ts_segment* segs, int n_segs, bool segmented) {
-    return adam_dispatch<T>(c.flags, [&](auto policy, int nbufs) {
-      return launch_any<decltype(policy)>(c, nbufs, segs, n_segs, segmented);
+    return with_state_type<T>(c.flags, [&](auto state) {
+      using S = typename decltype(state)::type;
+      return adam_dispatch<T, S>(c.flags, [&](auto policy, int nbufs) {
+        return launch_any<decltype(policy)>(c, nbufs, segs, n_segs, segmented);
+      });
     });
   }
 };
@@ -882,8 +933,11 @@ template <typename T>
 struct SgdBody {
   static int run(const Call& c, const ts_segment* segs, int n_segs, bool segmented) {
     const bool has_buf = c.bufs != nullptr && c.bufs[2].data != nullptr;
-    return sgd_dispatch<T>(c.flags, has_buf, [&](auto policy, int nbufs) {
-      return launch_any<decltype(policy)>(c, nbufs, segs, n_segs, segmented);
+    return with_state_type<T>(c.flags, [&](auto state) {
+      using S = typename decltype(state)::type;
+      return sgd_dispatch<T, S>(c.flags, has_buf, [&](auto policy, int nbufs) {
+        return launch_any<decltype(policy)>(c, nbufs, segs, n_segs, segmented);
+      });
     });
   }
 };
@@ -891,8 +945,11 @@ struct SgdBody {
 template <typename T>
 struct AdagradBody {
   static int run(const Call& c, const ts_segment* segs, int n_segs, bool segmented) {
-    return adagrad_dispatch<T>([&](auto policy, int nbufs) {
-      return launch_any<decltype(policy)>(c, nbufs, segs, n_segs, segmented);
+    return with_state_type<T>(c.flags, [&](auto state) {
+      using S = typename decltype(state)::type;
+      return adagrad_dispatch<T, S>([&](auto policy, int nbufs) {
+        return launch_any<decltype(policy)>(c, nbufs, segs, n_segs, segmented);
+      });
     });
   }
 };
@@ -954,7 +1011,7 @@ using churten::make_call;
 
 extern "C" {
 
-int ts_version(void) { return 110; }
+int ts_version(void) { return 120; }
 
 int ts_bump_steps(ts_dtype dtype, void* state_steps, const uint8_t* active_mask,
                   int64_t R, void* out_zero, void* stream) {

@@ -13,10 +13,14 @@
 //   torch/include/ATen/native/hip/fused_adam_utils.cuh:28-92   (adam_math)
 //   torch/include/ATen/native/hip/fused_adam_utils.cuh:131-139 (bias corrections)
 //   torch/include/ATen/native/hip/fused_adagrad_utils.cuh:16-50, 75-81
-// Multiply-add contraction is left to the compiler (hipcc's default
-// -ffp-contract=fast), exactly as for those headers; float division and sqrt
-// are IEEE correctly rounded (hipcc's default). Do not reassociate or hand-fuse
-// these expressions: each one is checked bit-for-bit against torch on the GPU.
+// torch compiles those headers with hipcc's default -ffp-contract=fast, so
+// each `a * b + c` there is one fused multiply-add. Here every such
+// contraction is written out as an explicit fma in the order torch's build
+// fuses it (the order the parity tests pin on the GPU), so
+// the result does not depend on which kernel the math is inlined into or on
+// what the compiler decides there. Float division and sqrt are IEEE correctly
+// rounded (hipcc's default). Each function is checked bit-for-bit against
+// torch on the GPU.
 #pragma once
 
 #include <hip/hip_runtime.h>
@@ -81,13 +85,20 @@ __device__ __forceinline__ void adam_element(
   }
   if (h.weight_decay != 0) {
     if constexpr (ADAMW) {
-      param -= h.lr * h.weight_decay * param;
+      // param -= lr * weight_decay * param
+      param = static_cast<opmath_t>(
+          ::fma(-(h.lr * h.weight_decay), double(param), double(param)));
     } else {
-      grad += param * h.weight_decay;
+      // grad += param * weight_decay
+      grad = static_cast<opmath_t>(::fma(double(param), h.weight_decay, double(grad)));
     }
   }
-  exp_avg = h.beta1 * exp_avg + (1 - h.beta1) * grad;
-  exp_avg_sq = h.beta2 * exp_avg_sq + (1 - h.beta2) * grad * grad;
+  // exp_avg = beta1 * exp_avg + (1 - beta1) * grad
+  exp_avg = static_cast<opmath_t>(
+      ::fma(h.beta1, double(exp_avg), (1 - h.beta1) * double(grad)));
+  // exp_avg_sq = beta2 * exp_avg_sq + (1 - beta2) * grad * grad
+  exp_avg_sq = static_cast<opmath_t>(
+      ::fma(h.beta2, double(exp_avg_sq), ((1 - h.beta2) * double(grad)) * double(grad)));
   const opmath_t step_size = h.lr / bias_correction1;
   opmath_t denom;
   if constexpr (AMSGRAD) {
@@ -119,28 +130,41 @@ template <typename hyper_t> struct SgdHyper {
   hyper_t weight_decay, momentum, lr, dampening;
 };
 
+// Every multiply-add is an explicit fma, in the order torch's ROCm
+// `_fused_sgd_` contracts them (pinned on the MI355X for float64 parameters,
+// where the products are inexact and the contraction shows: weight decay
+// fma(wd, p, g), buffer fma(mom, buf, (1 - damp) * g), Nesterov
+// fma(mom, buf, g), update fma(-lr, g, p)). For float32 parameters with
+// double hyperparameters the products are exact, so the same code gives the
+// same bits as any contraction would. Writing the fmas out keeps the result
+// independent of which kernel the element math is inlined into.
 template <typename opmath_t, typename hyper_t, bool HAS_BUF, bool NESTEROV>
 __device__ __forceinline__ void sgd_element(
     opmath_t& param, opmath_t grad, opmath_t& momentum_buffer,
     const SgdHyper<hyper_t>& h, const bool maximize, const bool is_first_step) {
+  using acc_t = decltype(hyper_t() * opmath_t());
   if (maximize) {
     grad *= -1.0;
   }
   if (h.weight_decay != 0) {
-    grad += h.weight_decay * param;
+    grad = static_cast<opmath_t>(
+        ::fma(acc_t(h.weight_decay), acc_t(param), acc_t(grad)));
   }
   if constexpr (HAS_BUF) {
-    const auto buf = is_first_step
-        ? grad
-        : (h.momentum * momentum_buffer + (1 - h.dampening) * grad);
-    momentum_buffer = buf;
+    // The new buffer stays in acc_t for the Nesterov term, as in torch.
+    const acc_t buf =
+        is_first_step
+            ? acc_t(grad)
+            : ::fma(acc_t(h.momentum), acc_t(momentum_buffer),
+                    acc_t(1 - h.dampening) * acc_t(grad));
+    momentum_buffer = static_cast<opmath_t>(buf);
     if constexpr (NESTEROV) {
-      grad = grad + h.momentum * buf;
+      grad = static_cast<opmath_t>(::fma(acc_t(h.momentum), buf, acc_t(grad)));
     } else {
-      grad = buf;
+      grad = static_cast<opmath_t>(buf);
     }
   }
-  param -= h.lr * grad;
+  param = static_cast<opmath_t>(::fma(-acc_t(h.lr), acc_t(grad), acc_t(param)));
 }
 
 // ---------------------------------------------------------------------------
@@ -160,16 +184,19 @@ __device__ __forceinline__ void adagrad_element(
     grad = -grad;
   }
   if (h.weight_decay != 0) {
-    grad += param * h.weight_decay;
+    // grad += param * weight_decay
+    grad = static_cast<opmath_t>(::fma(double(param), h.weight_decay, double(grad)));
   }
-  state_sum += grad * grad;
-  param = param - h.corrected_lr * grad / (std::sqrt(state_sum) + h.eps);
+  // state_sum += grad * grad, in the math type
+  state_sum = ::fma(grad, grad, state_sum);
+  param = static_cast<opmath_t>(double(param) - h.corrected_lr * double(grad) /
+                                                    (double(std::sqrt(state_sum)) + h.eps));
 }
 
 // corrected_lr = lr / (1 + (step - 1) * lr_decay), with `step - 1` in float.
 __device__ __forceinline__ double adagrad_corrected_lr(
     const double lr, const double lr_decay, const float step) {
-  const auto denom = 1 + (step - 1) * lr_decay;
+  const double denom = ::fma(static_cast<double>(step - 1), lr_decay, 1.0);
   return lr / denom;
 }
 

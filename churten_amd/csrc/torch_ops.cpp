@@ -26,6 +26,8 @@
 // Added here, because the kernel trusts its operands: every (R, T) operand must
 // match params' shape, dtype and device, and every (R,) input must have R
 // elements on params' device -- the reference would read out of bounds.
+// Extension: the optimizer-state buffers may be bfloat16 next to float32
+// params (all of them, TS_STATE_BF16); the reference rejects mixed dtypes.
 //
 // The common case (steps in the param dtype, a bool mask, contiguous (R,)
 // vectors) costs two launches: the step bump (which also writes the zero
@@ -87,6 +89,26 @@ void check_like(const at::Tensor& params, const at::Tensor& t, const char* op,
   TORCH_CHECK(t.scalar_type() == params.scalar_type(), op, ": ", name,
               " must have params' dtype ", params.scalar_type(), ", got ",
               t.scalar_type());
+  TORCH_CHECK(t.device() == params.device(), op, ": ", name,
+              " must be on ", params.device(), ", got ", t.device());
+}
+
+// Optimizer state may be bfloat16 next to float32 params (TS_STATE_BF16);
+// the first state buffer decides, and every state buffer must agree.
+uint32_t state_flag(const at::Tensor& params, const at::Tensor& first_state) {
+  return params.scalar_type() == at::kFloat && first_state.scalar_type() == at::kBFloat16
+             ? TS_STATE_BF16
+             : 0u;
+}
+
+void check_state(const at::Tensor& params, const at::Tensor& t, uint32_t sflag,
+                 const char* op, const char* name) {
+  TORCH_CHECK(t.dim() == 2 && t.sizes() == params.sizes(), op, ": ", name,
+              " must have params' shape ", params.sizes(), ", got ", t.sizes());
+  const auto want = sflag != 0 ? at::kBFloat16 : params.scalar_type();
+  TORCH_CHECK(t.scalar_type() == want, op, ": ", name, " must have dtype ", want,
+              " (params' dtype, or bfloat16 for every state buffer next to float32 params),"
+              " got ", t.scalar_type());
   TORCH_CHECK(t.device() == params.device(), op, ": ", name,
               " must be on ", params.device(), ", got ", t.device());
 }
@@ -216,14 +238,15 @@ at::Tensor adam_step_gpu(at::Tensor params, at::Tensor grads, at::Tensor exp_avg
   check_params(params, op);
   TORCH_CHECK(!amsgrad || max_exp_avg_sqs.has_value(), "amsgrad=True requires max_exp_avg_sqs");
   check_like(params, grads, op, "grads");
-  check_like(params, exp_avgs, op, "exp_avgs");
-  check_like(params, exp_avg_sqs, op, "exp_avg_sqs");
-  if (amsgrad) check_like(params, *max_exp_avg_sqs, op, "max_exp_avg_sqs");
+  const uint32_t sflag = state_flag(params, exp_avgs);
+  check_state(params, exp_avgs, sflag, op, "exp_avgs");
+  check_state(params, exp_avg_sqs, sflag, op, "exp_avg_sqs");
+  if (amsgrad) check_state(params, *max_exp_avg_sqs, sflag, op, "max_exp_avg_sqs");
   const c10::DeviceGuard guard(params.device());
   const Prepared p = prepare(
       params, state_steps, active_mask, {&lr, &beta1, &beta2, &eps, &weight_decay},
       {"lr", "beta1", "beta2", "eps", "weight_decay"},
-      (amsgrad ? TS_AMSGRAD : 0u) | (decoupled_weight_decay ? TS_ADAMW : 0u) |
+      sflag | (amsgrad ? TS_AMSGRAD : 0u) | (decoupled_weight_decay ? TS_ADAMW : 0u) |
           (maximize ? TS_MAXIMIZE : 0u),
       op);
   const ts_rt_buf bufs[5] = {rt_buf(params), rt_buf(grads), rt_buf(exp_avgs),
@@ -244,12 +267,18 @@ at::Tensor sgd_step_gpu(at::Tensor params, at::Tensor grads,
   check_params(params, op);
   TORCH_CHECK(!nesterov || momentum_buffers.has_value(), "nesterov=True requires momentum_buffers");
   check_like(params, grads, op, "grads");
-  if (momentum_buffers.has_value()) check_like(params, *momentum_buffers, op, "momentum_buffers");
+  const uint32_t sflag =
+      momentum_buffers.has_value() ? state_flag(params, *momentum_buffers) : 0u;
+  if (momentum_buffers.has_value()) {
+    check_state(params, *momentum_buffers, sflag, op, "momentum_buffers");
+  }
   const c10::DeviceGuard guard(params.device());
   const Prepared p = prepare(params, state_steps, active_mask,
                              {&lr, &momentum, &dampening, &weight_decay},
                              {"lr", "momentum", "dampening", "weight_decay"},
-                             (nesterov ? TS_NESTEROV : 0u) | (maximize ? TS_MAXIMIZE : 0u), op);
+                             sflag | (nesterov ? TS_NESTEROV : 0u) |
+                                 (maximize ? TS_MAXIMIZE : 0u),
+                             op);
   const ts_rt_buf bufs[3] = {rt_buf(params), rt_buf(grads),
                              momentum_buffers.has_value() ? rt_buf(*momentum_buffers) : kNoBuf};
   check_status(ts_sgd_step(bufs, p.dtype, p.steps.data_ptr(), p.h(0), p.h(1), p.h(2), p.h(3),
@@ -265,12 +294,13 @@ at::Tensor adagrad_step_gpu(at::Tensor params, at::Tensor grads, at::Tensor stat
   constexpr const char* op = "torchstrap::adagrad_step_";
   check_params(params, op);
   check_like(params, grads, op, "grads");
-  check_like(params, state_sums, op, "state_sums");
+  const uint32_t sflag = state_flag(params, state_sums);
+  check_state(params, state_sums, sflag, op, "state_sums");
   const c10::DeviceGuard guard(params.device());
   const Prepared p = prepare(params, state_steps, active_mask,
                              {&lr, &lr_decay, &weight_decay, &eps},
                              {"lr", "lr_decay", "weight_decay", "eps"},
-                             maximize ? TS_MAXIMIZE : 0u, op);
+                             sflag | (maximize ? TS_MAXIMIZE : 0u), op);
   const ts_rt_buf bufs[3] = {rt_buf(params), rt_buf(grads), rt_buf(state_sums)};
   check_status(ts_adagrad_step(bufs, p.dtype, p.steps.data_ptr(), p.h(0), p.h(1), p.h(2),
                                p.h(3), p.m(), p.R, p.T, p.flags, p.out.data_ptr(), p.stream),
@@ -306,15 +336,16 @@ at::Tensor adam_step_segments_gpu(at::Tensor params, at::TensorList grads, at::I
   check_params(params, op);
   TORCH_CHECK(!amsgrad || max_exp_avg_sqs.has_value(), "amsgrad=True requires max_exp_avg_sqs");
   if (grads_out.has_value()) check_like(params, *grads_out, op, "grads_out");
-  check_like(params, exp_avgs, op, "exp_avgs");
-  check_like(params, exp_avg_sqs, op, "exp_avg_sqs");
-  if (amsgrad) check_like(params, *max_exp_avg_sqs, op, "max_exp_avg_sqs");
+  const uint32_t sflag = state_flag(params, exp_avgs);
+  check_state(params, exp_avgs, sflag, op, "exp_avgs");
+  check_state(params, exp_avg_sqs, sflag, op, "exp_avg_sqs");
+  if (amsgrad) check_state(params, *max_exp_avg_sqs, sflag, op, "max_exp_avg_sqs");
   const c10::DeviceGuard guard(params.device());
   const SegTable st = segments_of(params, grads, cols, op);
   const Prepared p = prepare(
       params, state_steps, active_mask, {&lr, &beta1, &beta2, &eps, &weight_decay},
       {"lr", "beta1", "beta2", "eps", "weight_decay"},
-      (amsgrad ? TS_AMSGRAD : 0u) | (decoupled_weight_decay ? TS_ADAMW : 0u) |
+      sflag | (amsgrad ? TS_AMSGRAD : 0u) | (decoupled_weight_decay ? TS_ADAMW : 0u) |
           (maximize ? TS_MAXIMIZE : 0u),
       op);
   const ts_rt_buf bufs[5] = {rt_buf(params), grads_out.has_value() ? rt_buf(*grads_out) : kNoBuf,
@@ -338,13 +369,19 @@ at::Tensor sgd_step_segments_gpu(at::Tensor params, at::TensorList grads, at::In
   check_params(params, op);
   TORCH_CHECK(!nesterov || momentum_buffers.has_value(), "nesterov=True requires momentum_buffers");
   if (grads_out.has_value()) check_like(params, *grads_out, op, "grads_out");
-  if (momentum_buffers.has_value()) check_like(params, *momentum_buffers, op, "momentum_buffers");
+  const uint32_t sflag =
+      momentum_buffers.has_value() ? state_flag(params, *momentum_buffers) : 0u;
+  if (momentum_buffers.has_value()) {
+    check_state(params, *momentum_buffers, sflag, op, "momentum_buffers");
+  }
   const c10::DeviceGuard guard(params.device());
   const SegTable st = segments_of(params, grads, cols, op);
   const Prepared p = prepare(params, state_steps, active_mask,
                              {&lr, &momentum, &dampening, &weight_decay},
                              {"lr", "momentum", "dampening", "weight_decay"},
-                             (nesterov ? TS_NESTEROV : 0u) | (maximize ? TS_MAXIMIZE : 0u), op);
+                             sflag | (nesterov ? TS_NESTEROV : 0u) |
+                                 (maximize ? TS_MAXIMIZE : 0u),
+                             op);
   const ts_rt_buf bufs[3] = {rt_buf(params), grads_out.has_value() ? rt_buf(*grads_out) : kNoBuf,
                              momentum_buffers.has_value() ? rt_buf(*momentum_buffers) : kNoBuf};
   check_status(ts_sgd_step_segments(bufs, st.segs.data(), static_cast<int>(st.segs.size()),
@@ -363,13 +400,14 @@ at::Tensor adagrad_step_segments_gpu(at::Tensor params, at::TensorList grads,
   constexpr const char* op = "churten::adagrad_step_segments_";
   check_params(params, op);
   if (grads_out.has_value()) check_like(params, *grads_out, op, "grads_out");
-  check_like(params, state_sums, op, "state_sums");
+  const uint32_t sflag = state_flag(params, state_sums);
+  check_state(params, state_sums, sflag, op, "state_sums");
   const c10::DeviceGuard guard(params.device());
   const SegTable st = segments_of(params, grads, cols, op);
   const Prepared p = prepare(params, state_steps, active_mask,
                              {&lr, &lr_decay, &weight_decay, &eps},
                              {"lr", "lr_decay", "weight_decay", "eps"},
-                             maximize ? TS_MAXIMIZE : 0u, op);
+                             sflag | (maximize ? TS_MAXIMIZE : 0u), op);
   const ts_rt_buf bufs[3] = {rt_buf(params), grads_out.has_value() ? rt_buf(*grads_out) : kNoBuf,
                              rt_buf(state_sums)};
   check_status(ts_adagrad_step_segments(bufs, st.segs.data(), static_cast<int>(st.segs.size()),

@@ -22,11 +22,14 @@ __all__ = ["Adagrad", "adagrad_step_"]
 class Adagrad(metaclass=GradientTransformation):
     @classmethod
     def init(cls, state: State, *, lr=1e-2, lr_decay=0.0, weight_decay=0.0, eps=1e-10,
-             initial_accumulator_value=0.0, maximize: bool = False) -> State:
+             initial_accumulator_value=0.0, maximize: bool = False,
+             state_dtype: torch.dtype | None = None) -> State:
+        """``state_dtype=torch.bfloat16`` keeps the accumulators in bfloat16
+        next to float32 params."""
         for key, value in (("lr", lr), ("lr_decay", lr_decay), ("weight_decay", weight_decay),
                            ("eps", eps), ("state_steps", 0)):
             state.add_optim_state(key, value)
-        state.add_optim_state("state_sums", per_param=True)
+        state.add_optim_state("state_sums", per_param=True, dtype=state_dtype)
         sums = state.optimizer_state["state_sums"]
         if isinstance(initial_accumulator_value, torch.Tensor):
             sums.copy_(initial_accumulator_value.expand_as(sums))

@@ -26,14 +26,17 @@ class Adam(metaclass=GradientTransformation):
     @classmethod
     def init(cls, state: State, *, lr=1e-3, beta1=0.9, beta2=0.999, eps=1e-8,
              weight_decay=1e-2, amsgrad: bool = False, maximize: bool = False,
-             decoupled_weight_decay: bool = True) -> State:
+             decoupled_weight_decay: bool = True,
+             state_dtype: torch.dtype | None = None) -> State:
+        """``state_dtype=torch.bfloat16`` keeps the moments in bfloat16 next to
+        float32 params (20 instead of 28 bytes per element and step)."""
         for key, value in (("lr", lr), ("beta1", beta1), ("beta2", beta2), ("eps", eps),
                            ("weight_decay", weight_decay), ("state_steps", 0)):
             state.add_optim_state(key, value)
-        state.add_optim_state("exp_avgs", per_param=True)
-        state.add_optim_state("exp_avg_sqs", per_param=True)
+        state.add_optim_state("exp_avgs", per_param=True, dtype=state_dtype)
+        state.add_optim_state("exp_avg_sqs", per_param=True, dtype=state_dtype)
         if amsgrad:
-            state.add_optim_state("max_exp_avg_sqs", per_param=True)
+            state.add_optim_state("max_exp_avg_sqs", per_param=True, dtype=state_dtype)
         state.add_optim_meta("amsgrad", amsgrad)
         state.add_optim_meta("maximize", maximize)
         state.add_optim_meta("decoupled_weight_decay", decoupled_weight_decay)

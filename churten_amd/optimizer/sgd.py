@@ -29,7 +29,10 @@ def _any_nonzero(value) -> bool:
 class SGD(metaclass=GradientTransformation):
     @classmethod
     def init(cls, state: State, *, lr=1e-3, momentum=0.0, dampening=0.0, weight_decay=0.0,
-             nesterov: bool = False, maximize: bool = False) -> State:
+             nesterov: bool = False, maximize: bool = False,
+             state_dtype: torch.dtype | None = None) -> State:
+        """``state_dtype=torch.bfloat16`` keeps the momentum buffers in bfloat16
+        next to float32 params."""
         if nesterov and (not _any_nonzero(momentum) or _any_nonzero(dampening)):
             raise ValueError("Nesterov momentum requires a non-zero momentum and zero dampening")
         for key, value in (("lr", lr), ("momentum", momentum), ("dampening", dampening),
@@ -37,7 +40,7 @@ class SGD(metaclass=GradientTransformation):
             state.add_optim_state(key, value)
         has_momentum = _any_nonzero(momentum)
         if has_momentum:
-            state.add_optim_state("momentum_buffers", per_param=True)
+            state.add_optim_state("momentum_buffers", per_param=True, dtype=state_dtype)
         state.add_optim_meta("nesterov", nesterov)
         state.add_optim_meta("maximize", maximize)
         state.add_optim_meta("has_momentum", has_momentum)

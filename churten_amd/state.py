@@ -194,25 +194,31 @@ class State:
         return _GradScatter(self.grads, self.param_meta)
 
     # -- optimizer state ---------------------------------------------------
-    def add_optim_state(self, key: str, value: Any = None, per_param: bool = False) -> None:
-        self.optimizer_state[key] = self.like_tensor(value, per_param=per_param)
+    def add_optim_state(self, key: str, value: Any = None, per_param: bool = False,
+                        dtype: torch.dtype | None = None) -> None:
+        self.optimizer_state[key] = self.like_tensor(value, per_param=per_param, dtype=dtype)
 
     def add_optim_meta(self, key: str, value: Any) -> None:
         """A static, non-tensor optimizer flag (amsgrad, maximize, ...)."""
         self.optimizer_state[key] = value
 
-    def like_tensor(self, value: Any = None, per_param: bool = False) -> torch.Tensor:
+    def like_tensor(self, value: Any = None, per_param: bool = False,
+                    dtype: torch.dtype | None = None) -> torch.Tensor:
         """``(N,)`` (or ``(N, T)`` if ``per_param``) tensor in the param dtype:
-        zeros for None, filled for a number, broadcast copy of a tensor."""
+        zeros for None, filled for a number, broadcast copy of a tensor. A
+        ``per_param`` buffer may take another ``dtype`` (bfloat16 optimizer
+        state next to float32 params)."""
         like = dict(dtype=self.param_buffer_dtype, device=self.device)
+        if per_param:
+            out = torch.zeros_like(self.flat_params, dtype=dtype or self.param_buffer_dtype,
+                                   memory_format=torch.preserve_format)
+            if isinstance(value, torch.Tensor):
+                out.copy_(torch.as_tensor(value, **like).expand_as(out))
+            elif value is not None:
+                out.fill_(value)
+            return out
         if value is None:
-            if per_param:
-                return torch.zeros_like(self.flat_params, memory_format=torch.preserve_format)
             return torch.zeros(self.batch_size, **like)
         if isinstance(value, torch.Tensor):
-            v = torch.as_tensor(value, **like)
-            return (v.expand_as(self.flat_params) if per_param else v.expand(self.batch_size)).clone()
-        if per_param:
-            return torch.full_like(self.flat_params, fill_value=value,
-                                   memory_format=torch.preserve_format)
+            return torch.as_tensor(value, **like).expand(self.batch_size).clone()
         return torch.full(self.batch_size, fill_value=value, **like)

@@ -36,6 +36,8 @@
  *     arithmetic runs.
  *   - (R,) vectors (state_steps and the hyperparameters) are contiguous and
  *     in the parameter dtype; active_mask is R contiguous bytes (0 = frozen).
+ *   - Optimizer-state buffers are in the parameter dtype, or bfloat16 with
+ *     TS_STATE_BF16.
  *   - A frozen replica's rows are neither read nor written.
  *   - If TS_BUMP_STEPS is set, state_steps[r] += active_mask[r] is applied
  *     first (in the parameter dtype), and the update then reads the bumped
@@ -73,6 +75,14 @@ typedef enum ts_dtype {
 #define TS_MAXIMIZE 0x4u    /* all: ascend instead of descend */
 #define TS_NESTEROV 0x8u    /* SGD: Nesterov momentum (needs a buffer) */
 #define TS_BUMP_STEPS 0x10u /* all: state_steps += active_mask first */
+/* all: the optimizer-state buffers (bufs[2..]: exp_avgs, exp_avg_sqs,
+ * max_exp_avg_sqs, momentum_buffers, state_sums) hold bfloat16 while params
+ * and grads hold `dtype`, which must be TS_FLOAT32. The element math is the
+ * float32 math of the same op; state is widened on load and rounded to
+ * nearest-even on store, so parameters come out as the float32 op computes
+ * them from the widened state. Low-precision optimizer state has no
+ * counterpart in the reference operators (its README roadmap lists it). */
+#define TS_STATE_BF16 0x20u
 
 /* A per-parameter gradient: an (R, numel) tensor with element (r, j) at
  * data + r*stride_r + j, standing for columns [col, col + numel) of the

@@ -41,10 +41,18 @@
  * Layout: contiguous row-major (R, T) float32 arrays; `steps` is (R,) float32
  * and is bumped in place (steps[r] += mask[r]) before the update, as every
  * reference operator does (cuda/adam.cu:277, cpu/adam.cpp:394).
+ *
+ * bfloat16 optimizer state (this build's extension; the reference operators
+ * reject mixed dtypes): the state is held here as float32 arrays of
+ * bfloat16-representable values; the step is the float32 step above, after
+ * which oracle_round_bf16_rows rounds the active rows' state to nearest-even
+ * bfloat16. Pinned against torch's own float -> bfloat16 conversion
+ * (tests/test_oracle_bf16_state.py).
  */
 #include <math.h>
 #include <stddef.h>
 #include <stdint.h>
+#include <string.h>
 
 #define ORACLE_DEVICE 0
 #define ORACLE_CPU 1
@@ -389,4 +397,31 @@ int oracle_adagrad_step(int form, float* p, const float* g, float* s,
   return 0;
 }
 
-int oracle_version(void) { return 1; }
+/* ======================================================================== */
+/* bfloat16 state                                                           */
+/* ======================================================================== */
+
+/* float32 -> bfloat16 -> float32, round to nearest even; NaN -> 0x7FC0. */
+static float round_bf16(float x) {
+  uint32_t u;
+  memcpy(&u, &x, sizeof u);
+  if ((u & 0x7fffffffu) > 0x7f800000u) {
+    u = 0x7fc00000u;
+  } else {
+    u += 0x7fffu + ((u >> 16) & 1u);
+    u &= 0xffff0000u;
+  }
+  memcpy(&x, &u, sizeof x);
+  return x;
+}
+
+/* Rounds rows r with mask[r] != 0 of the (R, T) array x to bfloat16 in place. */
+int oracle_round_bf16_rows(float* x, const uint8_t* mask, int64_t R, int64_t T) {
+  for (int64_t r = 0; r < R; ++r) {
+    if (!mask[r]) continue;
+    for (int64_t t = 0; t < T; ++t) x[r * T + t] = round_bf16(x[r * T + t]);
+  }
+  return 0;
+}
+
+int oracle_version(void) { return 2; }

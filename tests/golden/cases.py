@@ -104,8 +104,25 @@ def _mask(c, R):
     return m
 
 
-def make_inputs(c):
-    """All inputs of a case as float32 numpy arrays (state is (R, T))."""
+def to_bf16_values(a: np.ndarray) -> np.ndarray:
+    """float32 array of the nearest-even bfloat16 values of ``a`` (finite inputs)."""
+    u = np.ascontiguousarray(a, dtype=F32).view(np.uint32).astype(np.uint64)
+    u = (u + 0x7FFF + ((u >> 16) & 1)) & 0xFFFF0000
+    return u.astype(np.uint32).view(F32)
+
+
+def make_inputs(c, state_bf16=False):
+    """All inputs of a case as float32 numpy arrays (state is (R, T)). With
+    ``state_bf16`` the optimizer-state arrays start bfloat16-representable."""
+    x = _make_inputs(c)
+    if state_bf16:
+        for k in ("m", "v", "mx", "mb", "s"):
+            if x.get(k) is not None:
+                x[k] = to_bf16_values(x[k])
+    return x
+
+
+def _make_inputs(c):
     rng = np.random.Generator(np.random.PCG64(c["seed"]))
     R, T = c["R"], c["T"]
 
@@ -160,25 +177,26 @@ def state_names(c, x):
     return ["p", "s"]
 
 
-def run_oracle(c, form, unit_stride=True):
-    """Runs the case through the C oracle; returns {name: array} incl. steps."""
+def run_oracle(c, form, unit_stride=True, state_bf16=False):
+    """Runs the case through the C oracle; returns {name: array} incl. steps.
+    ``state_bf16``: bfloat16 optimizer state next to float32 params."""
     from oracle import oracle as O
 
-    x = make_inputs(c)
+    x = make_inputs(c, state_bf16)
+    kw = dict(unit_stride=unit_stride, state_bf16=state_bf16)
     for g in x["grads"]:
         if c["op"] == "adam":
             O.adam_step(form, x["p"], g, x["m"], x["v"], x["mx"], x["steps"], x["lr"],
                         x["beta1"], x["beta2"], x["eps"], x["wd"], x["mask"],
                         amsgrad=c["amsgrad"], maximize=c["maximize"],
-                        decoupled_weight_decay=c["decoupled"], unit_stride=unit_stride)
+                        decoupled_weight_decay=c["decoupled"], **kw)
         elif c["op"] == "sgd":
             O.sgd_step(form, x["p"], g, x["mb"], x["steps"], x["lr"], x["momentum"],
                        x["dampening"], x["wd"], x["mask"], nesterov=c["nesterov"],
-                       maximize=c["maximize"], unit_stride=unit_stride)
+                       maximize=c["maximize"], **kw)
         else:
             O.adagrad_step(form, x["p"], g, x["s"], x["steps"], x["lr"], x["lr_decay"],
-                           x["wd"], x["eps"], x["mask"], maximize=c["maximize"],
-                           unit_stride=unit_stride)
+                           x["wd"], x["eps"], x["mask"], maximize=c["maximize"], **kw)
     out = {k: x[k] for k in state_names(c, x)}
     out["steps"] = x["steps"]
     return out

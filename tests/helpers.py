@@ -24,12 +24,35 @@ def to_layout(a: np.ndarray, dev, strided: bool) -> torch.Tensor:
     return backing
 
 
-def run_hip(c, strided: bool = False, dev: str = "cuda"):
+STATE_NAMES = ("m", "v", "mx", "mb", "s")
+
+
+def to_layout_tensor(t: torch.Tensor, strided: bool) -> torch.Tensor:
+    """The same values in a transposed-backing (R, T) view when ``strided``."""
+    if not strided:
+        return t
+    R, T = t.shape
+    backing = torch.empty(T, R, dtype=t.dtype, device=t.device).t()
+    backing.copy_(t)
+    return backing
+
+
+def run_hip(c, strided: bool = False, dev: str = "cuda", state_bf16: bool = False,
+            state_dtype=None):
+    """``state_bf16``: the case's optimizer state starts bfloat16-valued and is
+    held in bfloat16 tensors (params and grads stay float32), unless
+    ``state_dtype`` names another dtype for those tensors. Outputs are returned
+    widened to float32."""
     import churten_amd.kernels  # noqa: F401
 
-    x = C.make_inputs(c)
+    x = C.make_inputs(c, state_bf16)
     names = C.state_names(c, x)
     st = {k: to_layout(x[k], dev, strided) for k in names}
+    if state_bf16 and state_dtype in (None, torch.bfloat16):
+        for k in names:
+            if k in STATE_NAMES:
+                t = st[k].to(torch.bfloat16)
+                st[k] = t if not strided else to_layout_tensor(t, strided)
 
     def vec(k):
         return torch.from_numpy(x[k].copy()).to(dev)
@@ -51,8 +74,9 @@ def run_hip(c, strided: bool = False, dev: str = "cuda"):
         else:
             ops.adagrad_step_(st["p"], gt, st["s"], steps, vec("lr"), vec("lr_decay"),
                               vec("wd"), vec("eps"), mask, maximize=c["maximize"])
-    torch.cuda.synchronize()
-    out = {k: st[k].contiguous().cpu().numpy() for k in names}
+    if torch.device(dev).type == "cuda":
+        torch.cuda.synchronize()
+    out = {k: st[k].float().contiguous().cpu().numpy() for k in names}
     out["steps"] = steps.cpu().numpy()
     return out
 

@@ -56,7 +56,7 @@ def test_library_exports_every_declared_symbol():
     lib = ctypes.CDLL(str(LIB))
     for name in declared_symbols():
         assert hasattr(lib, name), name
-    assert lib.ts_version() == 110
+    assert lib.ts_version() == 120
 
 
 def test_invalid_arguments_rejected_before_any_launch():
@@ -110,6 +110,18 @@ def test_bad_segment_tables_rejected_before_any_launch(segs):
                                         fake, fake, R, T, flags, None, None) == 1
     assert lib.ts_scatter_segments(table, len(segs), 0, fake, ctypes.c_int64(16), T, R,
                                    None) == 1
+
+
+def test_bf16_state_flag_needs_float32_params():
+    lib = ctypes.CDLL(str(LIB))
+    fake = ctypes.c_void_p(0x10000)
+    bufs = (RTBuf * 5)(*[RTBuf(0x10000 * (i + 1), 16, 1) for i in range(5)])
+    R, T = ctypes.c_int64(2), ctypes.c_int64(16)
+    for dtype in (1, 2, 3):  # float64, float16, bfloat16 params
+        assert lib.ts_adam_step(bufs, dtype, fake, fake, fake, fake, fake, fake, fake, R, T,
+                                ctypes.c_uint32(0x20 | 0x10), None, None) == 1
+        assert lib.ts_adagrad_step(bufs, dtype, fake, fake, fake, fake, fake, fake, R, T,
+                                   ctypes.c_uint32(0x20), None, None) == 1
 
 
 def test_segmented_calls_reject_a_missing_table_and_nesterov_without_buffer():

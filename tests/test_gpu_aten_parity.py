@@ -34,22 +34,29 @@ def same(name, a, b):
         raise AssertionError(f"{name}: {n}/{a.numel()} elements differ, max {d:.3e}")
 
 
-def _vecs(R, *rows):
-    return [torch.tensor(r[:R], device=DEV, dtype=torch.float32) for r in rows]
+def _vecs(R, *rows, dtype=torch.float32):
+    """float32-rounded hyperparameters, in the parameter dtype."""
+    return [torch.tensor(r[:R], device=DEV, dtype=torch.float32).to(dtype) for r in rows]
 
 
+# float64 parameters: the products inside the update are inexact there, so these
+# cases also pin which multiply-adds torch's build fuses.
+DTYPES = [torch.float32, torch.float64]
+
+
+@pytest.mark.parametrize("dtype", DTYPES, ids=str)
 @pytest.mark.parametrize("T", [64, 45, 70001])
 @pytest.mark.parametrize("amsgrad,maximize,decoupled,wd",
                          list(itertools.product([False, True], [False, True],
                                                 [False, True], [0.0, 1e-2])))
-def test_adam_rows_bit_identical_to_aten(T, amsgrad, maximize, decoupled, wd, R=3):
+def test_adam_rows_bit_identical_to_aten(T, amsgrad, maximize, decoupled, wd, dtype, R=3):
     g = torch.Generator(device=DEV).manual_seed(T)
-    rnd = lambda: torch.randn(R, T, device=DEV, generator=g)
+    rnd = lambda: torch.randn(R, T, device=DEV, generator=g, dtype=dtype)
     p, m, v, mx = rnd(), rnd().abs(), rnd().abs(), rnd().abs()
     lr, b1, b2, eps = _vecs(R, [1e-2, 3e-3, 5e-2], [0.9, 0.8, 0.95],
-                            [0.999, 0.99, 0.9999], [1e-8, 1e-6, 1e-7])
-    wdv = torch.full((R,), f32(wd), device=DEV)
-    steps = torch.zeros(R, device=DEV)
+                            [0.999, 0.99, 0.9999], [1e-8, 1e-6, 1e-7], dtype=dtype)
+    wdv = torch.full((R,), f32(wd), device=DEV, dtype=dtype)
+    steps = torch.zeros(R, device=DEV, dtype=dtype)
     mask = torch.ones(R, dtype=torch.bool, device=DEV)
     ref = [[t[r].clone() for t in (p, m, v, mx)] + [torch.zeros((), device=DEV)]
            for r in range(R)]
@@ -81,18 +88,19 @@ def test_adam_rows_bit_identical_to_aten(T, amsgrad, maximize, decoupled, wd, R=
     c for c in itertools.product([0.0, 0.9], [0.0, 0.3], [0.0, 1e-2], [False, True],
                                  [False, True])
     if not (c[3] and (c[0] == 0.0 or c[1] != 0.0))])
+@pytest.mark.parametrize("dtype", DTYPES, ids=str)
 def test_sgd_rows_bit_identical_to_aten(T, momentum, dampening, wd, nesterov,
-                                        maximize, R=2):
+                                        maximize, dtype, R=2):
     g = torch.Generator(device=DEV).manual_seed(T + 1)
-    rnd = lambda: torch.randn(R, T, device=DEV, generator=g)
+    rnd = lambda: torch.randn(R, T, device=DEV, generator=g, dtype=dtype)
     p = rnd()
     has_buf = momentum != 0.0
     mb = rnd() if has_buf else None
-    (lr,) = _vecs(R, [1e-2, 3e-2])
-    mom = torch.full((R,), f32(momentum), device=DEV)
-    damp = torch.full((R,), f32(dampening), device=DEV)
-    wdv = torch.full((R,), f32(wd), device=DEV)
-    steps = torch.zeros(R, device=DEV)
+    (lr,) = _vecs(R, [1e-2, 3e-2], dtype=dtype)
+    mom = torch.full((R,), f32(momentum), device=DEV, dtype=dtype)
+    damp = torch.full((R,), f32(dampening), device=DEV, dtype=dtype)
+    wdv = torch.full((R,), f32(wd), device=DEV, dtype=dtype)
+    steps = torch.zeros(R, device=DEV, dtype=dtype)
     mask = torch.ones(R, dtype=torch.bool, device=DEV)
     ref = [(p[r].clone(), mb[r].clone() if has_buf else None) for r in range(R)]
     for it in range(3):
@@ -111,21 +119,22 @@ def test_sgd_rows_bit_identical_to_aten(T, momentum, dampening, wd, nesterov,
         same(f"params[{r}]", p[r], ref[r][0])
         if has_buf:
             same(f"momentum_buffers[{r}]", mb[r], ref[r][1])
-    assert torch.equal(steps, torch.full((R,), 3.0, device=DEV))
+    assert torch.equal(steps, torch.full((R,), 3.0, device=DEV, dtype=steps.dtype))
 
 
 @pytest.mark.parametrize("T", [64, 45, 70001])
 @pytest.mark.parametrize("lr_decay,wd,eps,maximize", list(itertools.product(
     [0.0, 1e-2], [0.0, 1e-2], [1e-10, 1e-6], [False, True])))
-def test_adagrad_rows_bit_identical_to_aten(T, lr_decay, wd, eps, maximize, R=2):
+@pytest.mark.parametrize("dtype", DTYPES, ids=str)
+def test_adagrad_rows_bit_identical_to_aten(T, lr_decay, wd, eps, maximize, dtype, R=2):
     g = torch.Generator(device=DEV).manual_seed(T + 2)
-    rnd = lambda: torch.randn(R, T, device=DEV, generator=g)
+    rnd = lambda: torch.randn(R, T, device=DEV, generator=g, dtype=dtype)
     p, s = rnd(), rnd().abs()
-    (lr,) = _vecs(R, [1e-2, 3e-2])
-    lrd = torch.full((R,), f32(lr_decay), device=DEV)
-    wdv = torch.full((R,), f32(wd), device=DEV)
-    ev = torch.full((R,), f32(eps), device=DEV)
-    steps = torch.zeros(R, device=DEV)
+    (lr,) = _vecs(R, [1e-2, 3e-2], dtype=dtype)
+    lrd = torch.full((R,), f32(lr_decay), device=DEV, dtype=dtype)
+    wdv = torch.full((R,), f32(wd), device=DEV, dtype=dtype)
+    ev = torch.full((R,), f32(eps), device=DEV, dtype=dtype)
+    steps = torch.zeros(R, device=DEV, dtype=dtype)
     mask = torch.ones(R, dtype=torch.bool, device=DEV)
     ref = [(p[r].clone(), s[r].clone(), torch.zeros((), device=DEV)) for r in range(R)]
     for _ in range(3):

@@ -105,11 +105,14 @@ def vid(v):
     return op + "-" + "-".join(k for k, x in kw.items() if x)
 
 
-def make_state(op, kw, R, T, dtype, device, gen, strided_state=False):
-    """(params, [state buffers], steps, [hyperparameters], flags)."""
-    def rt(positive=False):
+def make_state(op, kw, R, T, dtype, device, gen, strided_state=False, state_dtype=None):
+    """(params, [state buffers], steps, [hyperparameters], flags); the state
+    buffers are in ``state_dtype`` (default: ``dtype``)."""
+    def rt(positive=False, as_state=True):
         t = torch.randn(R, T, generator=gen).to(dtype)
         t = t.abs() if positive else t
+        if as_state and state_dtype is not None:
+            t = t.to(state_dtype)
         return _to_dev_strided(t, device) if strided_state else t.to(device)
 
     def vec(lo, hi):
@@ -132,7 +135,7 @@ def make_state(op, kw, R, T, dtype, device, gen, strided_state=False):
         st = [rt(True)]
         hyp = [vec(1e-3, 1e-1), vec(0.0, 0.1), vec(0.0, 1e-2), vec(1e-10, 1e-8)]
         flags = dict(kw)
-    return rt(), st, steps, hyp, flags
+    return rt(as_state=False), st, steps, hyp, flags
 
 
 def _to_dev_strided(t, device):
@@ -166,13 +169,14 @@ def clone_all(xs):
 
 
 def run_both(device, op, kw, kind, dtype, with_out, strided_grads, strided_state, seed,
-             n_steps=2):
+             n_steps=2, state_dtype=None):
     """Runs ``n_steps`` segmented steps and the same steps as scatter +
     consolidated update, from identical starting state; returns both."""
     R = 5
     shapes, cols, T = layout(kind, seed)
     gen = torch.Generator().manual_seed(seed + 100)
-    p, st, steps, hyp, flags = make_state(op, kw, R, T, dtype, device, gen, strided_state)
+    p, st, steps, hyp, flags = make_state(op, kw, R, T, dtype, device, gen, strided_state,
+                                          state_dtype)
     mask = torch.tensor([True, False, True, True, False], device=device)
     G0 = torch.randn(R, T, generator=gen).to(device, dtype)  # stale gradient contents
     a = dict(p=p, st=st, steps=steps, G=G0.clone() if with_out else None)
@@ -224,6 +228,18 @@ def test_gpu_segments_dtypes_and_strided_grads(variant, dtype):
     op, kw = variant
     a, b = run_both("cuda", op, kw, "ragged", dtype, True, strided_grads=True,
                     strided_state=False, seed=5)
+    torch.cuda.synchronize()
+    assert_same(a, b, True)
+
+
+@pytest.mark.gpu
+@pytest.mark.parametrize("variant", VARIANTS, ids=vid)
+@pytest.mark.parametrize("kind", ["state", "ragged", "many"])
+def test_gpu_segments_bf16_state(variant, kind):
+    """bfloat16 optimizer state next to float32 params, segmented vs dense."""
+    op, kw = variant
+    a, b = run_both("cuda", op, kw, kind, torch.float32, True, strided_grads=True,
+                    strided_state=False, seed=8, state_dtype=torch.bfloat16)
     torch.cuda.synchronize()
     assert_same(a, b, True)
 
@@ -338,6 +354,14 @@ def test_cpu_segments_match_scatter_then_update(variant, with_out):
     a, b = run_both("cpu", op, kw, "ragged", torch.float32, with_out, strided_grads=True,
                     strided_state=False, seed=1)
     assert_same(a, b, with_out)
+
+
+@pytest.mark.parametrize("variant", VARIANTS, ids=vid)
+def test_cpu_segments_bf16_state(variant):
+    op, kw = variant
+    a, b = run_both("cpu", op, kw, "ragged", torch.float32, True, strided_grads=True,
+                    strided_state=False, seed=2, state_dtype=torch.bfloat16)
+    assert_same(a, b, True)
 
 
 @pytest.mark.parametrize("kind", ["state", "ragged", "many"])

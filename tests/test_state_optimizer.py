@@ -246,3 +246,33 @@ def test_frozen_replica_does_not_move():
     Adam.apply_gradient(state, grads)
     assert torch.equal(state.params[1], before)
     assert state.optimizer_state["state_steps"].tolist() == [1.0, 0.0, 1.0]
+
+
+# ---------------------------------------------------------------------------
+# bfloat16 optimizer state (an extension; float32 params)
+# ---------------------------------------------------------------------------
+@pytest.mark.parametrize("device", DEVICES)
+@pytest.mark.parametrize("opt_cls,kw,keys", [
+    (Adam, dict(lr=1e-2, amsgrad=True), ("exp_avgs", "exp_avg_sqs", "max_exp_avg_sqs")),
+    (SGD, dict(lr=5e-2, momentum=0.9, nesterov=True), ("momentum_buffers",)),
+    (Adagrad, dict(lr=5e-2, initial_accumulator_value=0.1), ("state_sums",)),
+])
+def test_bf16_state_ensemble_tracks_float32_state(device, opt_cls, kw, keys):
+    net = make_net(device)
+    x, y = data(device)
+    gl = grad_fn(net)
+    runs = {}
+    for sd in (None, torch.bfloat16):
+        state = ensemble(net, 2)
+        opt_cls.init(state, state_dtype=sd, **kw)
+        for _ in range(5):
+            grads, _ = gl(state.params_dict, state.buffers_dict, x, y)
+            opt_cls.apply_gradient(state, grads)
+        runs[sd] = state
+    lo, hi = runs[torch.bfloat16], runs[None]
+    for k in keys:
+        assert lo.optimizer_state[k].dtype == torch.bfloat16
+        assert hi.optimizer_state[k].dtype == torch.float32
+    assert lo.params.dtype == torch.float32
+    torch.testing.assert_close(lo.params, hi.params, rtol=0, atol=2e-3)
+    assert lo.params.shape[1] == 72 and not lo.params[:, 71:].any()  # pad lane stays zero
