@@ -338,6 +338,7 @@ def grad_scatter_timing(cfg: int, steps: int):
 
 
 TS_STATE_BF16 = 0x20
+TS_ADAGRAD_F32 = 0x40
 
 
 def bf16_state_timing(cfg: int, launches: int):
@@ -456,6 +457,12 @@ def main():
 
     kern_ms = kernel_only_timing(op_name, op_args, kw, max(10, args.steps))
     achieved = nbytes / (kern_ms * 1e-3) / 1e9
+    adagrad_f32 = None
+    if op_name == "adagrad":  # the float32 variant on the same state
+        f32_ms = kernel_only_timing(op_name, op_args, kw, max(10, args.steps),
+                                    extra_flags=TS_ADAGRAD_F32)
+        adagrad_f32 = {"kernel_avg_ms": round(f32_ms, 4),
+                       "GBs": round(nbytes / (f32_ms * 1e-3) / 1e9, 1)}
     policy = {"adam": "AdamPolicy<float, %s, %s>" % (str(kw.get("decoupled_weight_decay")).lower(),
                                                      str(kw.get("amsgrad")).lower()),
               "sgd": "SgdPolicy<float, %s, %s>" % ("true" if op_args[2] is not None else "false",
@@ -512,6 +519,7 @@ def main():
         "python_loop_baseline": loop or None,
         "grad_scatter_step": scatter,
         "bf16_state": bf16,
+        "adagrad_f32": adagrad_f32,
         "speedup_vs_python_loop": ({k: round(v / step_ms, 2) for k, v in loop.items()}
                                    if loop else None),
     }

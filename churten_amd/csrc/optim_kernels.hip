@@ -213,6 +213,32 @@ struct AdagradPolicy {
   }
 };
 
+// Float32 Adagrad (TS_ADAGRAD_F32): the reference CPU kernel's float element
+// math instead of ATen's fp64 update; h = {lr, lr_decay, wd, eps}. The math
+// type is float for every storage type (float64 parameters are rejected).
+template <typename T_, typename S_ = T_>
+struct AdagradF32Policy {
+  using T = T_;
+  using S = S_;
+  using M = float;
+  static constexpr int NS = 1;
+  struct Rep {
+    AdagradF32Hyper h;
+  };
+  __device__ static void prologue(const Vectors<T>& v, uint32_t r, Rep& rep) {
+    const double wd = hyper_at(v.h[2], r);
+    rep.h.weight_decay = static_cast<float>(wd);
+    rep.h.has_weight_decay = wd != 0.0;
+    rep.h.eps = static_cast<float>(hyper_at(v.h[3], r));
+    rep.h.corrected_lr =
+        adagrad_corrected_lr_f32(hyper_at(v.h[0], r), hyper_at(v.h[1], r), hyper_at(v.steps, r));
+  }
+  __device__ static bool reads_state(const Rep&) { return true; }
+  __device__ static void update(M& p, M g, M (&s)[NS], const Rep& rep, bool maximize) {
+    adagrad_element_f32(p, g, s[0], rep.h, maximize);
+  }
+};
+
 template <typename P>
 constexpr int state_slots() {
   return P::NS > 0 ? P::NS : 1;
@@ -880,7 +906,14 @@ int sgd_dispatch(uint32_t flags, bool has_buf, Launch&& launch) {
 }
 
 template <typename T, typename S, typename Launch>
-int adagrad_dispatch(Launch&& launch) {
+int adagrad_dispatch(uint32_t flags, Launch&& launch) {
+  if ((flags & TS_ADAGRAD_F32) != 0) {
+    if constexpr (std::is_same<T, double>::value) {
+      return kInvalid;
+    } else {
+      return launch(AdagradF32Policy<T, S>{}, 3);
+    }
+  }
   return launch(AdagradPolicy<T, S>{}, 3);
 }
 
@@ -947,7 +980,7 @@ struct AdagradBody {
   static int run(const Call& c, const ts_segment* segs, int n_segs, bool segmented) {
     return with_state_type<T>(c.flags, [&](auto state) {
       using S = typename decltype(state)::type;
-      return adagrad_dispatch<T, S>([&](auto policy, int nbufs) {
+      return adagrad_dispatch<T, S>(c.flags, [&](auto policy, int nbufs) {
         return launch_any<decltype(policy)>(c, nbufs, segs, n_segs, segmented);
       });
     });
@@ -1011,7 +1044,7 @@ using churten::make_call;
 
 extern "C" {
 
-int ts_version(void) { return 120; }
+int ts_version(void) { return 130; }
 
 int ts_bump_steps(ts_dtype dtype, void* state_steps, const uint8_t* active_mask,
                   int64_t R, void* out_zero, void* stream) {

@@ -193,6 +193,37 @@ __device__ __forceinline__ void adagrad_element(
                                                     (double(std::sqrt(state_sum)) + h.eps));
 }
 
+// Float32 Adagrad (this build's explicitly non-ATen variant): the element loop
+// of the reference's CPU kernel (src/torchstrap/kernels/csrc/cpu/adagrad.cpp:
+// 94-156) -- every operation in float, the multiply-adds fused -- so on float32
+// parameters it is bit-identical to the reference's CPU build, not to torch's
+// fp64 device math.
+struct AdagradF32Hyper {
+  float corrected_lr, weight_decay, eps;
+  bool has_weight_decay;
+};
+
+__device__ __forceinline__ void adagrad_element_f32(float& param, float grad, float& state_sum,
+                                                    const AdagradF32Hyper& h,
+                                                    const bool maximize) {
+  if (maximize) {
+    grad = -grad;
+  }
+  if (h.has_weight_decay) {
+    grad = ::fmaf(param, h.weight_decay, grad);
+  }
+  state_sum = ::fmaf(grad, grad, state_sum);
+  const float std_val = ::sqrtf(state_sum) + h.eps;
+  param = param - (h.corrected_lr * grad) / std_val;
+}
+
+// The CPU kernel's corrected_lr: lr / (1 + (step - 1) * lr_decay) in double
+// from the double step (cpu/adagrad.cpp:207-212), then narrowed to float.
+__device__ __forceinline__ float adagrad_corrected_lr_f32(const double lr, const double lr_decay,
+                                                          const double step) {
+  return static_cast<float>(lr / ::fma(step - 1.0, lr_decay, 1.0));
+}
+
 // corrected_lr = lr / (1 + (step - 1) * lr_decay), with `step - 1` in float.
 __device__ __forceinline__ double adagrad_corrected_lr(
     const double lr, const double lr_decay, const float step) {

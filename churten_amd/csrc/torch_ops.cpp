@@ -287,12 +287,13 @@ at::Tensor sgd_step_gpu(at::Tensor params, at::Tensor grads,
   return p.out;
 }
 
-at::Tensor adagrad_step_gpu(at::Tensor params, at::Tensor grads, at::Tensor state_sums,
-                            at::Tensor state_steps, at::Tensor lr, at::Tensor lr_decay,
-                            at::Tensor weight_decay, at::Tensor eps, at::Tensor active_mask,
-                            bool maximize) {
-  constexpr const char* op = "torchstrap::adagrad_step_";
+at::Tensor adagrad_gpu(at::Tensor params, at::Tensor grads, at::Tensor state_sums,
+                       at::Tensor state_steps, at::Tensor lr, at::Tensor lr_decay,
+                       at::Tensor weight_decay, at::Tensor eps, at::Tensor active_mask,
+                       bool maximize, bool fp32_math, const char* op) {
   check_params(params, op);
+  TORCH_CHECK(!fp32_math || params.scalar_type() != at::kDouble, op,
+              ": the float32 Adagrad variant does not take float64 parameters");
   check_like(params, grads, op, "grads");
   const uint32_t sflag = state_flag(params, state_sums);
   check_state(params, state_sums, sflag, op, "state_sums");
@@ -300,12 +301,30 @@ at::Tensor adagrad_step_gpu(at::Tensor params, at::Tensor grads, at::Tensor stat
   const Prepared p = prepare(params, state_steps, active_mask,
                              {&lr, &lr_decay, &weight_decay, &eps},
                              {"lr", "lr_decay", "weight_decay", "eps"},
-                             sflag | (maximize ? TS_MAXIMIZE : 0u), op);
+                             sflag | (maximize ? TS_MAXIMIZE : 0u) |
+                                 (fp32_math ? TS_ADAGRAD_F32 : 0u),
+                             op);
   const ts_rt_buf bufs[3] = {rt_buf(params), rt_buf(grads), rt_buf(state_sums)};
   check_status(ts_adagrad_step(bufs, p.dtype, p.steps.data_ptr(), p.h(0), p.h(1), p.h(2),
                                p.h(3), p.m(), p.R, p.T, p.flags, p.out.data_ptr(), p.stream),
                op);
   return p.out;
+}
+
+at::Tensor adagrad_step_gpu(at::Tensor params, at::Tensor grads, at::Tensor state_sums,
+                            at::Tensor state_steps, at::Tensor lr, at::Tensor lr_decay,
+                            at::Tensor weight_decay, at::Tensor eps, at::Tensor active_mask,
+                            bool maximize) {
+  return adagrad_gpu(params, grads, state_sums, state_steps, lr, lr_decay, weight_decay, eps,
+                     active_mask, maximize, false, "torchstrap::adagrad_step_");
+}
+
+at::Tensor adagrad_step_f32_gpu(at::Tensor params, at::Tensor grads, at::Tensor state_sums,
+                                at::Tensor state_steps, at::Tensor lr, at::Tensor lr_decay,
+                                at::Tensor weight_decay, at::Tensor eps,
+                                at::Tensor active_mask, bool maximize) {
+  return adagrad_gpu(params, grads, state_sums, state_steps, lr, lr_decay, weight_decay, eps,
+                     active_mask, maximize, true, "churten::adagrad_step_f32_");
 }
 
 // ---------------------------------------------------------------------------
@@ -396,9 +415,11 @@ at::Tensor adagrad_step_segments_gpu(at::Tensor params, at::TensorList grads,
                                      at::Tensor state_sums, at::Tensor state_steps,
                                      at::Tensor lr, at::Tensor lr_decay,
                                      at::Tensor weight_decay, at::Tensor eps,
-                                     at::Tensor active_mask, bool maximize) {
+                                     at::Tensor active_mask, bool maximize, bool fp32_math) {
   constexpr const char* op = "churten::adagrad_step_segments_";
   check_params(params, op);
+  TORCH_CHECK(!fp32_math || params.scalar_type() != at::kDouble, op,
+              ": the float32 Adagrad variant does not take float64 parameters");
   if (grads_out.has_value()) check_like(params, *grads_out, op, "grads_out");
   const uint32_t sflag = state_flag(params, state_sums);
   check_state(params, state_sums, sflag, op, "state_sums");
@@ -407,7 +428,9 @@ at::Tensor adagrad_step_segments_gpu(at::Tensor params, at::TensorList grads,
   const Prepared p = prepare(params, state_steps, active_mask,
                              {&lr, &lr_decay, &weight_decay, &eps},
                              {"lr", "lr_decay", "weight_decay", "eps"},
-                             sflag | (maximize ? TS_MAXIMIZE : 0u), op);
+                             sflag | (maximize ? TS_MAXIMIZE : 0u) |
+                                 (fp32_math ? TS_ADAGRAD_F32 : 0u),
+                             op);
   const ts_rt_buf bufs[3] = {rt_buf(params), grads_out.has_value() ? rt_buf(*grads_out) : kNoBuf,
                              rt_buf(state_sums)};
   check_status(ts_adagrad_step_segments(bufs, st.segs.data(), static_cast<int>(st.segs.size()),
@@ -480,7 +503,11 @@ at::Tensor adagrad_step_segments_cpu(at::Tensor params, at::TensorList grads,
                                      at::Tensor state_sums, at::Tensor state_steps,
                                      at::Tensor lr, at::Tensor lr_decay,
                                      at::Tensor weight_decay, at::Tensor eps,
-                                     at::Tensor active_mask, bool maximize) {
+                                     at::Tensor active_mask, bool maximize, bool fp32_math) {
+  TORCH_CHECK(!fp32_math || params.scalar_type() != at::kDouble,
+              "churten::adagrad_step_segments_: the float32 Adagrad variant does not take "
+              "float64 parameters");
+  // The CPU kernel already runs the float32 element math.
   static auto step = c10::Dispatcher::singleton()
                          .findSchemaOrThrow("torchstrap::adagrad_step_", "")
                          .typed<at::Tensor(at::Tensor, at::Tensor, at::Tensor, at::Tensor,
@@ -489,6 +516,24 @@ at::Tensor adagrad_step_segments_cpu(at::Tensor params, at::TensorList grads,
   TORCH_CHECK(params.dim() == 2, "churten::adagrad_step_segments_: params must be 2-D");
   return step.call(params, consolidated(params, grads_out, grads, cols), state_sums,
                    state_steps, lr, lr_decay, weight_decay, eps, active_mask, maximize);
+}
+
+// The reference's CPU Adagrad kernel is itself the float32 element loop, so
+// the float32 variant on the CPU key is that kernel.
+at::Tensor adagrad_step_f32_cpu(at::Tensor params, at::Tensor grads, at::Tensor state_sums,
+                                at::Tensor state_steps, at::Tensor lr, at::Tensor lr_decay,
+                                at::Tensor weight_decay, at::Tensor eps,
+                                at::Tensor active_mask, bool maximize) {
+  TORCH_CHECK(params.scalar_type() != at::kDouble,
+              "churten::adagrad_step_f32_: the float32 Adagrad variant does not take float64 "
+              "parameters");
+  static auto step = c10::Dispatcher::singleton()
+                         .findSchemaOrThrow("torchstrap::adagrad_step_", "")
+                         .typed<at::Tensor(at::Tensor, at::Tensor, at::Tensor, at::Tensor,
+                                           at::Tensor, at::Tensor, at::Tensor, at::Tensor,
+                                           at::Tensor, bool)>();
+  return step.call(params, grads, state_sums, state_steps, lr, lr_decay, weight_decay, eps,
+                   active_mask, maximize);
 }
 
 }  // namespace
@@ -562,7 +607,11 @@ TORCH_LIBRARY(churten, m) {
   m.def("adagrad_step_segments_(Tensor(a!) params, Tensor[] grads, int[] cols, "
         "Tensor(b!)? grads_out, Tensor(c!) state_sums, Tensor(d!) state_steps, Tensor lr, "
         "Tensor lr_decay, Tensor weight_decay, Tensor eps, Tensor active_mask, "
-        "bool maximize) -> Tensor");
+        "bool maximize, bool fp32_math=False) -> Tensor");
+  // torchstrap::adagrad_step_'s schema; float32 element math instead of fp64.
+  m.def("adagrad_step_f32_(Tensor(a!) params, Tensor grads, Tensor(b!) state_sums, "
+        "Tensor(c!) state_steps, Tensor lr, Tensor lr_decay, Tensor weight_decay, Tensor eps, "
+        "Tensor active_mask, bool maximize) -> Tensor");
 }
 
 TORCH_LIBRARY_IMPL(churten, CUDA, m) {
@@ -570,6 +619,7 @@ TORCH_LIBRARY_IMPL(churten, CUDA, m) {
   m.impl("adam_step_segments_", &adam_step_segments_gpu);
   m.impl("sgd_step_segments_", &sgd_step_segments_gpu);
   m.impl("adagrad_step_segments_", &adagrad_step_segments_gpu);
+  m.impl("adagrad_step_f32_", &adagrad_step_f32_gpu);
 }
 
 TORCH_LIBRARY_IMPL(churten, CPU, m) {
@@ -577,6 +627,7 @@ TORCH_LIBRARY_IMPL(churten, CPU, m) {
   m.impl("adam_step_segments_", &adam_step_segments_cpu);
   m.impl("sgd_step_segments_", &sgd_step_segments_cpu);
   m.impl("adagrad_step_segments_", &adagrad_step_segments_cpu);
+  m.impl("adagrad_step_f32_", &adagrad_step_f32_cpu);
 }
 
 }  // namespace churten

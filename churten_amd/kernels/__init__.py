@@ -32,7 +32,7 @@ _C = _load_native()
 
 from churten_amd.kernels.adam import adam_step_  # noqa: E402
 from churten_amd.kernels.sgd import sgd_step_  # noqa: E402
-from churten_amd.kernels.adagrad import adagrad_step_  # noqa: E402
+from churten_amd.kernels.adagrad import adagrad_step_, adagrad_step_f32_  # noqa: E402
 from churten_amd.kernels.segments import (  # noqa: E402
     adagrad_step_segments_,
     adam_step_segments_,
@@ -40,5 +40,5 @@ from churten_amd.kernels.segments import (  # noqa: E402
     sgd_step_segments_,
 )
 
-__all__ = ("adam_step_", "sgd_step_", "adagrad_step_", "scatter_grads_",
+__all__ = ("adam_step_", "sgd_step_", "adagrad_step_", "adagrad_step_f32_", "scatter_grads_",
            "adam_step_segments_", "sgd_step_segments_", "adagrad_step_segments_")

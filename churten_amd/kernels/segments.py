@@ -55,5 +55,6 @@ def _sgd_step_segments_fake(params, grads, cols, grads_out, momentum_buffers, st
 
 @torch.library.register_fake("churten::adagrad_step_segments_")
 def _adagrad_step_segments_fake(params, grads, cols, grads_out, state_sums, state_steps, lr,
-                                lr_decay, weight_decay, eps, active_mask, maximize):
+                                lr_decay, weight_decay, eps, active_mask, maximize,
+                                fp32_math=False):
     return params.new_empty(())

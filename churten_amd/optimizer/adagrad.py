@@ -11,7 +11,7 @@ from __future__ import annotations
 
 import torch
 
-from churten_amd.kernels.adagrad import adagrad_step_
+from churten_amd.kernels.adagrad import adagrad_step_, adagrad_step_f32_
 from churten_amd.kernels.segments import adagrad_step_segments_
 from churten_amd.optimizer.grad_transform import GradientTransformation
 from churten_amd.state import State
@@ -23,9 +23,11 @@ class Adagrad(metaclass=GradientTransformation):
     @classmethod
     def init(cls, state: State, *, lr=1e-2, lr_decay=0.0, weight_decay=0.0, eps=1e-10,
              initial_accumulator_value=0.0, maximize: bool = False,
-             state_dtype: torch.dtype | None = None) -> State:
+             state_dtype: torch.dtype | None = None, fp32_math: bool = False) -> State:
         """``state_dtype=torch.bfloat16`` keeps the accumulators in bfloat16
-        next to float32 params."""
+        next to float32 params. ``fp32_math=True`` selects the float32 variant
+        (``churten::adagrad_step_f32_``): the reference CPU kernel's float
+        element math on the GPU too, not torch's fp64 device update."""
         for key, value in (("lr", lr), ("lr_decay", lr_decay), ("weight_decay", weight_decay),
                            ("eps", eps), ("state_steps", 0)):
             state.add_optim_state(key, value)
@@ -36,6 +38,7 @@ class Adagrad(metaclass=GradientTransformation):
         elif initial_accumulator_value != 0.0:
             sums.fill_(initial_accumulator_value)
         state.add_optim_meta("maximize", maximize)
+        state.add_optim_meta("fp32_math", fp32_math)
         return state
 
     @classmethod
@@ -55,8 +58,9 @@ class Adagrad(metaclass=GradientTransformation):
     @classmethod
     def update(cls, state: State, maximize: bool = False) -> State:
         args, flags = cls._state_args(state, maximize)
-        adagrad_step_(torch.atleast_2d(state.flat_params), torch.atleast_2d(state.flat_grads),
-                      *args, **flags)
+        op = adagrad_step_f32_ if state.optimizer_state.get("fp32_math") else adagrad_step_
+        op(torch.atleast_2d(state.flat_params), torch.atleast_2d(state.flat_grads), *args,
+           **flags)
         return state
 
     @classmethod
@@ -66,5 +70,6 @@ class Adagrad(metaclass=GradientTransformation):
         consolidated gradient unless it is None."""
         args, flags = cls._state_args(state)
         adagrad_step_segments_(torch.atleast_2d(state.flat_params), grads, cols, grads_out,
-                               *args, **flags)
+                               *args, fp32_math=bool(state.optimizer_state.get("fp32_math")),
+                               **flags)
         return state

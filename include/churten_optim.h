@@ -83,6 +83,12 @@ typedef enum ts_dtype {
  * them from the widened state. Low-precision optimizer state has no
  * counterpart in the reference operators (its README roadmap lists it). */
 #define TS_STATE_BF16 0x20u
+/* Adagrad: float32 element math -- the reference CPU kernel's loop
+ * (cpu/adagrad.cpp:94-156), bit-identical to the reference's CPU build on
+ * float32 parameters -- instead of ATen's fp64 device update. Explicitly not
+ * bit-exact to torch._fused_adagrad_ (the reference's README/CLAUDE.md name
+ * such a variant as a separate feature). Not available for float64. */
+#define TS_ADAGRAD_F32 0x40u
 
 /* A per-parameter gradient: an (R, numel) tensor with element (r, j) at
  * data + r*stride_r + j, standing for columns [col, col + numel) of the

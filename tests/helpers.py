@@ -38,11 +38,12 @@ def to_layout_tensor(t: torch.Tensor, strided: bool) -> torch.Tensor:
 
 
 def run_hip(c, strided: bool = False, dev: str = "cuda", state_bf16: bool = False,
-            state_dtype=None):
+            state_dtype=None, adagrad_f32: bool = False):
     """``state_bf16``: the case's optimizer state starts bfloat16-valued and is
     held in bfloat16 tensors (params and grads stay float32), unless
     ``state_dtype`` names another dtype for those tensors. Outputs are returned
-    widened to float32."""
+    widened to float32. ``adagrad_f32`` runs Adagrad cases through the float32
+    variant ``churten::adagrad_step_f32_``."""
     import churten_amd.kernels  # noqa: F401
 
     x = C.make_inputs(c, state_bf16)
@@ -72,8 +73,9 @@ def run_hip(c, strided: bool = False, dev: str = "cuda", state_bf16: bool = Fals
                           vec("dampening"), vec("wd"), mask, nesterov=c["nesterov"],
                           maximize=c["maximize"])
         else:
-            ops.adagrad_step_(st["p"], gt, st["s"], steps, vec("lr"), vec("lr_decay"),
-                              vec("wd"), vec("eps"), mask, maximize=c["maximize"])
+            fn = torch.ops.churten.adagrad_step_f32_ if adagrad_f32 else ops.adagrad_step_
+            fn(st["p"], gt, st["s"], steps, vec("lr"), vec("lr_decay"), vec("wd"), vec("eps"),
+               mask, maximize=c["maximize"])
     if torch.device(dev).type == "cuda":
         torch.cuda.synchronize()
     out = {k: st[k].float().contiguous().cpu().numpy() for k in names}
