@@ -369,6 +369,72 @@ def bf16_state_timing(cfg: int, launches: int):
             "step_equivalent_GBs": round(active * T * bytes_per_elem(cfg) / (ms * 1e-3) / 1e9, 1)}
 
 
+SNAPSHOT_N = 32
+
+
+def snapshot_timing(cfg: int):
+    """The checkpoint device-to-host path on the config's optimizer state
+    (params, grads and the optimizer's (N, T) buffers, as one State) at
+    N = SNAPSHOT_N replicas: the initial full copy into the pinned mirror, then
+    ``Snapshot.update`` of the active replicas' rows, then the same rows the
+    reference's way (device gather, pinned staging, host scatter into a
+    pageable mirror)."""
+    import torch
+
+    from churten_amd.optimizer import Adam  # noqa: F401  (registers the ops)
+    from churten_amd.snapshot import Snapshot
+    from churten_amd.state import State
+
+    op_name, args, kw, _ = make_config(cfg, N=SNAPSHOT_N)
+    if op_name != "adam":
+        return None
+    p, g, m, v, mx, steps, lr, b1, b2, eps, wd, mask = args
+    N, T = p.shape
+    state = State(params=p, buffers=torch.empty(N, 0, device=p.device),
+                  param_meta=[("w", torch.Size((N, T)), 0, T)], buffer_meta=[],
+                  active_mask=mask, grads=g)
+    state.optimizer_state.update(exp_avgs=m, exp_avg_sqs=v, state_steps=steps, lr=lr,
+                                 beta1=b1, beta2=b2, eps=eps, weight_decay=wd)
+    rt_bytes = 4 * N * T * 4
+    t0 = time.perf_counter()
+    snap = Snapshot(state)
+    t_init = time.perf_counter() - t0
+    active = int(mask.sum().item())
+    torch.cuda.synchronize()
+    t0 = time.perf_counter()
+    snap.update(state)
+    t_upd = time.perf_counter() - t0
+    moved = 4 * active * T * 4
+    # the reference's route for the same rows, on the (N, T) leaves
+    leaves = [p, g, m, v]
+    mirrors = [snap.tensors[k].clone() for k in ("params", "grads")] + [
+        snap.tensors["optimizer_state.exp_avgs"].clone(),
+        snap.tensors["optimizer_state.exp_avg_sqs"].clone()]  # pageable
+    staging = [torch.empty_like(x, pin_memory=True) for x in mirrors]
+    torch.cuda.synchronize()
+    t0 = time.perf_counter()
+    idx_cpu = mask.cpu().nonzero().flatten()
+    idx = idx_cpu.to(p.device)
+    for leaf, stg, mir in zip(leaves, staging, mirrors):
+        k = idx.numel()
+        stg[:k].copy_(leaf.index_select(0, idx), non_blocking=True)
+        torch.cuda.current_stream().synchronize()
+        mir[idx_cpu] = stg[:k]
+    t_ref = time.perf_counter() - t0
+    same = all(torch.equal(mir[idx_cpu], snap.tensors[n][idx_cpu]) for mir, n in zip(
+        mirrors, ("params", "grads", "optimizer_state.exp_avgs", "optimizer_state.exp_avg_sqs")))
+    del snap, mirrors, staging, state, args, leaves
+    torch.cuda.empty_cache()
+    return {"sample": f"config {cfg} at N={N}", "state_bytes": rt_bytes,
+            "initial_copy_s": round(t_init, 3),
+            "initial_GBs": round(rt_bytes / t_init / 1e9, 1),
+            "update_bytes": moved, "update_s": round(t_upd, 3),
+            "update_GBs": round(moved / t_upd / 1e9, 1),
+            "reference_route_s": round(t_ref, 3),
+            "reference_route_GBs": round(moved / t_ref / 1e9, 1),
+            "mirrors_identical": bool(same)}
+
+
 def read_traffic(kernel: str):
     """HBM bytes per launch from the committed rocprofv3 --pmc summary, if any."""
     f = ROOT / "profiles" / f"{kernel}_traffic.json"
@@ -403,6 +469,9 @@ def main():
     ap.add_argument("--cpu-steps", type=int, default=5)
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--no-loop-baseline", action="store_true")
+    ap.add_argument("--snapshot", action="store_true",
+                    help="also time the checkpoint device-to-host path (allocates the "
+                         "state's size twice in pinned host memory)")
     ap.add_argument("--no-bf16-state", action="store_true",
                     help="skip the bfloat16-optimizer-state timing")
     ap.add_argument("--no-grad-scatter", action="store_true",
@@ -473,6 +542,8 @@ def main():
     del op_args
     torch.cuda.empty_cache()
 
+    snapshot = snapshot_timing(args.config) if args.snapshot else None
+
     bf16 = None
     if not args.no_bf16_state and args.config != 3:
         bf16 = bf16_state_timing(args.config, max(10, args.steps // 2))
@@ -520,6 +591,7 @@ def main():
         "grad_scatter_step": scatter,
         "bf16_state": bf16,
         "adagrad_f32": adagrad_f32,
+        "snapshot": snapshot,
         "speedup_vs_python_loop": ({k: round(v / step_ms, 2) for k, v in loop.items()}
                                    if loop else None),
     }

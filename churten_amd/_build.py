@@ -79,7 +79,8 @@ def build_library(verbose: bool = False) -> Path:
     LIB_DIR.mkdir(parents=True, exist_ok=True)
     tmp = LIB.with_suffix(".so.tmp")
     _run(
-        [_hipcc(), *HIPCC_FLAGS, str(CSRC / "optim_kernels.hip"), "-o", str(tmp)],
+        [_hipcc(), *HIPCC_FLAGS, str(CSRC / "optim_kernels.hip"), str(CSRC / "rows.hip"),
+         "-o", str(tmp)],
         verbose,
     )
     os.replace(tmp, LIB)

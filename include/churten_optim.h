@@ -174,6 +174,21 @@ int ts_adagrad_step_segments(const ts_rt_buf* bufs, const ts_segment* grads, int
 int ts_scatter_segments(const ts_segment* src, int n_src, ts_dtype dtype, void* dst,
                         int64_t dst_stride_r, int64_t cols, int64_t R, void* stream);
 
+/* Replica-row transfer for the snapshot / checkpoint path: copies rows r of
+ * an (R, ...) buffer with rows[r] != 0 (rows is a HOST array of R bytes; NULL
+ * = every row), row_bytes bytes each, from src (row stride src_stride bytes)
+ * to dst (row stride dst_stride bytes), with one DMA copy per run of
+ * consecutive selected rows, enqueued on `stream`. The host side must be
+ * pinned memory for the copy to be asynchronous. Replaces the gather + pinned
+ * staging + host scatter of the reference's Snapshot.update / restore_to_live
+ * (src/torchstrap/callbacks/training.py:45-116). */
+#define TS_ROWS_TO_HOST 0   /* device buffer -> host mirror */
+#define TS_ROWS_TO_DEVICE 1 /* host mirror -> device buffer */
+#define TS_ROWS_DEVICE 2    /* device -> device */
+int ts_copy_rows(void* dst, int64_t dst_stride, const void* src, int64_t src_stride,
+                 int64_t row_bytes, const uint8_t* rows, int64_t R, int direction,
+                 void* stream);
+
 /* Library version, for INTEGRATION checks: major*10000 + minor*100 + patch. */
 int ts_version(void);
 

@@ -49,14 +49,14 @@ def test_header_declares_the_entry_points():
     assert declared_symbols() == sorted(
         ["ts_adagrad_step", "ts_adam_step", "ts_bump_steps", "ts_sgd_step", "ts_version",
          "ts_adam_step_segments", "ts_sgd_step_segments", "ts_adagrad_step_segments",
-         "ts_scatter_segments"])
+         "ts_scatter_segments", "ts_copy_rows"])
 
 
 def test_library_exports_every_declared_symbol():
     lib = ctypes.CDLL(str(LIB))
     for name in declared_symbols():
         assert hasattr(lib, name), name
-    assert lib.ts_version() == 130
+    assert lib.ts_version() == 140
 
 
 def test_invalid_arguments_rejected_before_any_launch():
