@@ -82,3 +82,57 @@ def test_config5_properties():
             got = _np(t[r : r + 1, t0 : t0 + 4096])
             assert np.array_equal(got.view(np.uint32), want.view(np.uint32)), (
                 f"row {r} window {t0}: {name}")
+
+
+def test_config5_segmented_update_equals_dense():
+    """The 12 per-parameter gradients of config 5's transformer block, read in
+    place by the segmented update (consolidated gradient refilled on the way),
+    give the same state, bit for bit, over all 52 GB, as the dense update."""
+    op, args, kw, _ = bench.make_config(5)
+    p, gr, m, v, mx, steps, *hyp = args
+    twin = [t.clone() for t in (p, m, v, steps)]
+    cols, grads, c = [], [], 0
+    for shape in bench.BLOCK_LAYOUT:
+        n = int(np.prod(shape))
+        cols.append(c)
+        grads.append(gr[:, c:c + n])  # (R, n) views with row stride T
+        c += n
+    gout = torch.zeros_like(gr)
+    torch.ops.torchstrap.adam_step_(p, gr, m, v, None, steps, *hyp, **kw)
+    torch.ops.churten.adam_step_segments_(twin[0], grads, cols, gout, twin[1], twin[2], None,
+                                          twin[3], *hyp, **kw)
+    torch.cuda.synchronize()
+    for name, a, b in (("params", p, twin[0]), ("exp_avgs", m, twin[1]),
+                       ("exp_avg_sqs", v, twin[2]), ("steps", steps, twin[3])):
+        assert torch.equal(a.view(torch.int32), b.view(torch.int32)), name
+    assert torch.equal(gout, gr)
+
+
+def test_config5_bf16_state_windows():
+    """Config 5 with bfloat16 moments: frozen rows untouched, windows of active
+    rows (past the 2^31-element mark too) bit-identical to the oracle's float32
+    step followed by nearest-even rounding."""
+    op, args, kw, _ = bench.make_config(5)
+    p, gr, m, v, mx, steps, *hyp = args
+    mask = hyp[-1]
+    mb, vb = m.to(torch.bfloat16), v.to(torch.bfloat16)
+    del m, v
+    R, T = p.shape
+    active = mask.nonzero().flatten().tolist()
+    frozen = (~mask).nonzero().flatten()
+    windows = [(active[0], 0), (active[-1], T - 4096)]
+    before = [[_np(t[r:r + 1, t0:t0 + 4096].float()) for t in (p, gr, mb, vb)] for r, t0 in windows]
+    hyp_np = [_np(t) for t in hyp[:-1]]
+    steps0 = _np(steps)
+    keep = [t[frozen].clone() for t in (p, mb, vb)]
+    torch.ops.torchstrap.adam_step_(p, gr, mb, vb, None, steps, *hyp, **kw)
+    torch.cuda.synchronize()
+    for t, k in zip((p, mb, vb), keep):
+        assert torch.equal(t[frozen], k)
+    for (r, t0), (pw, gw, mw, vw) in zip(windows, before):
+        sw = steps0[r:r + 1].copy()
+        O.adam_step(O.DEVICE, pw, gw, mw, vw, None, sw, *[h[r:r + 1].copy() for h in hyp_np],
+                    np.ones(1, bool), state_bf16=True, **kw)
+        for name, t, want in (("p", p, pw), ("m", mb, mw), ("v", vb, vw)):
+            got = _np(t[r:r + 1, t0:t0 + 4096].float())
+            assert np.array_equal(got.view(np.uint32), want.view(np.uint32)), (r, t0, name)
