@@ -435,6 +435,39 @@ def snapshot_timing(cfg: int):
             "mirrors_identical": bool(same)}
 
 
+def graph_replay_timing(cfg: int, replays: int):
+    """One operator call captured in a HIP graph and replayed: the per-step
+    time once the host-side launch work is gone (what a captured training step
+    sees). Returns microseconds per replay."""
+    import torch
+
+    op_name, args, kw, _ = make_config(cfg)
+    fn = getattr(torch.ops.torchstrap, f"{op_name}_step_")
+    s = torch.cuda.Stream()
+    s.wait_stream(torch.cuda.current_stream())
+    with torch.cuda.stream(s):
+        fn(*args, **kw)
+    torch.cuda.current_stream().wait_stream(s)
+    torch.cuda.synchronize()
+    graph = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(graph):
+        fn(*args, **kw)
+    graph.replay()
+    torch.cuda.synchronize()
+    e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    t0 = time.perf_counter()
+    e0.record()
+    for _ in range(replays):
+        graph.replay()
+    e1.record()
+    torch.cuda.synchronize()
+    wall = (time.perf_counter() - t0) / replays * 1e6
+    us = e0.elapsed_time(e1) / replays * 1e3
+    del graph, args
+    torch.cuda.empty_cache()
+    return {"us_per_step": round(us, 2), "wall_us_per_step": round(wall, 2)}
+
+
 def read_traffic(kernel: str):
     """HBM bytes per launch from the committed rocprofv3 --pmc summary, if any."""
     f = ROOT / "profiles" / f"{kernel}_traffic.json"
@@ -543,6 +576,7 @@ def main():
     torch.cuda.empty_cache()
 
     snapshot = snapshot_timing(args.config) if args.snapshot else None
+    graphed = graph_replay_timing(args.config, args.steps) if args.config != 5 else None
 
     bf16 = None
     if not args.no_bf16_state and args.config != 3:
@@ -592,6 +626,7 @@ def main():
         "bf16_state": bf16,
         "adagrad_f32": adagrad_f32,
         "snapshot": snapshot,
+        "graph_replay": graphed,
         "speedup_vs_python_loop": ({k: round(v / step_ms, 2) for k, v in loop.items()}
                                    if loop else None),
     }
