@@ -457,3 +457,35 @@ def test_state_gradient_scatter_uses_one_launch_or_copies():
     # a float64 gradient is converted by the per-name path
     state._consolidated_grads.update_({"0.bias": torch.ones(3, 10, dtype=torch.float64)})
     assert torch.equal(state._consolidated_grads["0.bias"], torch.ones(3, 10))
+
+
+# ---------------------------------------------------------------------------
+# torch.library.opcheck: schema / alias annotations, fake kernels, dispatch
+# ---------------------------------------------------------------------------
+@pytest.mark.parametrize("device", ["cpu", pytest.param("cuda", marks=pytest.mark.gpu)])
+def test_opcheck_churten_ops(device):
+    R, T = 3, 24
+    g = torch.Generator().manual_seed(0)
+    rnd = lambda *s: torch.randn(*s, generator=g).to(device)  # noqa: E731
+    vec = lambda x: torch.full((R,), x, device=device)  # noqa: E731
+    mask = torch.tensor([True, False, True], device=device)
+    grads, cols = [rnd(R, 2, 5), rnd(R, 7)], [0, 12]
+    torch.library.opcheck(torch.ops.churten.scatter_grads_.default,
+                          (torch.zeros(R, T, device=device), grads, cols))
+    torch.library.opcheck(
+        torch.ops.churten.adam_step_segments_.default,
+        (rnd(R, T), grads, cols, torch.zeros(R, T, device=device), rnd(R, T), rnd(R, T).abs(),
+         None, vec(1.0), vec(1e-2), vec(0.9), vec(0.999), vec(1e-8), vec(0.0), mask, False,
+         False, True))
+    torch.library.opcheck(
+        torch.ops.churten.sgd_step_segments_.default,
+        (rnd(R, T), grads, cols, None, rnd(R, T), vec(2.0), vec(1e-2), vec(0.9), vec(0.0),
+         vec(0.0), mask, True, False))
+    torch.library.opcheck(
+        torch.ops.churten.adagrad_step_segments_.default,
+        (rnd(R, T), grads, cols, None, rnd(R, T).abs(), vec(1.0), vec(1e-2), vec(0.0),
+         vec(0.0), vec(1e-10), mask, False, True))
+    torch.library.opcheck(
+        torch.ops.churten.adagrad_step_f32_.default,
+        (rnd(R, T), rnd(R, T), rnd(R, T).abs(), vec(1.0), vec(1e-2), vec(0.0), vec(0.0),
+         vec(1e-10), mask, False))
