@@ -1,10 +1,12 @@
 // optim_kernels.hip -- gfx950 kernels and the extern "C" launchers of
 // include/churten_optim.h.
 //
-// Structure. Each optimizer is a policy (AdamPolicy, SgdPolicy, AdagradPolicy):
-// its per-replica prologue (hyperparameters, bias corrections, is_first_step,
-// corrected_lr) and its per-element update, both from optim_math.h. Three
-// drivers move the bytes, identically for every policy:
+// Structure. Each optimizer is a policy (AdamPolicy, SgdPolicy, AdagradPolicy,
+// AdagradF32Policy): its per-replica prologue (hyperparameters, bias
+// corrections, is_first_step, corrected_lr) and its per-element update, both
+// from optim_math.h, over a parameter type T and an optimizer-state type S
+// (S = T, or bfloat16 state next to float32 parameters). Three drivers move the
+// bytes, identically for every policy:
 //
 //   stream_kernel   the consolidated (R, T) layout `State` produces: unit inner
 //                   stride, 16-byte aligned rows, T % 4 == 0. Non-temporal
@@ -18,9 +20,10 @@
 //                   the way through, so `flat_grads` stays what it would have
 //                   been.
 //
-// Operands are ordered [0] param, [1] grad, [2..] optimizer state (Adam:
-// exp_avg, exp_avg_sq, [max_exp_avg_sq]; SGD: [momentum_buffer]; Adagrad:
-// state_sum). The grad is read-only.
+// Operands are ordered [0] param, [1] grad (both T), [2..] optimizer state (S;
+// Adam: exp_avg, exp_avg_sq, [max_exp_avg_sq]; SGD: [momentum_buffer];
+// Adagrad: state_sum). The dense drivers never write the grad; the segmented
+// driver may store the gradient it read into the consolidated buffer.
 //
 // Work decomposition. Rows are cut into tiles of kTile consecutive elements
 // (segments into tiles of their own); a 1-D grid enumerates (replica, tile)
