@@ -221,3 +221,36 @@ def test_product_never_imports_the_oracle():
             text = f.read_text()
             assert "import oracle" not in text and "from oracle" not in text, f
             assert "liboracle" not in text and "optim_oracle" not in text, f
+
+
+@pytest.mark.parametrize("device", ["cpu", pytest.param("cuda", marks=pytest.mark.gpu)])
+def test_ops_trace_under_torch_compile(device):
+    """The fake kernels and alias annotations let a step containing the ops be
+    captured whole (fullgraph) and functionalized; results equal eager."""
+    import churten_amd.kernels as K
+
+    R, T = 3, 20
+    g0 = torch.Generator().manual_seed(0)
+    mk = lambda: torch.randn(R, T, generator=g0).to(device)  # noqa: E731
+    h = [torch.full((R,), x, device=device) for x in (1e-2, 0.9, 0.999, 1e-8, 1e-2)]
+    mask = torch.tensor([True, False, True], device=device)
+
+    def step(p, g, m, v, st, b, s):
+        K.adam_step_(p, g * 2.0, m, v, None, st, *h, mask, amsgrad=False, maximize=False,
+                     decoupled_weight_decay=True)
+        K.sgd_step_(b, g, None, st.clone(), h[0], h[4], h[4], h[4], mask, nesterov=False,
+                    maximize=False)
+        K.adagrad_step_(s, g, s.abs().clone(), st.clone(), h[0], h[4], h[4], h[3], mask,
+                        maximize=True)
+        return p.sum() + b.sum() + s.sum()
+
+    eager = [mk(), mk(), mk(), mk().abs(), torch.zeros(R, device=device), mk(), mk()]
+    comp = [t.clone() for t in eager]
+    compiled = torch.compile(step, fullgraph=True, backend="aot_eager")
+    g = eager[1]
+    for _ in range(2):
+        a = step(*eager[:1], g, *eager[2:])
+        b = compiled(*comp[:1], g, *comp[2:])
+        assert torch.equal(a, b)
+    for x, y in zip(eager, comp):
+        assert torch.equal(x, y)
