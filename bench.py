@@ -30,6 +30,7 @@ from pathlib import Path
 
 ROOT = Path(__file__).resolve().parent
 HBM_PEAK_GBS = 8000.0  # MI355X HBM3E
+FP64_PEAK_TFLOPS = 78.6  # MI355X FP64 vector
 
 # Per-replica tensor layouts of BASELINE.json's configs.
 MLP_LAYOUT = [(512, 256), (512,), (256, 512), (256,), (10, 256), (10,)]
@@ -559,7 +560,15 @@ def main():
 
     kern_ms = kernel_only_timing(op_name, op_args, kw, max(10, args.steps))
     achieved = nbytes / (kern_ms * 1e-3) / 1e9
+    fp64_roofline = None
     adagrad_f32 = None
+    if op_name == "adagrad":
+        # second bound: the fp64 update, ~6 FP64 FLOPs per active element (fma = 2, incl. one
+        # divide), against the MI355X's 78.6 TFLOP/s FP64 vector peak
+        flops = 6 * (nbytes // bytes_per_elem(args.config))
+        fp64_roofline = {"bound": "fp64", "achieved": round(flops / (kern_ms * 1e-3) / 1e12, 3),
+                         "peak": FP64_PEAK_TFLOPS, "unit": "TFLOP/s",
+                         "frac": round(flops / (kern_ms * 1e-3) / 1e12 / FP64_PEAK_TFLOPS, 4)}
     if op_name == "adagrad":  # the float32 variant on the same state
         f32_ms = kernel_only_timing(op_name, op_args, kw, max(10, args.steps),
                                     extra_flags=TS_ADAGRAD_F32)
@@ -625,6 +634,7 @@ def main():
         "grad_scatter_step": scatter,
         "bf16_state": bf16,
         "adagrad_f32": adagrad_f32,
+        "fp64_roofline": fp64_roofline,
         "snapshot": snapshot,
         "graph_replay": graphed,
         "speedup_vs_python_loop": ({k: round(v / step_ms, 2) for k, v in loop.items()}
