@@ -8,10 +8,12 @@
 // (S = T, or bfloat16 state next to float32 parameters). Three drivers move the
 // bytes, identically for every policy:
 //
-//   stream_kernel   the consolidated (R, T) layout `State` produces: unit inner
-//                   stride, 16-byte aligned rows, T % 4 == 0. Non-temporal
-//                   16-byte loads and stores.
-//   element_kernel  any strides, ragged T, misaligned rows: one element per
+//   stream_kernel   unit inner stride (the consolidated layout `State`
+//                   produces, and ragged or misaligned rows): non-temporal
+//                   16-byte loads and stores from each row's first 16-byte
+//                   boundary, the at most three head and tail elements of a
+//                   row one at a time.
+//   element_kernel  any other strides (transposed views): one element per
 //                   access, same tile geometry.
 //   segment_kernel  the gradient arrives as one tensor per parameter (a segment
 //                   table) instead of the consolidated (R, T) gradient buffer:
@@ -106,9 +108,15 @@ struct Vectors {
   const uint8_t* mask;
 };
 
+// Tiles of kTile elements per row. For the streaming driver, row r's first
+// 16-byte boundary lies head(r) = (4 - (res0 + r * rmod) % 4) % 4 elements in
+// (res0: the base's element offset modulo 4, rmod: the row stride modulo 4,
+// the same for every operand); packs stream from there and the few head and
+// tail elements of each row go one at a time.
 struct Grid {
   int64_t T;
   uint32_t tiles_per_row;
+  uint32_t res0, rmod;
 };
 
 __device__ __forceinline__ void tile_of_block(const Grid& g, uint32_t& r,
@@ -308,14 +316,23 @@ __global__ __launch_bounds__(kThreads) void stream_kernel(KArgs<P> a) {
   P::prologue(a.vec, r, rep);
   const bool load_state = P::reads_state(rep);
 
-  Pack<T>* prow = reinterpret_cast<Pack<T>*>(pg_row<P>(a.x, 0, r) + t0);
-  const Pack<T>* grow = reinterpret_cast<const Pack<T>*>(pg_row<P>(a.x, 1, r) + t0);
+  const int64_t width = a.g.T;
+  const int64_t head = min<int64_t>(width, (4u - (a.g.res0 + r * a.g.rmod) % 4u) % 4u);
+  const int64_t packs_row = (width - head) / kPack;
+  T* const pbase = pg_row<P>(a.x, 0, r);
+  const T* const gbase = pg_row<P>(a.x, 1, r);
+  S* sbase[SS];
+#pragma unroll
+  for (int b = 0; b < NS; ++b) sbase[b] = state_row<P>(a.x, 2 + b, r);
+
+  Pack<T>* prow = reinterpret_cast<Pack<T>*>(pbase + head) + t0 / kPack;
+  const Pack<T>* grow = reinterpret_cast<const Pack<T>*>(gbase + head) + t0 / kPack;
   Pack<S>* srow[SS];
 #pragma unroll
   for (int b = 0; b < NS; ++b) {
-    srow[b] = reinterpret_cast<Pack<S>*>(state_row<P>(a.x, 2 + b, r) + t0);
+    srow[b] = reinterpret_cast<Pack<S>*>(sbase[b] + head) + t0 / kPack;
   }
-  const int64_t packs_left = (a.g.T - t0) / kPack;
+  const int64_t packs_left = packs_row - t0 / kPack;
 
   Pack<T> vp[kUnroll], vg[kUnroll];
   Pack<S> vs[SS][kUnroll];
@@ -352,6 +369,28 @@ __global__ __launch_bounds__(kThreads) void stream_kernel(KArgs<P> a) {
         store_stream(srow[b] + i, vs[b][u]);
       }
     }
+  }
+
+  // The row's unaligned head (tile 0) and ragged tail (last tile), at most
+  // three elements each, one element per thread.
+  int64_t j = -1;
+  if (t0 == 0 && threadIdx.x < head) {
+    j = threadIdx.x;
+  } else if (t0 + kTile >= width && threadIdx.x >= 4 &&
+             head + packs_row * kPack + (threadIdx.x - 4) < width) {
+    j = head + packs_row * kPack + (threadIdx.x - 4);
+  }
+  if (j >= 0) {
+    T pe = pbase[j];
+    S st[SS];
+    if (load_state) {
+#pragma unroll
+      for (int b = 0; b < NS; ++b) st[b] = sbase[b][j];
+    }
+    apply_element<P>(pe, gbase[j], st, load_state, rep, a.maximize);
+    pbase[j] = pe;
+#pragma unroll
+    for (int b = 0; b < NS; ++b) sbase[b][j] = st[b];
   }
 }
 
@@ -666,6 +705,31 @@ bool rows_vectorizable(const Operands<typename P::T>& x, int n) {
   return true;
 }
 
+// The streaming driver takes any unit-inner-stride operands whose 16-byte
+// boundaries fall on the same element index in every row of every operand:
+// element-aligned bases with one common base residue (element offset modulo 4)
+// and row strides congruent modulo 4. Sets res0 / rmod for the grid.
+template <typename P>
+bool rows_streamable(const Operands<typename P::T>& x, int n, uint32_t& res0, uint32_t& rmod) {
+  bool first = true;
+  for (int b = 0; b < n; ++b) {
+    if (x.data[b] == nullptr) continue;
+    const size_t elem = b < 2 ? sizeof(typename P::T) : sizeof(typename P::S);
+    const uintptr_t addr = reinterpret_cast<uintptr_t>(x.data[b]);
+    if (x.stride_t[b] != 1 || addr % elem != 0) return false;
+    const uint32_t res = static_cast<uint32_t>((addr / elem) % kPack);
+    const uint32_t mod = static_cast<uint32_t>(((x.stride_r[b] % kPack) + kPack) % kPack);
+    if (first) {
+      res0 = res;
+      rmod = mod;
+      first = false;
+    } else if (res != res0 || mod != rmod) {
+      return false;
+    }
+  }
+  return true;
+}
+
 bool make_grid(int64_t R, int64_t T, Grid& g, uint32_t& blocks) {
   const int64_t tiles = (T + kTile - 1) / kTile;
   if (R <= 0 || T <= 0 || tiles > INT32_MAX || R > INT32_MAX / tiles) {
@@ -673,6 +737,8 @@ bool make_grid(int64_t R, int64_t T, Grid& g, uint32_t& blocks) {
   }
   g.T = T;
   g.tiles_per_row = static_cast<uint32_t>(tiles);
+  g.res0 = 0;
+  g.rmod = 0;
   blocks = static_cast<uint32_t>(R * tiles);
   return true;
 }
@@ -851,7 +917,7 @@ int launch_dense(const Call& c, int nbufs) {
   };
   return run_step<T>(c, prepare, [&]() -> int {
     const dim3 grid(blocks), block(kThreads);
-    if (c.T % kPack == 0 && rows_vectorizable<P>(a.x, nbufs)) {
+    if (rows_streamable<P>(a.x, nbufs, a.g.res0, a.g.rmod)) {
       hipLaunchKernelGGL(stream_kernel<P>, grid, block, 0, c.stream, a);
     } else {
       hipLaunchKernelGGL(element_kernel<P>, grid, block, 0, c.stream, a);

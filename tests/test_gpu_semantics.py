@@ -267,19 +267,67 @@ def test_odd_widths_bit_exact_to_oracle(T):
     del g, grad
 
 
-def test_misaligned_row_views_take_element_path_bit_exact():
-    """Rows of a column-slice view are not 16-byte aligned: same bits as contiguous."""
-    R, T = 4, 64
-    big = adam_args(R, T + 1, seed=12)
-    view = [t[:, 1:] if t is not None and t.dim() == 2 else t for t in big]
+@pytest.mark.parametrize("offset,extra", [(1, 1), (2, 3), (3, 2), (0, 5), (1, 0)])
+@pytest.mark.parametrize("T", [64, 1023, 2050])
+def test_misaligned_row_views_bit_exact(offset, extra, T):
+    """Column-slice views whose rows start off a 16-byte boundary (a different
+    one on every row when the row stride is not a multiple of 4): the streaming
+    driver's per-row head/tail handling gives the same bits as contiguous
+    buffers; views whose operands disagree on the boundary (here: grads offset
+    differently) take the element path, same bits again."""
+    R = 5
+    big = adam_args(R, T + offset + extra, amsgrad=True, seed=T + offset)
+    view = [t[:, offset:offset + T] if t is not None and t.dim() == 2 else t for t in big]
+    odd_g = adam_args(R, T + 3, seed=99)[1][:, (offset + 1) % 4:(offset + 1) % 4 + T]
     dense = [t.clone().contiguous() if t is not None else None for t in view]
-    dense[5:] = [t.clone() for t in view[5:]]
-    mask = torch.ones(R, dtype=torch.bool, device=DEV)
-    K.adam_step_(*view, mask, amsgrad=False, maximize=True, decoupled_weight_decay=False)
-    K.adam_step_(*dense, mask, amsgrad=False, maximize=True, decoupled_weight_decay=False)
+    mixed = [t.clone() if t is not None else None for t in dense]
+    mixed[1] = odd_g.clone()
+    odd_view = [t.clone() if t is not None else None for t in view]
+    odd_view[1] = odd_g
+    mask = torch.tensor([True, False, True, True, True], device=DEV)
+    kw = dict(amsgrad=True, maximize=True, decoupled_weight_decay=False)
+    K.adam_step_(*view, mask, **kw)
+    K.adam_step_(*dense, mask, **kw)
+    K.adam_step_(*odd_view, mask, **kw)
+    K.adam_step_(*mixed, mask, **kw)
     torch.cuda.synchronize()
-    for a, b in zip(view[:4], dense[:4]):
-        assert torch.equal(a, b)
+    for i in (0, 2, 3, 4, 5):
+        assert torch.equal(view[i], dense[i]), i
+        assert torch.equal(odd_view[i], mixed[i]), i
+
+
+@pytest.mark.parametrize("op", ["sgd", "adagrad", "adam-bf16"])
+def test_ragged_rows_other_policies_bit_exact(op):
+    """Rows of width T = 4k + 3 in one contiguous (R, T) allocation (every row
+    starts at a different 16-byte phase) against the same rows padded to 4k + 4."""
+    R, T = 6, 4099
+    g = torch.Generator(device=DEV).manual_seed(5)
+    rnd = lambda: torch.randn(R, T, device=DEV, generator=g)  # noqa: E731
+    pad = lambda t: torch.nn.functional.pad(t, (0, 1))  # noqa: E731
+    mask = torch.tensor([True, True, False, True, True, True], device=DEV)
+    if op == "sgd":
+        ragged = [rnd(), rnd(), rnd(), torch.ones(R, device=DEV)]
+        hyp = [full(R, 1e-2), full(R, 0.9), full(R, 0.1), full(R, 1e-3)]
+        run = lambda a: K.sgd_step_(a[0], a[1], a[2], a[3], *hyp, mask, nesterov=False,  # noqa
+                                    maximize=False)
+    elif op == "adagrad":
+        ragged = [rnd(), rnd(), rnd().abs(), torch.ones(R, device=DEV)]
+        hyp = [full(R, 1e-2), full(R, 1e-3), full(R, 1e-3), full(R, 1e-10)]
+        run = lambda a: K.adagrad_step_(a[0], a[1], a[2], a[3], *hyp, mask,  # noqa
+                                        maximize=False)
+    else:
+        ragged = [rnd(), rnd(), rnd().to(torch.bfloat16), rnd().abs().to(torch.bfloat16),
+                  torch.ones(R, device=DEV)]
+        hyp = [full(R, 1e-2), full(R, 0.9), full(R, 0.999), full(R, 1e-8), full(R, 1e-2)]
+        run = lambda a: K.adam_step_(a[0], a[1], a[2], a[3], None, a[4], *hyp, mask,  # noqa
+                                     amsgrad=False, maximize=False, decoupled_weight_decay=True)
+    padded = [pad(t) if t.dim() == 2 else t.clone() for t in ragged]
+    run(ragged)
+    run(padded)
+    torch.cuda.synchronize()
+    for a, b in zip(ragged, padded):
+        want = b[:, :T] if b.dim() == 2 else b
+        assert torch.equal(a, want)
 
 
 def test_noncontiguous_and_foreign_dtype_side_inputs():
