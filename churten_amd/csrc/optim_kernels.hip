@@ -10,9 +10,9 @@
 //
 //   stream_kernel   unit inner stride (the consolidated layout `State`
 //                   produces, and ragged or misaligned rows): non-temporal
-//                   16-byte loads and stores from each row's first 16-byte
-//                   boundary, the at most three head and tail elements of a
-//                   row one at a time.
+//                   16-byte loads and stores from each row's first 256-byte
+//                   boundary (tiles never share a cache line), the few head
+//                   and tail elements of a row one at a time.
 //   element_kernel  any other strides (transposed views): one element per
 //                   access, same tile geometry.
 //   segment_kernel  the gradient arrives as one tensor per parameter (a segment
@@ -20,7 +20,8 @@
 //                   the gradient scatter of the training step is fused into the
 //                   update. Optionally the consolidated gradient is written on
 //                   the way through, so `flat_grads` stays what it would have
-//                   been.
+//                   been. Same access pattern as stream_kernel over each
+//                   segment's columns, whatever the segment's offset.
 //
 // Operands are ordered [0] param, [1] grad (both T), [2..] optimizer state (S;
 // Adam: exp_avg, exp_avg_sq, [max_exp_avg_sq]; SGD: [momentum_buffer];
@@ -66,6 +67,17 @@ constexpr int kUnroll = 2;
 constexpr int kPer = kPack * kUnroll;  // elements per thread per tile
 constexpr int64_t kTile = int64_t(kThreads) * kPer;
 
+// Tile boundaries sit on 256-byte boundaries of the (R, T) rows. Consecutive
+// tiles run on different XCDs (each with its own L2); a 128-byte line split
+// between two of them is fetched twice and written back as two partial lines.
+// Measured on the MI355X with the same buffers viewed 16 / 64 / 128 / 0 bytes
+// off a 256-byte boundary: the Adam step took 19% / 8% / 1% / 0% longer.
+constexpr uint32_t kAlignBytes = 256;
+template <typename T>
+constexpr uint32_t align_elems() {
+  return kAlignBytes / sizeof(T);
+}
+
 template <typename T>
 struct alignas(sizeof(T) * kPack) Pack {
   T v[kPack];
@@ -109,10 +121,12 @@ struct Vectors {
 };
 
 // Tiles of kTile elements per row. For the streaming driver, row r's first
-// 16-byte boundary lies head(r) = (4 - (res0 + r * rmod) % 4) % 4 elements in
-// (res0: the base's element offset modulo 4, rmod: the row stride modulo 4,
-// the same for every operand); packs stream from there and the few head and
-// tail elements of each row go one at a time.
+// 256-byte boundary lies head(r) = (A - (res0 + r * rmod) % A) % A elements in
+// (A: 256 bytes in elements of the parameter type; res0: the parameter base's
+// element offset modulo A, rmod: its row stride modulo A); packs stream from
+// there and the head and the at most three tail elements of each row go one at
+// a time. Every operand shares the parameter's phase modulo 4, so the packs are
+// 16-byte aligned in all of them.
 struct Grid {
   int64_t T;
   uint32_t tiles_per_row;
@@ -316,8 +330,9 @@ __global__ __launch_bounds__(kThreads) void stream_kernel(KArgs<P> a) {
   P::prologue(a.vec, r, rep);
   const bool load_state = P::reads_state(rep);
 
+  constexpr uint32_t A = align_elems<T>();
   const int64_t width = a.g.T;
-  const int64_t head = min<int64_t>(width, (4u - (a.g.res0 + r * a.g.rmod) % 4u) % 4u);
+  const int64_t head = min<int64_t>(width, (A - (a.g.res0 + r * a.g.rmod) % A) % A);
   const int64_t packs_row = (width - head) / kPack;
   T* const pbase = pg_row<P>(a.x, 0, r);
   const T* const gbase = pg_row<P>(a.x, 1, r);
@@ -371,16 +386,9 @@ __global__ __launch_bounds__(kThreads) void stream_kernel(KArgs<P> a) {
     }
   }
 
-  // The row's unaligned head (tile 0) and ragged tail (last tile), at most
-  // three elements each, one element per thread.
-  int64_t j = -1;
-  if (t0 == 0 && threadIdx.x < head) {
-    j = threadIdx.x;
-  } else if (t0 + kTile >= width && threadIdx.x >= 4 &&
-             head + packs_row * kPack + (threadIdx.x - 4) < width) {
-    j = head + packs_row * kPack + (threadIdx.x - 4);
-  }
-  if (j >= 0) {
+  // The row's head before its first 256-byte boundary (tile 0) and its at most
+  // three tail elements (last tile), one element per access.
+  const auto one = [&](int64_t j) {
     T pe = pbase[j];
     S st[SS];
     if (load_state) {
@@ -391,6 +399,12 @@ __global__ __launch_bounds__(kThreads) void stream_kernel(KArgs<P> a) {
     pbase[j] = pe;
 #pragma unroll
     for (int b = 0; b < NS; ++b) sbase[b][j] = st[b];
+  };
+  if (t0 == 0) {
+    for (int64_t j = threadIdx.x; j < head; j += kThreads) one(j);
+  }
+  if (t0 + kTile >= width) {
+    for (int64_t j = head + packs_row * kPack + threadIdx.x; j < width; j += kThreads) one(j);
   }
 }
 
@@ -456,7 +470,8 @@ constexpr int kMaxSegments = 64;
 // Up to kMaxSegments per-parameter (R, numel) tensors, each mapped onto the
 // columns [col, col + numel) of the (R, T) layout. tile0 is the prefix sum of
 // the segments' tile counts, so a row has tile0[n] tiles; bit s of `vec_ok`
-// says segment s can take 16-byte accesses.
+// says segment s takes the vector walk (the (R, T) operands are streamable and
+// the segment's data is element-aligned).
 template <typename T>
 struct Segments {
   const T* data[kMaxSegments];
@@ -470,7 +485,8 @@ struct Segments {
 
 template <typename P>
 struct SegArgs {
-  KArgs<P> k;  // k.x.data[1]: consolidated gradient to write, or null
+  KArgs<P> k;  // k.x.data[1]: consolidated gradient to write, or null;
+               // k.g.res0 / rmod: the (R, T) operands' 16-byte phase
   Segments<typename P::T> seg;
 };
 
@@ -482,6 +498,62 @@ __device__ __forceinline__ int segment_of_tile(const uint32_t* tile0, int n, uin
     else hi = mid - 1;
   }
   return lo;
+}
+
+// A segment's tile on the vector walk. The walk follows the (R, T) layout: in
+// row r the segment's first 256-byte boundary lies `head` elements in (head <
+// A, as for the streaming driver); packs of 4 elements stream from there, tile
+// k taking packs [k * kTile / 4, (k + 1) * kTile / 4). Tile 0 also takes the
+// head elements and the segment's last tile the at most three tail elements,
+// one element per access. The per-parameter gradient's rows keep their own
+// alignment: they are read with element-aligned pack loads.
+struct SegTile {
+  int64_t head;   // elements before the first pack
+  int64_t first;  // element index of this tile's first pack
+  int64_t packs;  // packs in this tile (may be <= 0)
+  int64_t tail;   // first tail element (== numel: none)
+  bool has_head, has_tail;
+};
+
+template <typename T>
+__device__ __forceinline__ SegTile seg_tile(uint32_t res0, uint32_t rmod, uint32_t r,
+                                            int64_t col, int64_t numel, int64_t j0) {
+  constexpr uint32_t A = align_elems<T>();
+  SegTile t;
+  const uint32_t phase = (res0 + r * rmod + static_cast<uint32_t>(col % A)) % A;
+  t.head = min<int64_t>(numel, (A - phase) % A);
+  const int64_t packs_seg = (numel - t.head) / kPack;
+  t.first = t.head + j0;
+  t.packs = packs_seg - j0 / kPack;
+  t.tail = t.head + packs_seg * kPack;
+  t.has_head = j0 == 0;
+  t.has_tail = j0 + kTile >= numel;
+  return t;
+}
+
+// Runs fn(j) for the tile's single elements, spread over the threads.
+template <typename Fn>
+__device__ __forceinline__ void seg_singles(const SegTile& t, int64_t numel, Fn&& fn) {
+  if (t.has_head) {
+    for (int64_t j = threadIdx.x; j < t.head; j += kThreads) fn(j);
+  }
+  if (t.has_tail) {
+    for (int64_t j = t.tail + threadIdx.x; j < numel; j += kThreads) fn(j);
+  }
+}
+
+// Packs from element-aligned addresses (a per-parameter gradient's row need
+// not share the (R, T) layout's 16-byte boundaries). gfx950 code runs in
+// unaligned access mode, and hipcc emits the same single global_load_dwordx4
+// (dwordx2 for 16-bit types) for this type as for an aligned pack.
+template <typename T>
+using PackBitsU = uint32_t
+    __attribute__((ext_vector_type(sizeof(T) * kPack / 4), aligned(sizeof(T))));
+
+template <typename T>
+__device__ __forceinline__ Pack<T> load_stream_any(const T* p) {
+  return __builtin_bit_cast(
+      Pack<T>, __builtin_nontemporal_load(reinterpret_cast<const PackBitsU<T>*>(p)));
 }
 
 template <typename P>
@@ -502,18 +574,42 @@ __global__ __launch_bounds__(kThreads) void segment_kernel(SegArgs<P> a) {
   if (!active && (gap || !write_grad)) {
     return;
   }
+  const int64_t numel = a.seg.numel[s];
+  const int64_t col = a.seg.col[s];
   const int64_t j0 = int64_t(local - a.seg.tile0[s]) * kTile;
-  const int64_t cnt = min(kTile, a.seg.numel[s] - j0);
-  const int64_t c0 = a.seg.col[s] + j0;
+  const bool vec = (a.seg.vec_ok >> s) & 1u;
+  // Row r of the segment's columns in the (R, T) operands, and of its gradient
+  // source: the segment's row, or for a gap the consolidated buffer (null:
+  // zero). Only a real segment is stored into the consolidated buffer.
   T* const g_dst =
-      write_grad ? a.k.x.data[1] + int64_t(r) * a.k.x.stride_r[1] + c0 * a.k.x.stride_t[1]
-                 : nullptr;
+      write_grad ? pg_row<P>(a.k.x, 1, r) + col * a.k.x.stride_t[1] : nullptr;
+  const T* g_src = g_dst;
+  int64_t g_stride = write_grad ? a.k.x.stride_t[1] : 0;
+  if (!gap) {
+    g_src = a.seg.data[s] + int64_t(r) * a.seg.stride_r[s];
+    g_stride = 1;
+  }
+  const bool store_grad = write_grad && !gap;
+
   if (!active) {
     // A frozen replica's optimizer state is not touched, but the consolidated
     // gradient is still filled, as the separate scatter would have filled it.
-    const T* g_row = a.seg.data[s] + int64_t(r) * a.seg.stride_r[s] + j0;
-    for (int64_t j = threadIdx.x; j < cnt; j += kThreads) {
-      g_dst[j * a.k.x.stride_t[1]] = g_row[j];
+    if (vec) {
+      const SegTile t = seg_tile<T>(a.k.g.res0, a.k.g.rmod, r, col, numel, j0);
+#pragma unroll
+      for (int u = 0; u < kUnroll; ++u) {
+        const int64_t i = int64_t(u) * kThreads + threadIdx.x;
+        if (i < t.packs) {
+          store_stream(reinterpret_cast<Pack<T>*>(g_dst + t.first) + i,
+                       load_stream_any(g_src + t.first + i * kPack));
+        }
+      }
+      seg_singles(t, numel, [&](int64_t j) { g_dst[j] = g_src[j]; });
+    } else {
+      const int64_t cnt = min(kTile, numel - j0);
+      for (int64_t j = j0 + threadIdx.x; j < j0 + cnt; j += kThreads) {
+        g_dst[j * a.k.x.stride_t[1]] = g_src[j];
+      }
     }
     return;
   }
@@ -521,77 +617,17 @@ __global__ __launch_bounds__(kThreads) void segment_kernel(SegArgs<P> a) {
   typename P::Rep rep;
   P::prologue(a.k.vec, r, rep);
   const bool load_state = P::reads_state(rep);
-
-  // Gradient source: the segment's row, or for a gap the consolidated buffer
-  // (null: zero). Only a real segment is stored into the consolidated buffer.
-  const T* g_src = g_dst;
-  int64_t g_stride = write_grad ? a.k.x.stride_t[1] : 0;
-  if (!gap) {
-    g_src = a.seg.data[s] + int64_t(r) * a.seg.stride_r[s] + j0;
-    g_stride = 1;
-  }
-  const bool store_grad = write_grad && !gap;
   const T zero = narrow<T>(op_t<T>(0));
 
-  T* const prow = pg_row<P>(a.k.x, 0, r) + c0 * a.k.x.stride_t[0];
+  T* const prow = pg_row<P>(a.k.x, 0, r) + col * a.k.x.stride_t[0];
   S* srow[SS];
 #pragma unroll
   for (int b = 0; b < NS; ++b) {
-    srow[b] = state_row<P>(a.k.x, 2 + b, r) + c0 * a.k.x.stride_t[2 + b];
+    srow[b] = state_row<P>(a.k.x, 2 + b, r) + col * a.k.x.stride_t[2 + b];
   }
 
-  int64_t done = 0;  // leading elements handled by the vector loop
-  if ((a.seg.vec_ok >> s) & 1u) {
-    const int64_t packs = cnt / kPack;
-    Pack<T> vp[kUnroll], vg[kUnroll];
-    Pack<S> vs[SS][kUnroll];
-#pragma unroll
-    for (int u = 0; u < kUnroll; ++u) {
-      const int64_t i = int64_t(u) * kThreads + threadIdx.x;
-      if (i < packs) {
-        vp[u] = load_stream(reinterpret_cast<const Pack<T>*>(prow) + i);
-        if (g_src != nullptr) {
-          vg[u] = load_stream(reinterpret_cast<const Pack<T>*>(g_src) + i);
-        } else {
-#pragma unroll
-          for (int k = 0; k < kPack; ++k) vg[u].v[k] = zero;
-        }
-        if (load_state) {
-#pragma unroll
-          for (int b = 0; b < NS; ++b) {
-            vs[b][u] = load_stream(reinterpret_cast<const Pack<S>*>(srow[b]) + i);
-          }
-        }
-      }
-    }
-#pragma unroll
-    for (int u = 0; u < kUnroll; ++u) {
-      const int64_t i = int64_t(u) * kThreads + threadIdx.x;
-      if (i < packs) {
-        if (store_grad) {
-          store_stream(reinterpret_cast<Pack<T>*>(g_dst) + i, vg[u]);
-        }
-#pragma unroll
-        for (int k = 0; k < kPack; ++k) {
-          S st[SS];
-#pragma unroll
-          for (int b = 0; b < NS; ++b) st[b] = vs[b][u].v[k];
-          apply_element<P>(vp[u].v[k], vg[u].v[k], st, load_state, rep, a.k.maximize);
-#pragma unroll
-          for (int b = 0; b < NS; ++b) vs[b][u].v[k] = st[b];
-        }
-        store_stream(reinterpret_cast<Pack<T>*>(prow) + i, vp[u]);
-#pragma unroll
-        for (int b = 0; b < NS; ++b) {
-          store_stream(reinterpret_cast<Pack<S>*>(srow[b]) + i, vs[b][u]);
-        }
-      }
-    }
-    done = packs * kPack;
-  }
-  // Remaining elements (a partial last pack, or the whole tile of a segment
-  // that cannot take vector accesses), one element per thread and access.
-  for (int64_t j = done + threadIdx.x; j < cnt; j += kThreads) {
+  // Element j of the segment, one access per operand.
+  const auto one = [&](int64_t j) {
     T p = prow[j * a.k.x.stride_t[0]];
     const T g = g_src != nullptr ? g_src[j * g_stride] : zero;
     S st[SS];
@@ -606,15 +642,76 @@ __global__ __launch_bounds__(kThreads) void segment_kernel(SegArgs<P> a) {
     }
 #pragma unroll
     for (int b = 0; b < NS; ++b) srow[b][j * a.k.x.stride_t[2 + b]] = st[b];
+  };
+
+  if (!vec) {
+    const int64_t cnt = min(kTile, numel - j0);
+    for (int64_t j = j0 + threadIdx.x; j < j0 + cnt; j += kThreads) one(j);
+    return;
   }
+
+  // Vector walk (unit inner strides): the (R, T) operands' packs are aligned.
+  const SegTile t = seg_tile<T>(a.k.g.res0, a.k.g.rmod, r, col, numel, j0);
+  Pack<T>* const pp = reinterpret_cast<Pack<T>*>(prow + t.first);
+  Pack<S>* sp[SS];
+#pragma unroll
+  for (int b = 0; b < NS; ++b) sp[b] = reinterpret_cast<Pack<S>*>(srow[b] + t.first);
+  Pack<T> vp[kUnroll], vg[kUnroll];
+  Pack<S> vs[SS][kUnroll];
+#pragma unroll
+  for (int u = 0; u < kUnroll; ++u) {
+    const int64_t i = int64_t(u) * kThreads + threadIdx.x;
+    if (i < t.packs) {
+      vp[u] = load_stream(pp + i);
+      if (gap) {
+        if (g_src != nullptr) {
+          vg[u] = load_stream(reinterpret_cast<const Pack<T>*>(g_src + t.first) + i);
+        } else {
+#pragma unroll
+          for (int k = 0; k < kPack; ++k) vg[u].v[k] = zero;
+        }
+      } else {
+        vg[u] = load_stream_any(g_src + t.first + i * kPack);
+      }
+      if (load_state) {
+#pragma unroll
+        for (int b = 0; b < NS; ++b) vs[b][u] = load_stream(sp[b] + i);
+      }
+    }
+  }
+#pragma unroll
+  for (int u = 0; u < kUnroll; ++u) {
+    const int64_t i = int64_t(u) * kThreads + threadIdx.x;
+    if (i < t.packs) {
+      if (store_grad) {
+        store_stream(reinterpret_cast<Pack<T>*>(g_dst + t.first) + i, vg[u]);
+      }
+#pragma unroll
+      for (int k = 0; k < kPack; ++k) {
+        S st[SS];
+#pragma unroll
+        for (int b = 0; b < NS; ++b) st[b] = vs[b][u].v[k];
+        apply_element<P>(vp[u].v[k], vg[u].v[k], st, load_state, rep, a.k.maximize);
+#pragma unroll
+        for (int b = 0; b < NS; ++b) vs[b][u].v[k] = st[b];
+      }
+      store_stream(pp + i, vp[u]);
+#pragma unroll
+      for (int b = 0; b < NS; ++b) store_stream(sp[b] + i, vs[b][u]);
+    }
+  }
+  seg_singles(t, numel, one);
 }
 
 // Plain gradient scatter: copies every segment into its columns of the (R, T)
-// destination, every row (frozen replicas included, as a copy would).
+// destination, every row (frozen replicas included, as a copy would). The
+// vector walk follows the destination's 256-byte boundaries (res0 / rmod as
+// for the update).
 template <typename T>
 struct ScatterArgs {
   T* dst;
   int64_t dst_stride_r;
+  uint32_t res0, rmod;
   Segments<T> seg;
 };
 
@@ -624,27 +721,28 @@ __global__ __launch_bounds__(kThreads) void scatter_kernel(ScatterArgs<T> a) {
   const uint32_t r = blockIdx.x / tiles_per_row;
   const uint32_t local = blockIdx.x - r * tiles_per_row;
   const int s = segment_of_tile(a.seg.tile0, a.seg.n, local);
+  const int64_t numel = a.seg.numel[s];
   const int64_t j0 = int64_t(local - a.seg.tile0[s]) * kTile;
-  const int64_t cnt = min(kTile, a.seg.numel[s] - j0);
-  const T* src = a.seg.data[s] + int64_t(r) * a.seg.stride_r[s] + j0;
-  T* dst = a.dst + int64_t(r) * a.dst_stride_r + a.seg.col[s] + j0;
-  int64_t done = 0;
+  const T* src = a.seg.data[s] + int64_t(r) * a.seg.stride_r[s];
+  T* dst = a.dst + int64_t(r) * a.dst_stride_r + a.seg.col[s];
   if ((a.seg.vec_ok >> s) & 1u) {
-    const int64_t packs = cnt / kPack;
+    const SegTile t = seg_tile<T>(a.res0, a.rmod, r, a.seg.col[s], numel, j0);
     Pack<T> v[kUnroll];
 #pragma unroll
     for (int u = 0; u < kUnroll; ++u) {
       const int64_t i = int64_t(u) * kThreads + threadIdx.x;
-      if (i < packs) v[u] = load_stream(reinterpret_cast<const Pack<T>*>(src) + i);
+      if (i < t.packs) v[u] = load_stream_any(src + t.first + i * kPack);
     }
 #pragma unroll
     for (int u = 0; u < kUnroll; ++u) {
       const int64_t i = int64_t(u) * kThreads + threadIdx.x;
-      if (i < packs) store_stream(reinterpret_cast<Pack<T>*>(dst) + i, v[u]);
+      if (i < t.packs) store_stream(reinterpret_cast<Pack<T>*>(dst + t.first) + i, v[u]);
     }
-    done = packs * kPack;
+    seg_singles(t, numel, [&](int64_t j) { dst[j] = src[j]; });
+    return;
   }
-  for (int64_t j = done + threadIdx.x; j < cnt; j += kThreads) {
+  const int64_t cnt = min(kTile, numel - j0);
+  for (int64_t j = j0 + threadIdx.x; j < j0 + cnt; j += kThreads) {
     dst[j] = src[j];
   }
 }
@@ -690,28 +788,16 @@ bool fill_operands(const ts_rt_buf* bufs, int n, Operands<T>& x, bool grad_optio
   return true;
 }
 
-// The vector path needs unit inner stride and pack-aligned row starts on
-// every (present) operand; operands 0 and 1 hold P::T, the rest P::S.
-template <typename P>
-bool rows_vectorizable(const Operands<typename P::T>& x, int n) {
-  for (int b = 0; b < n; ++b) {
-    if (x.data[b] == nullptr) continue;
-    const size_t elem = b < 2 ? sizeof(typename P::T) : sizeof(typename P::S);
-    if (x.stride_t[b] != 1 || x.stride_r[b] % kPack != 0 ||
-        reinterpret_cast<uintptr_t>(x.data[b]) % (elem * kPack) != 0) {
-      return false;
-    }
-  }
-  return true;
-}
-
 // The streaming driver takes any unit-inner-stride operands whose 16-byte
 // boundaries fall on the same element index in every row of every operand:
 // element-aligned bases with one common base residue (element offset modulo 4)
-// and row strides congruent modulo 4. Sets res0 / rmod for the grid.
+// and row strides congruent modulo 4. Sets res0 / rmod (the parameter's phase
+// modulo 256 bytes) for the grid.
 template <typename P>
 bool rows_streamable(const Operands<typename P::T>& x, int n, uint32_t& res0, uint32_t& rmod) {
+  constexpr uint32_t A = align_elems<typename P::T>();
   bool first = true;
+  uint32_t res4 = 0, mod4 = 0;
   for (int b = 0; b < n; ++b) {
     if (x.data[b] == nullptr) continue;
     const size_t elem = b < 2 ? sizeof(typename P::T) : sizeof(typename P::S);
@@ -720,10 +806,12 @@ bool rows_streamable(const Operands<typename P::T>& x, int n, uint32_t& res0, ui
     const uint32_t res = static_cast<uint32_t>((addr / elem) % kPack);
     const uint32_t mod = static_cast<uint32_t>(((x.stride_r[b] % kPack) + kPack) % kPack);
     if (first) {
-      res0 = res;
-      rmod = mod;
+      res4 = res;
+      mod4 = mod;
+      res0 = static_cast<uint32_t>((addr / elem) % A);
+      rmod = static_cast<uint32_t>(((x.stride_r[b] % A) + A) % A);
       first = false;
-    } else if (res != res0 || mod != rmod) {
+    } else if (res != res4 || mod != mod4) {
       return false;
     }
   }
@@ -815,8 +903,7 @@ int64_t next_chunk(SegmentWalk& w, int64_t R, bool vec_rows, Segments<T>& out) {
     out.tile0[k] = static_cast<uint32_t>(tiles);
     tiles += static_cast<uint64_t>((s.numel + kTile - 1) / kTile);
     if (tiles > UINT32_MAX) return -1;
-    const bool ok = vec_rows && s.col % kPack == 0 && s.stride_r % kPack == 0 &&
-                    reinterpret_cast<uintptr_t>(s.data) % (sizeof(T) * kPack) == 0;
+    const bool ok = vec_rows && reinterpret_cast<uintptr_t>(s.data) % sizeof(T) == 0;
     out.vec_ok |= (ok ? uint64_t(1) : uint64_t(0)) << k;
   }
   out.tile0[out.n] = static_cast<uint32_t>(tiles);
@@ -941,7 +1028,8 @@ int launch_segments(const Call& c, int nbufs, const ts_segment* segs, int n_segs
     if (!fill_kargs<P>(c, nbufs, a.k, true) || !segments_valid(segs, n_segs, c.T)) {
       return false;
     }
-    vec_rows = rows_vectorizable<P>(a.k.x, nbufs);
+    a.k.g = Grid{c.T, 0, 0, 0};
+    vec_rows = rows_streamable<P>(a.k.x, nbufs, a.k.g.res0, a.k.g.rmod);
     return walk_fits<T>(walk, c.R, vec_rows, a.seg);
   };
   return run_step<T>(c, prepare, [&]() -> int {
@@ -1066,8 +1154,10 @@ struct ScatterBody {
     ScatterArgs<T> a;
     a.dst = static_cast<T*>(dst);
     a.dst_stride_r = dst_stride_r;
-    const bool vec_rows = dst_stride_r % kPack == 0 &&
-                          reinterpret_cast<uintptr_t>(dst) % (sizeof(T) * kPack) == 0;
+    constexpr uint32_t A = align_elems<T>();
+    const bool vec_rows = reinterpret_cast<uintptr_t>(dst) % sizeof(T) == 0;
+    a.res0 = static_cast<uint32_t>((reinterpret_cast<uintptr_t>(dst) / sizeof(T)) % A);
+    a.rmod = static_cast<uint32_t>(((dst_stride_r % A) + A) % A);
     const SegmentWalk walk{segs, n_segs, cols, false};
     const bool any = std::any_of(segs, segs + n_segs, [](const ts_segment& s) {
       return s.numel > 0;

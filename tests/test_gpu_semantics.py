@@ -267,14 +267,16 @@ def test_odd_widths_bit_exact_to_oracle(T):
     del g, grad
 
 
-@pytest.mark.parametrize("offset,extra", [(1, 1), (2, 3), (3, 2), (0, 5), (1, 0)])
-@pytest.mark.parametrize("T", [64, 1023, 2050])
+@pytest.mark.parametrize("offset,extra", [(1, 1), (2, 3), (3, 2), (0, 5), (1, 0), (4, 1),
+                                          (17, 3), (40, 0), (63, 2)])
+@pytest.mark.parametrize("T", [5, 30, 64, 1023, 2050])
 def test_misaligned_row_views_bit_exact(offset, extra, T):
-    """Column-slice views whose rows start off a 16-byte boundary (a different
-    one on every row when the row stride is not a multiple of 4): the streaming
-    driver's per-row head/tail handling gives the same bits as contiguous
-    buffers; views whose operands disagree on the boundary (here: grads offset
-    differently) take the element path, same bits again."""
+    """Column-slice views whose rows start off a 16- or 256-byte boundary (a
+    different one on every row when the row stride is not a multiple of 4 or
+    64): the streaming driver's per-row head/tail handling gives the same bits
+    as contiguous buffers, also for rows shorter than the head; views whose
+    operands disagree on the 16-byte boundary (here: grads offset differently)
+    take the element path, same bits again."""
     R = 5
     big = adam_args(R, T + offset + extra, amsgrad=True, seed=T + offset)
     view = [t[:, offset:offset + T] if t is not None and t.dim() == 2 else t for t in big]
@@ -294,6 +296,24 @@ def test_misaligned_row_views_bit_exact(offset, extra, T):
     for i in (0, 2, 3, 4, 5):
         assert torch.equal(view[i], dense[i]), i
         assert torch.equal(odd_view[i], mixed[i]), i
+
+
+@pytest.mark.parametrize("dtype", [torch.float64, torch.float16, torch.bfloat16])
+@pytest.mark.parametrize("offset", [1, 6, 31, 127])
+def test_misaligned_row_views_other_dtypes_bit_exact(dtype, offset):
+    """As above for the other parameter types (256 bytes = 32 / 128 elements):
+    heads of up to 127 elements per row."""
+    R, T = 5, 1500
+    big = adam_args(R, T + offset + 3, seed=offset, dtype=dtype)
+    view = [t[:, offset:offset + T] if t is not None and t.dim() == 2 else t for t in big]
+    dense = [t.clone().contiguous() if t is not None else None for t in view]
+    mask = torch.tensor([True, True, False, True, True], device=DEV)
+    kw = dict(amsgrad=False, maximize=False, decoupled_weight_decay=True)
+    K.adam_step_(*view, mask, **kw)
+    K.adam_step_(*dense, mask, **kw)
+    torch.cuda.synchronize()
+    for i in (0, 2, 3, 5):
+        assert torch.equal(view[i], dense[i]), i
 
 
 @pytest.mark.parametrize("op", ["sgd", "adagrad", "adam-bf16"])

@@ -79,6 +79,26 @@ def make_grads(shapes, R, dtype, device, gen, strided: bool):
     return out
 
 
+def at_offset(t, off: int):
+    """A copy of ``t`` whose storage starts ``off`` elements into a flat buffer
+    (data off the 16-byte grid for off % 4 != 0)."""
+    flat = torch.empty(t.numel() + off, dtype=t.dtype, device=t.device)
+    out = flat[off:].view(t.shape)
+    out.copy_(t)
+    return out
+
+
+def column_view(t, off: int):
+    """A copy of the (R, T) ``t`` as columns [off, off + T) of an (R, T + off + 1)
+    buffer: rows start ``off`` elements past a boundary and the row stride
+    changes residue."""
+    R, T = t.shape
+    buf = torch.empty(R, T + off + 1, dtype=t.dtype, device=t.device)
+    out = buf[:, off:off + T]
+    out.copy_(t)
+    return out
+
+
 def scatter_reference(dst, grads, cols):
     for g, c in zip(grads, cols):
         n = g[0].numel()
@@ -169,9 +189,11 @@ def clone_all(xs):
 
 
 def run_both(device, op, kw, kind, dtype, with_out, strided_grads, strided_state, seed,
-             n_steps=2, state_dtype=None):
+             n_steps=2, state_dtype=None, offset=0):
     """Runs ``n_steps`` segmented steps and the same steps as scatter +
-    consolidated update, from identical starting state; returns both."""
+    consolidated update, from identical starting state; returns both. With
+    ``offset`` the segmented call's (R, T) operands are ``column_view``s and its
+    gradients start ``offset`` elements into their storage."""
     R = 5
     shapes, cols, T = layout(kind, seed)
     gen = torch.Generator().manual_seed(seed + 100)
@@ -180,13 +202,19 @@ def run_both(device, op, kw, kind, dtype, with_out, strided_grads, strided_state
     mask = torch.tensor([True, False, True, True, False], device=device)
     G0 = torch.randn(R, T, generator=gen).to(device, dtype)  # stale gradient contents
     a = dict(p=p, st=st, steps=steps, G=G0.clone() if with_out else None)
+    if offset:
+        a["p"] = column_view(p, offset)
+        a["st"] = [column_view(x, offset) if x is not None else None for x in st]
+        if with_out:
+            a["G"] = column_view(G0, offset)
     b = dict(p=p.clone(), st=clone_all(st), steps=steps.clone(),
              G=G0.clone() if with_out else torch.zeros_like(G0))
     for _ in range(n_steps):
         grads = make_grads(shapes, R, dtype, device, gen, strided_grads)
+        seg_grads = [at_offset(g, offset) for g in grads] if offset else grads
         # order of the table must not matter
         order = list(reversed(range(len(grads))))
-        out = segments_call(op, a["p"], [grads[i] for i in order], [cols[i] for i in order],
+        out = segments_call(op, a["p"], [seg_grads[i] for i in order], [cols[i] for i in order],
                             a["G"], a["st"], a["steps"], hyp, mask, flags)
         assert out.shape == () and out.item() == 0
         if not with_out:
@@ -254,6 +282,38 @@ def test_gpu_segments_strided_state_buffers(variant, kind):
                     strided_state=True, seed=3)
     torch.cuda.synchronize()
     assert_same(a, b, True)
+
+
+@pytest.mark.gpu
+@pytest.mark.parametrize("variant", VARIANTS, ids=vid)
+@pytest.mark.parametrize("offset", [1, 2, 3])
+@pytest.mark.parametrize("dtype", DTYPES, ids=str)
+def test_gpu_segments_misaligned_operands(variant, offset, dtype):
+    """(R, T) operands whose rows start off the 16-byte grid, with a row stride
+    of another residue, and gradients at odd element offsets: the vector walk
+    follows each consolidated row's own boundaries."""
+    op, kw = variant
+    for kind, with_out in (("big", True), ("ragged", False)):
+        a, b = run_both("cuda", op, kw, kind, dtype, with_out, strided_grads=False,
+                        strided_state=False, seed=21 + offset, offset=offset)
+        torch.cuda.synchronize()
+        assert_same(a, b, with_out)
+
+
+@pytest.mark.gpu
+@pytest.mark.parametrize("offset", [1, 2, 3])
+@pytest.mark.parametrize("dtype", DTYPES, ids=str)
+def test_gpu_scatter_misaligned_destination(offset, dtype):
+    R = 5
+    shapes, cols, T = layout("big", 4)
+    gen = torch.Generator().manual_seed(offset)
+    grads = [at_offset(g, offset) for g in make_grads(shapes, R, dtype, "cuda", gen, False)]
+    want = torch.randn(R, T, generator=gen).to("cuda", dtype)
+    got = column_view(want, offset)
+    scatter_reference(want, grads, cols)
+    K.scatter_grads_(got, grads, cols)
+    torch.cuda.synchronize()
+    assert bits_equal(got, want)
 
 
 @pytest.mark.gpu
