@@ -5,7 +5,7 @@
 // AdagradF32Policy): its per-replica prologue (hyperparameters, bias
 // corrections, is_first_step, corrected_lr) and its per-element update, both
 // from optim_math.h, over a parameter type T and an optimizer-state type S
-// (S = T, or bfloat16 state next to float32 parameters). Three drivers move the
+// (S = T, or bfloat16 state next to float32 parameters). Four drivers move the
 // bytes, identically for every policy:
 //
 //   stream_kernel   unit inner stride (the consolidated layout `State`
@@ -13,8 +13,13 @@
 //                   16-byte loads and stores from each row's first 256-byte
 //                   boundary (tiles never share a cache line), the few head
 //                   and tail elements of a row one at a time.
-//   element_kernel  any other strides (transposed views): one element per
-//                   access, same tile geometry.
+//   column_kernel   unit replica stride on every operand (transposed views,
+//                   as an outer vmap over a non-leading dimension gives): each
+//                   thread keeps one replica and walks columns, so the threads
+//                   of a workgroup read consecutive replicas -- contiguous
+//                   memory.
+//   element_kernel  any other strides: one element per access, same tile
+//                   geometry as stream_kernel.
 //   segment_kernel  the gradient arrives as one tensor per parameter (a segment
 //                   table) instead of the consolidated (R, T) gradient buffer:
 //                   the gradient scatter of the training step is fused into the
@@ -38,6 +43,9 @@
 // scalar loads) and derive the per-replica constants, then stream their tile.
 // All drivers inline the same per-element update, so the same element gives
 // the same bits whichever driver processed it.
+//
+// (column_kernel instead enumerates (column block, replica block) pairs and
+// tests the flag per thread.)
 //
 // Everything is enqueued on the caller's stream; nothing is allocated.
 
@@ -462,6 +470,92 @@ __global__ __launch_bounds__(kThreads) void element_kernel(KArgs<P> a) {
   }
 }
 
+// Replica-minor operands: every (R, T) operand has unit replica stride (the
+// transposed views an outer vmap over a non-leading dimension produces, or
+// (T, R) buffers seen as (R, T)). A row-walking workgroup would touch one
+// element per cache line there, so this driver turns the walk around: a
+// workgroup covers `rb` consecutive replicas times a block of columns, each
+// thread keeps one replica (its hyperparameters and per-replica constants,
+// computed once) and walks columns `cpi` apart, so the threads of one
+// iteration read consecutive replicas of consecutive columns -- contiguous
+// memory when the column stride is R.
+constexpr int kColThreads = 256;
+constexpr int kColIters = 32;  // columns per thread per workgroup
+constexpr int kColUnroll = 4;
+
+struct ColGrid {
+  int64_t R, T;
+  uint32_t rb;         // replicas per workgroup, min(R, kColThreads)
+  uint32_t cpi;        // columns per iteration, kColThreads / rb
+  uint32_t n_rblocks;  // ceil(R / rb)
+};
+
+template <typename P>
+struct ColArgs {
+  Operands<typename P::T> x;
+  Vectors<typename P::T> vec;
+  ColGrid g;
+  bool maximize;
+};
+
+template <typename P>
+__global__ __launch_bounds__(kColThreads) void column_kernel(ColArgs<P> a) {
+  using T = typename P::T;
+  using S = typename P::S;
+  constexpr int NS = P::NS;
+  constexpr int SS = state_slots<P>();
+  const uint32_t rblk = blockIdx.x % a.g.n_rblocks;
+  const uint32_t cblk = blockIdx.x / a.g.n_rblocks;
+  const uint32_t rr = threadIdx.x % a.g.rb;
+  const uint32_t cc = threadIdx.x / a.g.rb;
+  const int64_t r = int64_t(rblk) * a.g.rb + rr;
+  // Threads past the last replica or column lane, and frozen replicas, have
+  // nothing to do (the workgroup has no barrier).
+  if (cc >= a.g.cpi || r >= a.g.R || !a.vec.mask[r]) {
+    return;
+  }
+  typename P::Rep rep;
+  P::prologue(a.vec, static_cast<uint32_t>(r), rep);
+  const bool load_state = P::reads_state(rep);
+
+  T* const pcol = a.x.data[0] + r;
+  const T* const gcol = a.x.data[1] + r;
+  S* scol[SS];
+#pragma unroll
+  for (int b = 0; b < NS; ++b) scol[b] = reinterpret_cast<S*>(a.x.data[2 + b]) + r;
+  const int64_t t_first = int64_t(cblk) * a.g.cpi * kColIters + cc;
+
+  for (int j = 0; j < kColIters; j += kColUnroll) {
+    T vp[kColUnroll], vg[kColUnroll];
+    S vs[SS][kColUnroll];
+#pragma unroll
+    for (int u = 0; u < kColUnroll; ++u) {
+      const int64_t t = t_first + int64_t(j + u) * a.g.cpi;
+      if (t < a.g.T) {
+        vp[u] = pcol[t * a.x.stride_t[0]];
+        vg[u] = gcol[t * a.x.stride_t[1]];
+        if (load_state) {
+#pragma unroll
+          for (int b = 0; b < NS; ++b) vs[b][u] = scol[b][t * a.x.stride_t[2 + b]];
+        }
+      }
+    }
+#pragma unroll
+    for (int u = 0; u < kColUnroll; ++u) {
+      const int64_t t = t_first + int64_t(j + u) * a.g.cpi;
+      if (t < a.g.T) {
+        S st[SS];
+#pragma unroll
+        for (int b = 0; b < NS; ++b) st[b] = vs[b][u];
+        apply_element<P>(vp[u], vg[u], st, load_state, rep, a.maximize);
+        pcol[t * a.x.stride_t[0]] = vp[u];
+#pragma unroll
+        for (int b = 0; b < NS; ++b) scol[b][t * a.x.stride_t[2 + b]] = st[b];
+      }
+    }
+  }
+}
+
 // ---------------------------------------------------------------------------
 // Segmented gradients
 // ---------------------------------------------------------------------------
@@ -818,6 +912,31 @@ bool rows_streamable(const Operands<typename P::T>& x, int n, uint32_t& res0, ui
   return true;
 }
 
+// Every present operand has unit replica stride (and R > 1, where that says
+// anything): the column driver's layout.
+template <typename T>
+bool replica_minor(const Operands<T>& x, int n) {
+  for (int b = 0; b < n; ++b) {
+    if (x.data[b] != nullptr && x.stride_r[b] != 1) return false;
+  }
+  return true;
+}
+
+bool make_col_grid(int64_t R, int64_t T, ColGrid& g, uint32_t& blocks) {
+  if (R <= 1 || T <= 0) return false;
+  g.R = R;
+  g.T = T;
+  g.rb = static_cast<uint32_t>(std::min<int64_t>(R, kColThreads));
+  g.cpi = kColThreads / g.rb;
+  const int64_t n_rblocks = (R + g.rb - 1) / g.rb;
+  const int64_t cols_per_block = int64_t(g.cpi) * kColIters;
+  const int64_t n_cblocks = (T + cols_per_block - 1) / cols_per_block;
+  if (n_rblocks > INT32_MAX / n_cblocks) return false;
+  g.n_rblocks = static_cast<uint32_t>(n_rblocks);
+  blocks = static_cast<uint32_t>(n_rblocks * n_cblocks);
+  return true;
+}
+
 bool make_grid(int64_t R, int64_t T, Grid& g, uint32_t& blocks) {
   const int64_t tiles = (T + kTile - 1) / kTile;
   if (R <= 0 || T <= 0 || tiles > INT32_MAX || R > INT32_MAX / tiles) {
@@ -1004,8 +1123,16 @@ int launch_dense(const Call& c, int nbufs) {
   };
   return run_step<T>(c, prepare, [&]() -> int {
     const dim3 grid(blocks), block(kThreads);
+    ColArgs<P> ca;
+    uint32_t col_blocks = 0;
     if (rows_streamable<P>(a.x, nbufs, a.g.res0, a.g.rmod)) {
       hipLaunchKernelGGL(stream_kernel<P>, grid, block, 0, c.stream, a);
+    } else if (replica_minor(a.x, nbufs) && make_col_grid(c.R, c.T, ca.g, col_blocks)) {
+      ca.x = a.x;
+      ca.vec = a.vec;
+      ca.maximize = a.maximize;
+      hipLaunchKernelGGL(column_kernel<P>, dim3(col_blocks), dim3(kColThreads), 0, c.stream,
+                         ca);
     } else {
       hipLaunchKernelGGL(element_kernel<P>, grid, block, 0, c.stream, a);
     }

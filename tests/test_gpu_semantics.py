@@ -350,6 +350,72 @@ def test_ragged_rows_other_policies_bit_exact(op):
         assert torch.equal(a, want)
 
 
+def _replica_minor(t: torch.Tensor, pad: int) -> torch.Tensor:
+    """The (R, T) values as a view of a (T, R + pad) buffer: unit replica stride."""
+    R, T = t.shape
+    back = torch.empty(T, R + pad, dtype=t.dtype, device=t.device)
+    view = back[:, :R].t()
+    view.copy_(t)
+    return view
+
+
+@pytest.mark.parametrize("op", ["adam-amsgrad", "adamw", "sgd-nesterov", "sgd-first", "adagrad",
+                                "adagrad-f32", "adam-bf16", "adam-f64"])
+@pytest.mark.parametrize("R,T", [(2, 1), (3, 1000), (64, 33), (100, 517), (257, 40), (600, 9)])
+@pytest.mark.parametrize("pad", [0, 3])
+def test_replica_minor_views_bit_exact(op, R, T, pad):
+    """Operands with unit replica stride ((T, R) buffers, optionally padded, seen
+    as (R, T): what an outer vmap over a non-leading dimension hands over) take
+    the column driver: the same bits as contiguous buffers, frozen replicas
+    untouched."""
+    g = torch.Generator(device=DEV).manual_seed(R * 1000 + T)
+    dt = torch.float64 if op == "adam-f64" else torch.float32
+    st_dt = torch.bfloat16 if op == "adam-bf16" else dt
+    rnd = lambda dtype=dt: torch.randn(R, T, device=DEV, generator=g).to(dtype)  # noqa: E731
+    pos = lambda dtype=dt: rnd(dtype).abs()  # noqa: E731
+    vec = lambda lo, hi: (lo + (hi - lo) * torch.rand(R, device=DEV, generator=g)).to(dt)  # noqa
+    mask = torch.rand(R, device=DEV, generator=g) < 0.7
+    mask[0] = False
+    steps = torch.randint(0 if op == "sgd-first" else 1, 50, (R,), device=DEV,
+                          generator=g).to(dt)
+    if op == "sgd-first":
+        steps.zero_()
+    if op.startswith("adam"):
+        ams = op == "adam-amsgrad"
+        bufs = [rnd(), rnd(), rnd(st_dt), pos(st_dt)] + ([pos(st_dt)] if ams else [])
+        hyp = [vec(1e-3, 1e-2), vec(0.8, 0.95), vec(0.99, 0.9999), vec(1e-8, 1e-6),
+               vec(0.0, 1e-2)]
+        kw = dict(amsgrad=ams, maximize=op == "adam-bf16",
+                  decoupled_weight_decay=op != "adam-amsgrad")
+
+        def run(b, s):
+            K.adam_step_(b[0], b[1], b[2], b[3], b[4] if ams else None, s, *hyp, mask, **kw)
+    elif op.startswith("sgd"):
+        bufs = [rnd(), rnd(), rnd()]
+        hyp = [vec(1e-3, 1e-1), vec(0.5, 0.9), torch.zeros(R, device=DEV), vec(0.0, 1e-2)]
+
+        def run(b, s):
+            K.sgd_step_(b[0], b[1], b[2], s, *hyp, mask, nesterov=True, maximize=False)
+    else:
+        bufs = [rnd(), rnd(), pos()]
+        hyp = [vec(1e-3, 1e-1), vec(0.0, 0.1), vec(0.0, 1e-2), vec(1e-10, 1e-8)]
+        f = K.adagrad_step_f32_ if op == "adagrad-f32" else K.adagrad_step_
+
+        def run(b, s):
+            f(b[0], b[1], b[2], s, *hyp, mask, maximize=True)
+    view = [_replica_minor(t, pad) for t in bufs]
+    dense = [t.clone() for t in bufs]
+    before = [t.clone() for t in bufs]
+    s_view, s_dense = steps.clone(), steps.clone()
+    run(view, s_view)
+    run(dense, s_dense)
+    torch.cuda.synchronize()
+    assert torch.equal(s_view, s_dense)
+    for i, (a, b) in enumerate(zip(view, dense)):
+        assert torch.equal(a, b), i
+        assert torch.equal(a[~mask], before[i][~mask]), i
+
+
 def test_noncontiguous_and_foreign_dtype_side_inputs():
     """(R,) inputs may be strided or float64 and steps float64, mask float:
     normalised like the reference (to the param dtype / bool)."""
