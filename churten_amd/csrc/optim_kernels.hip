@@ -923,7 +923,7 @@ bool replica_minor(const Operands<T>& x, int n) {
 }
 
 bool make_col_grid(int64_t R, int64_t T, ColGrid& g, uint32_t& blocks) {
-  if (R <= 1 || T <= 0) return false;
+  if (R <= 1 || R > INT32_MAX || T <= 0) return false;
   g.R = R;
   g.T = T;
   g.rb = static_cast<uint32_t>(std::min<int64_t>(R, kColThreads));
