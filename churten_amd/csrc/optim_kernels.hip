@@ -141,6 +141,10 @@ struct Grid {
   uint32_t res0, rmod;
 };
 
+// Integer minimum for tile bounds (a plain compare-and-select; HIP's generic
+// min template goes through double for 64-bit integers).
+__device__ __forceinline__ int64_t imin(int64_t a, int64_t b) { return a < b ? a : b; }
+
 __device__ __forceinline__ void tile_of_block(const Grid& g, uint32_t& r,
                                               int64_t& t0) {
   const uint32_t tile = blockIdx.x;
@@ -340,7 +344,7 @@ __global__ __launch_bounds__(kThreads) void stream_kernel(KArgs<P> a) {
 
   constexpr uint32_t A = align_elems<T>();
   const int64_t width = a.g.T;
-  const int64_t head = min<int64_t>(width, (A - (a.g.res0 + r * a.g.rmod) % A) % A);
+  const int64_t head = imin(width, (A - (a.g.res0 + r * a.g.rmod) % A) % A);
   const int64_t packs_row = (width - head) / kPack;
   T* const pbase = pg_row<P>(a.x, 0, r);
   const T* const gbase = pg_row<P>(a.x, 1, r);
@@ -615,7 +619,7 @@ __device__ __forceinline__ SegTile seg_tile(uint32_t res0, uint32_t rmod, uint32
   constexpr uint32_t A = align_elems<T>();
   SegTile t;
   const uint32_t phase = (res0 + r * rmod + static_cast<uint32_t>(col % A)) % A;
-  t.head = min<int64_t>(numel, (A - phase) % A);
+  t.head = imin(numel, (A - phase) % A);
   const int64_t packs_seg = (numel - t.head) / kPack;
   t.first = t.head + j0;
   t.packs = packs_seg - j0 / kPack;
@@ -700,7 +704,7 @@ __global__ __launch_bounds__(kThreads) void segment_kernel(SegArgs<P> a) {
       }
       seg_singles(t, numel, [&](int64_t j) { g_dst[j] = g_src[j]; });
     } else {
-      const int64_t cnt = min(kTile, numel - j0);
+      const int64_t cnt = imin(kTile, numel - j0);
       for (int64_t j = j0 + threadIdx.x; j < j0 + cnt; j += kThreads) {
         g_dst[j * a.k.x.stride_t[1]] = g_src[j];
       }
@@ -739,7 +743,7 @@ __global__ __launch_bounds__(kThreads) void segment_kernel(SegArgs<P> a) {
   };
 
   if (!vec) {
-    const int64_t cnt = min(kTile, numel - j0);
+    const int64_t cnt = imin(kTile, numel - j0);
     for (int64_t j = j0 + threadIdx.x; j < j0 + cnt; j += kThreads) one(j);
     return;
   }
@@ -835,7 +839,7 @@ __global__ __launch_bounds__(kThreads) void scatter_kernel(ScatterArgs<T> a) {
     seg_singles(t, numel, [&](int64_t j) { dst[j] = src[j]; });
     return;
   }
-  const int64_t cnt = min(kTile, numel - j0);
+  const int64_t cnt = imin(kTile, numel - j0);
   for (int64_t j = j0 + threadIdx.x; j < j0 + cnt; j += kThreads) {
     dst[j] = src[j];
   }
