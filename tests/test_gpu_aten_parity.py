@@ -83,6 +83,8 @@ def test_adam_rows_bit_identical_to_aten(T, amsgrad, maximize, decoupled, wd, dt
         assert steps[r].item() == ref[r][4].item() == 3
 
 
+# torch warns that is_first_step means nothing without momentum buffers.
+@pytest.mark.filterwarnings("ignore:`is_first_step` argument has no effect")
 @pytest.mark.parametrize("T", [64, 45, 70001])
 @pytest.mark.parametrize("momentum,dampening,wd,nesterov,maximize", [
     c for c in itertools.product([0.0, 0.9], [0.0, 0.3], [0.0, 1e-2], [False, True],
