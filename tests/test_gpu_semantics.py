@@ -360,7 +360,7 @@ def _replica_minor(t: torch.Tensor, pad: int) -> torch.Tensor:
 
 
 @pytest.mark.parametrize("op", ["adam-amsgrad", "adamw", "sgd-nesterov", "sgd-first", "adagrad",
-                                "adagrad-f32", "adam-bf16", "adam-f64"])
+                                "adagrad-f32", "adam-bf16", "adam-f64", "adam-f16", "adam-bf16p"])
 @pytest.mark.parametrize("R,T", [(2, 1), (3, 1000), (64, 33), (100, 517), (257, 40), (600, 9)])
 @pytest.mark.parametrize("pad", [0, 3])
 def test_replica_minor_views_bit_exact(op, R, T, pad):
@@ -369,7 +369,8 @@ def test_replica_minor_views_bit_exact(op, R, T, pad):
     the column driver: the same bits as contiguous buffers, frozen replicas
     untouched."""
     g = torch.Generator(device=DEV).manual_seed(R * 1000 + T)
-    dt = torch.float64 if op == "adam-f64" else torch.float32
+    dt = {"adam-f64": torch.float64, "adam-f16": torch.float16,
+          "adam-bf16p": torch.bfloat16}.get(op, torch.float32)
     st_dt = torch.bfloat16 if op == "adam-bf16" else dt
     rnd = lambda dtype=dt: torch.randn(R, T, device=DEV, generator=g).to(dtype)  # noqa: E731
     pos = lambda dtype=dt: rnd(dtype).abs()  # noqa: E731
