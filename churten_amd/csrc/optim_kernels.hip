@@ -584,7 +584,7 @@ struct Segments {
 template <typename P>
 struct SegArgs {
   KArgs<P> k;  // k.x.data[1]: consolidated gradient to write, or null;
-               // k.g.res0 / rmod: the (R, T) operands' 16-byte phase
+               // k.g.res0 / rmod: the params rows' 256-byte phase
   Segments<typename P::T> seg;
 };
 
