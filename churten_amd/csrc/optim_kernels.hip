@@ -9,10 +9,11 @@
 // bytes, identically for every policy:
 //
 //   stream_kernel   unit inner stride (the consolidated layout `State`
-//                   produces, and ragged or misaligned rows): non-temporal
-//                   16-byte loads and stores from each row's first 256-byte
-//                   boundary (tiles never share a cache line), the few head
-//                   and tail elements of a row one at a time.
+//                   produces, and ragged or misaligned rows): one wavefront
+//                   per 512-element tile, non-temporal 16-byte loads and
+//                   stores from each row's first 256-byte boundary (tiles never
+//                   share a cache line), the few head and tail elements of a
+//                   row one at a time; large launches cap residency per CU.
 //   column_kernel   unit replica stride on every operand (transposed views,
 //                   as an outer vmap over a non-leading dimension gives): each
 //                   thread keeps one replica and walks columns, so the threads
@@ -63,17 +64,22 @@
 namespace churten {
 namespace {
 
-// Launch shape, measured on the MI355X over the 52 GB north-star state: 128
-// threads x 2 packs of 4 elements per thread (1024-element tiles) with
-// non-temporal vector loads and stores gave the best HBM throughput of the
-// shapes tried (64..1024 threads, 1..8 packs, persistent grid-stride loops,
-// XCD-contiguous tile order); non-temporal hints on both loads and stores were
-// worth ~10% over plain accesses, either alone nothing.
+// Launch shape, measured on the MI355X over the 52 GB north-star state: 2
+// packs of 4 elements per thread with non-temporal vector loads and stores
+// (non-temporal hints on both loads and stores were worth ~10% over plain
+// accesses, either alone nothing). The streaming driver runs one wavefront per
+// workgroup (512-element tiles) under a residency cap (below): of 64/128/256
+// threads x 1/2/4 packs x 8-24 resident waves per CU, that was fastest,
+// ahead of 128 x 2 with its best cap by 2-6% and uncapped 128 x 2 by 6-10%.
+// The other drivers keep 128 threads (1024-element tiles), where their own
+// sweeps put them.
 constexpr int kThreads = 128;
 constexpr int kPack = 4;
 constexpr int kUnroll = 2;
 constexpr int kPer = kPack * kUnroll;  // elements per thread per tile
 constexpr int64_t kTile = int64_t(kThreads) * kPer;
+constexpr int kStreamThreads = 64;
+constexpr int64_t kStreamTile = int64_t(kStreamThreads) * kPer;
 
 // Tile boundaries sit on 256-byte boundaries of the (R, T) rows. Consecutive
 // tiles run on different XCDs (each with its own L2); a 128-byte line split
@@ -145,11 +151,12 @@ struct Grid {
 // min template goes through double for 64-bit integers).
 __device__ __forceinline__ int64_t imin(int64_t a, int64_t b) { return a < b ? a : b; }
 
+template <int64_t TILE>
 __device__ __forceinline__ void tile_of_block(const Grid& g, uint32_t& r,
                                               int64_t& t0) {
   const uint32_t tile = blockIdx.x;
   r = tile / g.tiles_per_row;
-  t0 = int64_t(tile - r * g.tiles_per_row) * kTile;
+  t0 = int64_t(tile - r * g.tiles_per_row) * TILE;
 }
 
 template <typename T>
@@ -161,21 +168,29 @@ __device__ __forceinline__ double hyper_at(const T* h, uint32_t r) {
 // Policies
 // ---------------------------------------------------------------------------
 // Residency cap of the streaming driver. A large streaming launch runs faster
-// with fewer workgroups resident per CU than the register budget allows (12):
-// measured on the MI355X over config-5-sized fp32 state, 7 per CU for Adam
-// (+2.4-4.4%) and 8 for SGD with momentum and Adagrad (+4-6%). bfloat16 state
-// lost with any cap and fp64 gained nothing; those, 16-bit parameters and the
-// other drivers keep full residency. The cap is dynamic LDS that the
-// kernel never touches (160 KiB per CU / bytes per workgroup), so it changes
-// residency and nothing else. `kStreamLds` is each policy's reservation; small
-// grids (under kCapMinBlocks workgroups) launch without it, since there the
-// cap would only serialise the launch.
+// with fewer one-wave workgroups resident per CU than the register budget
+// allows (24): measured on the MI355X over config-5-sized fp32 state (same
+// buffers, interleaved, several processes), 14 per CU for Adam, 12 with
+// amsgrad, 14 for SGD with momentum and 16 for Adagrad, +3-10% over no cap.
+// bfloat16 state lost with any cap and fp64 gained nothing; those, 16-bit
+// parameters and the other drivers keep full residency. The cap is dynamic
+// LDS that the kernel never touches (the smallest 256-byte multiple that fits
+// only n workgroups in the CU's 160 KiB), so it changes residency and nothing
+// else. `kStreamLds` is each policy's reservation; small grids (under
+// kCapMinBlocks workgroups) launch without it, since there the cap would only
+// serialise the launch.
+constexpr uint32_t kLdsPerCU = 160 * 1024;
+constexpr uint32_t lds_for_residency(uint32_t n) {
+  uint32_t x = (kLdsPerCU / n) / 256 * 256;
+  while (kLdsPerCU / x > n) x += 256;
+  return x;
+}
 template <typename T, typename S>
-constexpr uint32_t kResidency7 =
-    std::is_same<T, float>::value && std::is_same<S, float>::value ? 22528u : 0u;
+constexpr bool kFp32State = std::is_same<T, float>::value && std::is_same<S, float>::value;
 template <typename T, typename S>
-constexpr uint32_t kResidency8 =
-    std::is_same<T, float>::value && std::is_same<S, float>::value ? 20480u : 0u;
+constexpr uint32_t residency_lds(uint32_t n) {
+  return kFp32State<T, S> ? lds_for_residency(n) : 0u;
+}
 constexpr uint32_t kCapMinBlocks = 8192;
 
 // Every policy has a parameter/gradient type T and an optimizer-state type S:
@@ -191,7 +206,7 @@ struct AdamPolicy {
   using S = S_;
   using M = op_t<T>;
   static constexpr int NS = AMSGRAD ? 3 : 2;
-  static constexpr uint32_t kStreamLds = kResidency7<T, S>;
+  static constexpr uint32_t kStreamLds = residency_lds<T, S>(AMSGRAD ? 12 : 14);
   struct Rep {
     AdamHyper h;
     M bc1, bc2s;
@@ -225,7 +240,7 @@ struct SgdPolicy {
   using S = S_;
   using M = op_t<T>;
   static constexpr int NS = HAS_BUF ? 1 : 0;
-  static constexpr uint32_t kStreamLds = HAS_BUF ? kResidency8<T, S> : 0u;
+  static constexpr uint32_t kStreamLds = HAS_BUF ? residency_lds<T, S>(14) : 0u;
   struct Rep {
     SgdHyper<double> h;
     bool first;
@@ -255,7 +270,7 @@ struct AdagradPolicy {
   using S = S_;
   using M = op_t<T>;
   static constexpr int NS = 1;
-  static constexpr uint32_t kStreamLds = kResidency8<T, S>;
+  static constexpr uint32_t kStreamLds = residency_lds<T, S>(16);
   struct Rep {
     AdagradHyper h;
   };
@@ -280,7 +295,7 @@ struct AdagradF32Policy {
   using S = S_;
   using M = float;
   static constexpr int NS = 1;
-  static constexpr uint32_t kStreamLds = kResidency8<T, S>;
+  static constexpr uint32_t kStreamLds = residency_lds<T, S>(16);
   struct Rep {
     AdagradF32Hyper h;
   };
@@ -349,14 +364,14 @@ __device__ __forceinline__ typename P::S* state_row(const Operands<typename P::T
 // Drivers
 // ---------------------------------------------------------------------------
 template <typename P>
-__global__ __launch_bounds__(kThreads) void stream_kernel(KArgs<P> a) {
+__global__ __launch_bounds__(kStreamThreads) void stream_kernel(KArgs<P> a) {
   using T = typename P::T;
   using S = typename P::S;
   constexpr int NS = P::NS;
   constexpr int SS = state_slots<P>();
   uint32_t r;
   int64_t t0;
-  tile_of_block(a.g, r, t0);
+  tile_of_block<kStreamTile>(a.g, r, t0);
   if (!a.vec.mask[r]) {
     return;
   }
@@ -387,7 +402,7 @@ __global__ __launch_bounds__(kThreads) void stream_kernel(KArgs<P> a) {
   Pack<S> vs[SS][kUnroll];
 #pragma unroll
   for (int u = 0; u < kUnroll; ++u) {
-    const int64_t i = int64_t(u) * kThreads + threadIdx.x;
+    const int64_t i = int64_t(u) * kStreamThreads + threadIdx.x;
     if (i < packs_left) {
       vp[u] = load_stream(prow + i);
       vg[u] = load_stream(grow + i);
@@ -401,7 +416,7 @@ __global__ __launch_bounds__(kThreads) void stream_kernel(KArgs<P> a) {
   }
 #pragma unroll
   for (int u = 0; u < kUnroll; ++u) {
-    const int64_t i = int64_t(u) * kThreads + threadIdx.x;
+    const int64_t i = int64_t(u) * kStreamThreads + threadIdx.x;
     if (i < packs_left) {
 #pragma unroll
       for (int k = 0; k < kPack; ++k) {
@@ -435,10 +450,10 @@ __global__ __launch_bounds__(kThreads) void stream_kernel(KArgs<P> a) {
     for (int b = 0; b < NS; ++b) sbase[b][j] = st[b];
   };
   if (t0 == 0) {
-    for (int64_t j = threadIdx.x; j < head; j += kThreads) one(j);
+    for (int64_t j = threadIdx.x; j < head; j += kStreamThreads) one(j);
   }
-  if (t0 + kTile >= width) {
-    for (int64_t j = head + packs_row * kPack + threadIdx.x; j < width; j += kThreads) one(j);
+  if (t0 + kStreamTile >= width) {
+    for (int64_t j = head + packs_row * kPack + threadIdx.x; j < width; j += kStreamThreads) one(j);
   }
 }
 
@@ -450,7 +465,7 @@ __global__ __launch_bounds__(kThreads) void element_kernel(KArgs<P> a) {
   constexpr int SS = state_slots<P>();
   uint32_t r;
   int64_t t0;
-  tile_of_block(a.g, r, t0);
+  tile_of_block<kTile>(a.g, r, t0);
   if (!a.vec.mask[r]) {
     return;
   }
@@ -963,8 +978,8 @@ bool make_col_grid(int64_t R, int64_t T, ColGrid& g, uint32_t& blocks) {
   return true;
 }
 
-bool make_grid(int64_t R, int64_t T, Grid& g, uint32_t& blocks) {
-  const int64_t tiles = (T + kTile - 1) / kTile;
+bool make_grid(int64_t R, int64_t T, int64_t tile, Grid& g, uint32_t& blocks) {
+  const int64_t tiles = (T + tile - 1) / tile;
   if (R <= 0 || T <= 0 || tiles > INT32_MAX || R > INT32_MAX / tiles) {
     return false;
   }
@@ -1144,16 +1159,23 @@ int launch_dense(const Call& c, int nbufs) {
   using T = typename P::T;
   KArgs<P> a;
   uint32_t blocks = 0;
+  bool streamable = false;
   const auto prepare = [&] {
-    return fill_kargs<P>(c, nbufs, a, false) && make_grid(c.R, c.T, a.g, blocks);
+    if (!fill_kargs<P>(c, nbufs, a, false)) return false;
+    uint32_t res0 = 0, rmod = 0;
+    streamable = rows_streamable<P>(a.x, nbufs, res0, rmod);
+    if (!make_grid(c.R, c.T, streamable ? kStreamTile : kTile, a.g, blocks)) return false;
+    a.g.res0 = res0;
+    a.g.rmod = rmod;
+    return true;
   };
   return run_step<T>(c, prepare, [&]() -> int {
     const dim3 grid(blocks), block(kThreads);
     ColArgs<P> ca;
     uint32_t col_blocks = 0;
-    if (rows_streamable<P>(a.x, nbufs, a.g.res0, a.g.rmod)) {
+    if (streamable) {
       const uint32_t lds = blocks >= kCapMinBlocks ? P::kStreamLds : 0u;
-      hipLaunchKernelGGL(stream_kernel<P>, grid, block, lds, c.stream, a);
+      hipLaunchKernelGGL(stream_kernel<P>, grid, dim3(kStreamThreads), lds, c.stream, a);
     } else if (replica_minor(a.x, nbufs) && make_col_grid(c.R, c.T, ca.g, col_blocks)) {
       ca.x = a.x;
       ca.vec = a.vec;
