@@ -10,10 +10,11 @@
 //
 //   stream_kernel   unit inner stride (the consolidated layout `State`
 //                   produces, and ragged or misaligned rows): one wavefront
-//                   per 512-element tile, non-temporal 16-byte loads and
-//                   stores from each row's first 256-byte boundary (tiles never
-//                   share a cache line), the few head and tail elements of a
-//                   row one at a time; large launches cap residency per CU.
+//                   per tile (1-8 packs per thread by operand types),
+//                   non-temporal 16-byte loads and stores from each row's
+//                   first 256-byte boundary (tiles never share a cache line),
+//                   the few head and tail elements of a row one at a time;
+//                   large launches cap residency per CU.
 //   column_kernel   unit replica stride on every operand (transposed views,
 //                   as an outer vmap over a non-leading dimension gives): each
 //                   thread keeps one replica and walks columns, so the threads
@@ -79,7 +80,6 @@ constexpr int kUnroll = 2;
 constexpr int kPer = kPack * kUnroll;  // elements per thread per tile
 constexpr int64_t kTile = int64_t(kThreads) * kPer;
 constexpr int kStreamThreads = 64;
-constexpr int64_t kStreamTile = int64_t(kStreamThreads) * kPer;
 
 // Tile boundaries sit on 256-byte boundaries of the (R, T) rows. Consecutive
 // tiles run on different XCDs (each with its own L2); a 128-byte line split
@@ -194,6 +194,20 @@ constexpr uint32_t residency_lds(uint32_t n) {
 }
 constexpr uint32_t kCapMinBlocks = 8192;
 
+// Packs per thread of the streaming driver, by operand types: float32
+// throughout, float32 params with bfloat16 state, 16-bit params, float64.
+// Measured per policy on config-5-sized state (1/2/4/8 packs, one process per
+// sweep, two sweeps): float32 keeps 2 (under its residency cap); bfloat16
+// state wants 4 for Adam (+13%) but 1 for SGD and Adagrad (+8-15%); 16-bit
+// params 4-8 (+12-22%); float64 is flat.
+template <typename T, typename S>
+constexpr int stream_unroll(int fp32, int bf16_state, int narrow, int wide) {
+  return std::is_same<T, double>::value ? wide
+         : sizeof(T) == 2              ? narrow
+         : !std::is_same<S, T>::value  ? bf16_state
+                                       : fp32;
+}
+
 // Every policy has a parameter/gradient type T and an optimizer-state type S:
 // S == T is the reference's contract; S = bf16_t with T = float keeps the
 // moments (momentum buffers, sums) in bfloat16 while the element math and the
@@ -208,6 +222,7 @@ struct AdamPolicy {
   using M = op_t<T>;
   static constexpr int NS = AMSGRAD ? 3 : 2;
   static constexpr uint32_t kStreamLds = residency_lds<T, S>(AMSGRAD ? 12 : 14);
+  static constexpr int kStreamUnroll = stream_unroll<T, S>(2, 4, 4, 2);
   struct Rep {
     AdamHyper h;
     M bc1, bc2s;
@@ -242,6 +257,7 @@ struct SgdPolicy {
   using M = op_t<T>;
   static constexpr int NS = HAS_BUF ? 1 : 0;
   static constexpr uint32_t kStreamLds = HAS_BUF ? residency_lds<T, S>(14) : 0u;
+  static constexpr int kStreamUnroll = stream_unroll<T, S>(2, 1, 8, 2);
   struct Rep {
     SgdHyper<double> h;
     bool first;
@@ -272,6 +288,7 @@ struct AdagradPolicy {
   using M = op_t<T>;
   static constexpr int NS = 1;
   static constexpr uint32_t kStreamLds = residency_lds<T, S>(16);
+  static constexpr int kStreamUnroll = stream_unroll<T, S>(2, 1, 4, 2);
   struct Rep {
     AdagradHyper h;
   };
@@ -297,6 +314,7 @@ struct AdagradF32Policy {
   using M = float;
   static constexpr int NS = 1;
   static constexpr uint32_t kStreamLds = residency_lds<T, S>(16);
+  static constexpr int kStreamUnroll = stream_unroll<T, S>(2, 1, 4, 2);
   struct Rep {
     AdagradF32Hyper h;
   };
@@ -317,6 +335,12 @@ struct AdagradF32Policy {
 template <typename P>
 constexpr int state_slots() {
   return P::NS > 0 ? P::NS : 1;
+}
+
+// Elements per streaming tile: one wavefront x the policy's packs per thread.
+template <typename P>
+constexpr int64_t stream_tile() {
+  return int64_t(kStreamThreads) * kPack * P::kStreamUnroll;
 }
 
 template <typename P>
@@ -370,6 +394,8 @@ __global__ __launch_bounds__(kStreamThreads) void stream_kernel(KArgs<P> a) {
   using S = typename P::S;
   constexpr int NS = P::NS;
   constexpr int SS = state_slots<P>();
+  constexpr int U = P::kStreamUnroll;
+  constexpr int64_t kStreamTile = stream_tile<P>();
   uint32_t r;
   int64_t t0;
   tile_of_block<kStreamTile>(a.g, r, t0);
@@ -399,10 +425,10 @@ __global__ __launch_bounds__(kStreamThreads) void stream_kernel(KArgs<P> a) {
   }
   const int64_t packs_left = packs_row - t0 / kPack;
 
-  Pack<T> vp[kUnroll], vg[kUnroll];
-  Pack<S> vs[SS][kUnroll];
+  Pack<T> vp[U], vg[U];
+  Pack<S> vs[SS][U];
 #pragma unroll
-  for (int u = 0; u < kUnroll; ++u) {
+  for (int u = 0; u < U; ++u) {
     const int64_t i = int64_t(u) * kStreamThreads + threadIdx.x;
     if (i < packs_left) {
       vp[u] = load_stream(prow + i);
@@ -416,7 +442,7 @@ __global__ __launch_bounds__(kStreamThreads) void stream_kernel(KArgs<P> a) {
     }
   }
 #pragma unroll
-  for (int u = 0; u < kUnroll; ++u) {
+  for (int u = 0; u < U; ++u) {
     const int64_t i = int64_t(u) * kStreamThreads + threadIdx.x;
     if (i < packs_left) {
 #pragma unroll
@@ -1165,7 +1191,7 @@ int launch_dense(const Call& c, int nbufs) {
     if (!fill_kargs<P>(c, nbufs, a, false)) return false;
     uint32_t res0 = 0, rmod = 0;
     streamable = rows_streamable<P>(a.x, nbufs, res0, rmod);
-    if (!make_grid(c.R, c.T, streamable ? kStreamTile : kTile, a.g, blocks)) return false;
+    if (!make_grid(c.R, c.T, streamable ? stream_tile<P>() : kTile, a.g, blocks)) return false;
     a.g.res0 = res0;
     a.g.rmod = rmod;
     return true;
