@@ -543,18 +543,27 @@ def main():
         fn(*op_args, **kw)
     torch.cuda.synchronize()
 
-    # K steps bracketed by events on the launch stream, plus one event between
-    # consecutive steps for the per-step median.
+    # K steps bracketed by two events on the launch stream (nothing else is
+    # enqueued between the steps, as in a training loop).
     stream = torch.cuda.current_stream()
-    ev = [torch.cuda.Event(enable_timing=True) for _ in range(args.steps + 1)]
+    start, end = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
     t0 = time.perf_counter()
+    start.record(stream)
+    for _ in range(args.steps):
+        fn(*op_args, **kw)
+    end.record(stream)
+    torch.cuda.synchronize()
+    wall_ms = (time.perf_counter() - t0) * 1e3 / args.steps
+    step_ms = start.elapsed_time(end) / args.steps
+    # Then K more steps with an event between consecutive steps, for the
+    # per-step median (recording an event per step costs host time, which
+    # shows on microsecond steps, so it stays out of the timed K).
+    ev = [torch.cuda.Event(enable_timing=True) for _ in range(args.steps + 1)]
     ev[0].record(stream)
     for i in range(args.steps):
         fn(*op_args, **kw)
         ev[i + 1].record(stream)
     torch.cuda.synchronize()
-    wall_ms = (time.perf_counter() - t0) * 1e3 / args.steps
-    step_ms = ev[0].elapsed_time(ev[-1]) / args.steps
     per_step = sorted(ev[i].elapsed_time(ev[i + 1]) for i in range(args.steps))
     median_ms = per_step[len(per_step) // 2]
 
