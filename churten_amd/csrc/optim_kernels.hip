@@ -223,6 +223,7 @@ struct AdamPolicy {
   static constexpr int NS = AMSGRAD ? 3 : 2;
   static constexpr uint32_t kStreamLds = residency_lds<T, S>(AMSGRAD ? 12 : 14);
   static constexpr int kStreamUnroll = stream_unroll<T, S>(2, 4, 4, 2);
+  static constexpr int kSegmentUnroll = stream_unroll<T, S>(2, 4, 4, 2);
   struct Rep {
     AdamHyper h;
     M bc1, bc2s;
@@ -258,6 +259,7 @@ struct SgdPolicy {
   static constexpr int NS = HAS_BUF ? 1 : 0;
   static constexpr uint32_t kStreamLds = HAS_BUF ? residency_lds<T, S>(14) : 0u;
   static constexpr int kStreamUnroll = stream_unroll<T, S>(2, 1, 8, 2);
+  static constexpr int kSegmentUnroll = 2;
   struct Rep {
     SgdHyper<double> h;
     bool first;
@@ -289,6 +291,7 @@ struct AdagradPolicy {
   static constexpr int NS = 1;
   static constexpr uint32_t kStreamLds = residency_lds<T, S>(16);
   static constexpr int kStreamUnroll = stream_unroll<T, S>(2, 1, 4, 2);
+  static constexpr int kSegmentUnroll = 2;
   struct Rep {
     AdagradHyper h;
   };
@@ -315,6 +318,7 @@ struct AdagradF32Policy {
   static constexpr int NS = 1;
   static constexpr uint32_t kStreamLds = residency_lds<T, S>(16);
   static constexpr int kStreamUnroll = stream_unroll<T, S>(2, 1, 4, 2);
+  static constexpr int kSegmentUnroll = 2;
   struct Rep {
     AdagradF32Hyper h;
   };
@@ -341,6 +345,15 @@ constexpr int state_slots() {
 template <typename P>
 constexpr int64_t stream_tile() {
   return int64_t(kStreamThreads) * kPack * P::kStreamUnroll;
+}
+
+// Elements per segmented-driver tile (128 threads). Measured per policy at the
+// config-5 layout with per-parameter gradients (1/2/4 packs): Adam with
+// bfloat16 moments or 16-bit params wants 4 (+8-17%); SGD and Adagrad were
+// within noise of 2 for every operand type, and float32/float64 Adam too.
+template <typename P>
+constexpr int64_t segment_tile() {
+  return int64_t(kThreads) * kPack * P::kSegmentUnroll;
 }
 
 template <typename P>
@@ -665,7 +678,7 @@ __device__ __forceinline__ int segment_of_tile(const uint32_t* tile0, int n, uin
 // A segment's tile on the vector walk. The walk follows the (R, T) layout: in
 // row r the segment's first 256-byte boundary lies `head` elements in (head <
 // A, as for the streaming driver); packs of 4 elements stream from there, tile
-// k taking packs [k * kTile / 4, (k + 1) * kTile / 4). Tile 0 also takes the
+// k taking packs [k * TILE / 4, (k + 1) * TILE / 4). Tile 0 also takes the
 // head elements and the segment's last tile the at most three tail elements,
 // one element per access. The per-parameter gradient's rows keep their own
 // alignment: they are read with element-aligned pack loads.
@@ -677,7 +690,7 @@ struct SegTile {
   bool has_head, has_tail;
 };
 
-template <typename T>
+template <typename T, int64_t TILE>
 __device__ __forceinline__ SegTile seg_tile(uint32_t res0, uint32_t rmod, uint32_t r,
                                             int64_t col, int64_t numel, int64_t j0) {
   constexpr uint32_t A = align_elems<T>();
@@ -689,7 +702,7 @@ __device__ __forceinline__ SegTile seg_tile(uint32_t res0, uint32_t rmod, uint32
   t.packs = packs_seg - j0 / kPack;
   t.tail = t.head + packs_seg * kPack;
   t.has_head = j0 == 0;
-  t.has_tail = j0 + kTile >= numel;
+  t.has_tail = j0 + TILE >= numel;
   return t;
 }
 
@@ -724,6 +737,8 @@ __global__ __launch_bounds__(kThreads) void segment_kernel(SegArgs<P> a) {
   using S = typename P::S;
   constexpr int NS = P::NS;
   constexpr int SS = state_slots<P>();
+  constexpr int U = P::kSegmentUnroll;
+  constexpr int64_t kSegTile = segment_tile<P>();
   const uint32_t tiles_per_row = a.seg.tile0[a.seg.n];
   const uint32_t r = blockIdx.x / tiles_per_row;
   const uint32_t local = blockIdx.x - r * tiles_per_row;
@@ -738,7 +753,7 @@ __global__ __launch_bounds__(kThreads) void segment_kernel(SegArgs<P> a) {
   }
   const int64_t numel = a.seg.numel[s];
   const int64_t col = a.seg.col[s];
-  const int64_t j0 = int64_t(local - a.seg.tile0[s]) * kTile;
+  const int64_t j0 = int64_t(local - a.seg.tile0[s]) * kSegTile;
   const bool vec = (a.seg.vec_ok >> s) & 1u;
   // Row r of the segment's columns in the (R, T) operands, and of its gradient
   // source: the segment's row, or for a gap the consolidated buffer (null:
@@ -757,9 +772,9 @@ __global__ __launch_bounds__(kThreads) void segment_kernel(SegArgs<P> a) {
     // A frozen replica's optimizer state is not touched, but the consolidated
     // gradient is still filled, as the separate scatter would have filled it.
     if (vec) {
-      const SegTile t = seg_tile<T>(a.k.g.res0, a.k.g.rmod, r, col, numel, j0);
+      const SegTile t = seg_tile<T, kSegTile>(a.k.g.res0, a.k.g.rmod, r, col, numel, j0);
 #pragma unroll
-      for (int u = 0; u < kUnroll; ++u) {
+      for (int u = 0; u < U; ++u) {
         const int64_t i = int64_t(u) * kThreads + threadIdx.x;
         if (i < t.packs) {
           store_stream(reinterpret_cast<Pack<T>*>(g_dst + t.first) + i,
@@ -768,7 +783,7 @@ __global__ __launch_bounds__(kThreads) void segment_kernel(SegArgs<P> a) {
       }
       seg_singles(t, numel, [&](int64_t j) { g_dst[j] = g_src[j]; });
     } else {
-      const int64_t cnt = imin(kTile, numel - j0);
+      const int64_t cnt = imin(kSegTile, numel - j0);
       for (int64_t j = j0 + threadIdx.x; j < j0 + cnt; j += kThreads) {
         g_dst[j * a.k.x.stride_t[1]] = g_src[j];
       }
@@ -807,21 +822,21 @@ __global__ __launch_bounds__(kThreads) void segment_kernel(SegArgs<P> a) {
   };
 
   if (!vec) {
-    const int64_t cnt = imin(kTile, numel - j0);
+    const int64_t cnt = imin(kSegTile, numel - j0);
     for (int64_t j = j0 + threadIdx.x; j < j0 + cnt; j += kThreads) one(j);
     return;
   }
 
   // Vector walk (unit inner strides): the (R, T) operands' packs are aligned.
-  const SegTile t = seg_tile<T>(a.k.g.res0, a.k.g.rmod, r, col, numel, j0);
+  const SegTile t = seg_tile<T, kSegTile>(a.k.g.res0, a.k.g.rmod, r, col, numel, j0);
   Pack<T>* const pp = reinterpret_cast<Pack<T>*>(prow + t.first);
   Pack<S>* sp[SS];
 #pragma unroll
   for (int b = 0; b < NS; ++b) sp[b] = reinterpret_cast<Pack<S>*>(srow[b] + t.first);
-  Pack<T> vp[kUnroll], vg[kUnroll];
-  Pack<S> vs[SS][kUnroll];
+  Pack<T> vp[U], vg[U];
+  Pack<S> vs[SS][U];
 #pragma unroll
-  for (int u = 0; u < kUnroll; ++u) {
+  for (int u = 0; u < U; ++u) {
     const int64_t i = int64_t(u) * kThreads + threadIdx.x;
     if (i < t.packs) {
       vp[u] = load_stream(pp + i);
@@ -842,7 +857,7 @@ __global__ __launch_bounds__(kThreads) void segment_kernel(SegArgs<P> a) {
     }
   }
 #pragma unroll
-  for (int u = 0; u < kUnroll; ++u) {
+  for (int u = 0; u < U; ++u) {
     const int64_t i = int64_t(u) * kThreads + threadIdx.x;
     if (i < t.packs) {
       if (store_grad) {
@@ -888,7 +903,7 @@ __global__ __launch_bounds__(kThreads) void scatter_kernel(ScatterArgs<T> a) {
   const T* src = a.seg.data[s] + int64_t(r) * a.seg.stride_r[s];
   T* dst = a.dst + int64_t(r) * a.dst_stride_r + a.seg.col[s];
   if ((a.seg.vec_ok >> s) & 1u) {
-    const SegTile t = seg_tile<T>(a.res0, a.rmod, r, a.seg.col[s], numel, j0);
+    const SegTile t = seg_tile<T, kTile>(a.res0, a.rmod, r, a.seg.col[s], numel, j0);
     Pack<T> v[kUnroll];
 #pragma unroll
     for (int u = 0; u < kUnroll; ++u) {
@@ -1076,7 +1091,7 @@ struct SegmentWalk {
 // returns the grid size (0 when the walk is done, -1 when it exceeds the 1-D
 // grid). `vec_rows` says whether the (R, T) operands allow vector access.
 template <typename T>
-int64_t next_chunk(SegmentWalk& w, int64_t R, bool vec_rows, Segments<T>& out) {
+int64_t next_chunk(SegmentWalk& w, int64_t R, int64_t tile, bool vec_rows, Segments<T>& out) {
   out.n = 0;
   out.vec_ok = 0;
   uint64_t tiles = 0;
@@ -1088,7 +1103,7 @@ int64_t next_chunk(SegmentWalk& w, int64_t R, bool vec_rows, Segments<T>& out) {
     out.col[k] = s.col;
     out.numel[k] = s.numel;
     out.tile0[k] = static_cast<uint32_t>(tiles);
-    tiles += static_cast<uint64_t>((s.numel + kTile - 1) / kTile);
+    tiles += static_cast<uint64_t>((s.numel + tile - 1) / tile);
     if (tiles > UINT32_MAX) return -1;
     const bool ok = vec_rows && reinterpret_cast<uintptr_t>(s.data) % sizeof(T) == 0;
     out.vec_ok |= (ok ? uint64_t(1) : uint64_t(0)) << k;
@@ -1100,9 +1115,9 @@ int64_t next_chunk(SegmentWalk& w, int64_t R, bool vec_rows, Segments<T>& out) {
 
 // Checks that every launch of a walk fits the grid, without launching.
 template <typename T>
-bool walk_fits(SegmentWalk w, int64_t R, bool vec_rows, Segments<T>& scratch) {
+bool walk_fits(SegmentWalk w, int64_t R, int64_t tile, bool vec_rows, Segments<T>& scratch) {
   int64_t blocks;
-  while ((blocks = next_chunk<T>(w, R, vec_rows, scratch)) != 0 || scratch.n > 0) {
+  while ((blocks = next_chunk<T>(w, R, tile, vec_rows, scratch)) != 0 || scratch.n > 0) {
     if (blocks < 0) return false;
   }
   return true;
@@ -1110,10 +1125,10 @@ bool walk_fits(SegmentWalk w, int64_t R, bool vec_rows, Segments<T>& scratch) {
 
 // Launches `kernel` once per chunk of the walk.
 template <typename T, typename Args, typename Kernel>
-int launch_walk(SegmentWalk w, int64_t R, bool vec_rows, Args& a, Segments<T>& seg,
+int launch_walk(SegmentWalk w, int64_t R, int64_t tile, bool vec_rows, Args& a, Segments<T>& seg,
                 Kernel kernel, hipStream_t stream) {
   int64_t blocks;
-  while ((blocks = next_chunk<T>(w, R, vec_rows, seg)) != 0 || seg.n > 0) {
+  while ((blocks = next_chunk<T>(w, R, tile, vec_rows, seg)) != 0 || seg.n > 0) {
     if (blocks < 0) return kInvalid;
     if (blocks == 0) continue;
     hipLaunchKernelGGL(kernel, dim3(static_cast<uint32_t>(blocks)), dim3(kThreads), 0, stream,
@@ -1233,10 +1248,11 @@ int launch_segments(const Call& c, int nbufs, const ts_segment* segs, int n_segs
     }
     a.k.g = Grid{c.T, 0, 0, 0};
     vec_rows = rows_streamable<P>(a.k.x, nbufs, a.k.g.res0, a.k.g.rmod);
-    return walk_fits<T>(walk, c.R, vec_rows, a.seg);
+    return walk_fits<T>(walk, c.R, segment_tile<P>(), vec_rows, a.seg);
   };
   return run_step<T>(c, prepare, [&]() -> int {
-    return launch_walk<T>(walk, c.R, vec_rows, a, a.seg, segment_kernel<P>, c.stream);
+    return launch_walk<T>(walk, c.R, segment_tile<P>(), vec_rows, a, a.seg, segment_kernel<P>,
+                          c.stream);
   });
 }
 
@@ -1365,8 +1381,8 @@ struct ScatterBody {
     const bool any = std::any_of(segs, segs + n_segs, [](const ts_segment& s) {
       return s.numel > 0;
     });
-    if ((any && dst == nullptr) || !walk_fits<T>(walk, R, vec_rows, a.seg)) return kInvalid;
-    return launch_walk<T>(walk, R, vec_rows, a, a.seg, scatter_kernel<T>, stream);
+    if ((any && dst == nullptr) || !walk_fits<T>(walk, R, kTile, vec_rows, a.seg)) return kInvalid;
+    return launch_walk<T>(walk, R, kTile, vec_rows, a, a.seg, scatter_kernel<T>, stream);
   }
 };
 
