@@ -12,7 +12,8 @@ every output row. Rows the ATen call cannot express (a momentum-0 replica
 inside a call that carries momentum buffers) are not recorded. Frozen rows are
 recorded as their inputs.
 
-Run on a GPU box:  python tests/golden/make_device_golden.py --out gpurun_out/device_ref.json
+Run on an MI355X:  python tests/golden/make_device_golden.py --out <path>/device_ref.json
+(then copy the file to tests/golden/).
 """
 
 from __future__ import annotations
@@ -84,7 +85,7 @@ def run_rows(c, dev):
 
 def main():
     ap = argparse.ArgumentParser()
-    ap.add_argument("--out", default="gpurun_out/device_ref.json")
+    ap.add_argument("--out", default="device_ref.json")
     args = ap.parse_args()
     dev = torch.device("cuda")
     records = []
