@@ -51,7 +51,14 @@ __device__ __forceinline__ float widen(bf16_t x) {
 template <typename T> __device__ __forceinline__ T narrow(op_t<T> x);
 template <> __device__ __forceinline__ float narrow<float>(float x) { return x; }
 template <> __device__ __forceinline__ double narrow<double>(double x) { return x; }
+// The float value itself is rounded to half. torch narrows in two steps
+// (double expression -> float opmath value -> half on store); hipcc's default
+// -ffp-contract=fast lets the backend fold such a double -> float -> half chain
+// into one double -> half rounding, which differs whenever the float lands on
+// a half-way point between two halves. The empty asm makes the float opaque,
+// so both roundings happen.
 template <> __device__ __forceinline__ _Float16 narrow<_Float16>(float x) {
+  asm("" : "+v"(x));
   return static_cast<_Float16>(x);
 }
 template <> __device__ __forceinline__ bf16_t narrow<bf16_t>(float x) {

@@ -40,8 +40,11 @@ def _vecs(R, *rows, dtype=torch.float32):
 
 
 # float64 parameters: the products inside the update are inexact there, so these
-# cases also pin which multiply-adds torch's build fuses.
-DTYPES = [torch.float32, torch.float64]
+# cases also pin which multiply-adds torch's build fuses. 16-bit parameters: the
+# update narrows a double expression to the float math value and that to the
+# storage type, two roundings that must not be folded into one (70001-element
+# rows hit the half-way cases).
+DTYPES = [torch.float32, torch.float64, torch.float16, torch.bfloat16]
 
 
 @pytest.mark.parametrize("dtype", DTYPES, ids=str)
