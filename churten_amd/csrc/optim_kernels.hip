@@ -69,11 +69,11 @@ namespace {
 // packs of 4 elements per thread with non-temporal vector loads and stores
 // (non-temporal hints on both loads and stores were worth ~10% over plain
 // accesses, either alone nothing). The streaming driver runs one wavefront per
-// workgroup (512-element tiles) under a residency cap (below): of 64/128/256
-// threads x 1/2/4 packs x 8-24 resident waves per CU, that was fastest,
-// ahead of 128 x 2 with its best cap by 2-6% and uncapped 128 x 2 by 6-10%.
-// The other drivers keep 128 threads (1024-element tiles), where their own
-// sweeps put them.
+// workgroup under a residency cap (below; 512-element tiles for float32): of
+// 64/128/256 threads x 1/2/4 packs x 8-24 resident waves per CU, that was
+// fastest, ahead of 128 x 2 with its best cap by 2-6% and uncapped 128 x 2 by
+// 6-10%. The other drivers keep 128 threads (1024-element tiles for float32),
+// where their own sweeps put them; packs per thread follow the policy.
 constexpr int kThreads = 128;
 constexpr int kPack = 4;
 constexpr int kUnroll = 2;
@@ -134,7 +134,7 @@ struct Vectors {
   const uint8_t* mask;
 };
 
-// Tiles of kTile elements per row. For the streaming driver, row r's first
+// Tiles of a driver's tile size per row. For the streaming driver, row r's first
 // 256-byte boundary lies head(r) = (A - (res0 + r * rmod) % A) % A elements in
 // (A: 256 bytes in elements of the parameter type; res0: the parameter base's
 // element offset modulo A, rmod: its row stride modulo A); packs stream from
