@@ -136,3 +136,40 @@ def test_config5_bf16_state_windows():
         for name, t, want in (("p", p, pw), ("m", mb, mw), ("v", vb, vw)):
             got = _np(t[r:r + 1, t0:t0 + 4096].float())
             assert np.array_equal(got.view(np.uint32), want.view(np.uint32)), (r, t0, name)
+
+
+def test_single_row_past_2_31_elements():
+    """One replica row of 2^31 + 4099 elements (34 GB of Adam state): element
+    indices inside a row pass 2^31 and the row is ragged. Windows at the
+    start, across 2^31 and at the very end equal the oracle; the same step with
+    the gradient as one per-parameter segment equals the dense step, bit for
+    bit, over the whole row."""
+    T = 2**31 + 4099
+    g = torch.Generator(device="cuda").manual_seed(31)
+    p = torch.randn(1, T, device="cuda", generator=g).mul_(0.02)
+    gr = torch.randn(1, T, device="cuda", generator=g).mul_(1e-3)
+    m = torch.randn(1, T, device="cuda", generator=g).mul_(1e-3)
+    v = torch.rand(1, T, device="cuda", generator=g).mul_(1e-4)
+    steps = torch.full((1,), 7.0, device="cuda")
+    hyp = [torch.full((1,), x, device="cuda") for x in (1e-3, 0.9, 0.999, 1e-8, 1e-2)]
+    mask = torch.ones(1, dtype=torch.bool, device="cuda")
+    kw = dict(amsgrad=False, maximize=False, decoupled_weight_decay=True)
+    windows = [0, 2**31 - 2048, T - 4096]
+    before = [[_np(t[:, t0:t0 + 4096]) for t in (p, gr, m, v)] for t0 in windows]
+    twin = [t.clone() for t in (p, m, v)]
+    steps2 = steps.clone()
+    torch.ops.torchstrap.adam_step_(p, gr, m, v, None, steps, *hyp, mask, **kw)
+    torch.ops.churten.adam_step_segments_(twin[0], [gr], [0], None, twin[1], twin[2], None,
+                                          steps2, *hyp, mask, **kw)
+    torch.cuda.synchronize()
+    for name, a, b in (("params", p, twin[0]), ("exp_avgs", m, twin[1]),
+                       ("exp_avg_sqs", v, twin[2])):
+        assert torch.equal(a.view(torch.int32), b.view(torch.int32)), name
+    del twin
+    hw = [_np(h) for h in hyp]
+    for t0, (pw, gw, mw, vw) in zip(windows, before):
+        O.adam_step(O.DEVICE, pw, gw, mw, vw, None, np.full(1, 7.0, np.float32), *hw,
+                    np.ones(1, bool), **kw)
+        for name, t, want in (("p", p, pw), ("m", m, mw), ("v", v, vw)):
+            got = _np(t[:, t0:t0 + 4096])
+            assert np.array_equal(got.view(np.uint32), want.view(np.uint32)), f"{name} @ {t0}"
