@@ -103,7 +103,10 @@ def run_case(c):
         def step(b, s):
             f(b[0], b[1], b[2], s, *hyp, mask, maximize=bool(c["seed"] & 1))
     kinds = c["kinds"]
-    view = [placed(t, kinds[i % len(kinds)], c["off"] + i, c["pad"]) for i, t in enumerate(bufs)]
+    # operands differ in offset (rows: other 16-byte phases) and padding (cols:
+    # other column strides)
+    view = [placed(t, kinds[i % len(kinds)], c["off"] + i, c["pad"] + 3 * i)
+            for i, t in enumerate(bufs)]
     dense = [t.clone() for t in bufs]
     s_view, s_dense = steps.clone(), steps.clone()
     for _ in range(2):
