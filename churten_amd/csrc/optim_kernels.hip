@@ -20,8 +20,7 @@
 //                   thread keeps one replica and walks columns, so the threads
 //                   of a workgroup read consecutive replicas -- contiguous
 //                   memory.
-//   element_kernel  any other strides: one element per access, same tile
-//                   geometry as stream_kernel.
+//   element_kernel  any other inner strides: one element per access.
 //   segment_kernel  the gradient arrives as one tensor per parameter (a segment
 //                   table) instead of the consolidated (R, T) gradient buffer:
 //                   the gradient scatter of the training step is fused into the
@@ -115,6 +114,52 @@ __device__ __forceinline__ void store_stream(Pack<T>* p, const Pack<T>& v) {
   __builtin_nontemporal_store(__builtin_bit_cast(PackBits<T>, v),
                               reinterpret_cast<PackBits<T>*>(p));
 }
+
+// Packs at addresses that are only element-aligned: operands whose 16-byte
+// boundaries do not line up with the parameters' (a column view at another
+// offset, a per-parameter gradient's rows). gfx950 code runs in unaligned
+// access mode, and hipcc emits the same single global_load/store_dwordx4
+// (dwordx2 for 16-bit types) for these types as for an aligned pack; on an
+// aligned address the access is the aligned one.
+template <typename T>
+using PackBitsU = uint32_t
+    __attribute__((ext_vector_type(sizeof(T) * kPack / 4), aligned(sizeof(T))));
+
+template <typename T>
+__device__ __forceinline__ Pack<T> load_stream_any(const T* p) {
+  return __builtin_bit_cast(
+      Pack<T>, __builtin_nontemporal_load(reinterpret_cast<const PackBitsU<T>*>(p)));
+}
+
+template <typename T>
+__device__ __forceinline__ void store_stream_any(T* p, const Pack<T>& v) {
+  __builtin_nontemporal_store(__builtin_bit_cast(PackBitsU<T>, v),
+                              reinterpret_cast<PackBitsU<T>*>(p));
+}
+
+// The packs of an operand from a given element on: 16-byte aligned wherever
+// the parameters' packs are (ANY = false, the usual case: the compiler knows
+// the alignment) or only element-aligned (ANY = true). Indexed by pack.
+template <bool ANY, typename T>
+struct Packs;
+
+template <typename T>
+struct Packs<false, T> {
+  Pack<T>* p = nullptr;
+  Packs() = default;
+  __device__ explicit Packs(T* e) : p(reinterpret_cast<Pack<T>*>(e)) {}
+  __device__ Pack<T> load(int64_t i) const { return load_stream(p + i); }
+  __device__ void store(int64_t i, const Pack<T>& v) const { store_stream(p + i, v); }
+};
+
+template <typename T>
+struct Packs<true, T> {
+  T* p = nullptr;
+  Packs() = default;
+  __device__ explicit Packs(T* e) : p(e) {}
+  __device__ Pack<T> load(int64_t i) const { return load_stream_any(p + i * kPack); }
+  __device__ void store(int64_t i, const Pack<T>& v) const { store_stream_any(p + i * kPack, v); }
+};
 
 constexpr int kMaxOperands = 5;
 
@@ -401,7 +446,7 @@ __device__ __forceinline__ typename P::S* state_row(const Operands<typename P::T
 // ---------------------------------------------------------------------------
 // Drivers
 // ---------------------------------------------------------------------------
-template <typename P>
+template <typename P, bool ANY>
 __global__ __launch_bounds__(kStreamThreads) void stream_kernel(KArgs<P> a) {
   using T = typename P::T;
   using S = typename P::S;
@@ -429,13 +474,13 @@ __global__ __launch_bounds__(kStreamThreads) void stream_kernel(KArgs<P> a) {
 #pragma unroll
   for (int b = 0; b < NS; ++b) sbase[b] = state_row<P>(a.x, 2 + b, r);
 
+  // The parameters' packs are 16-byte aligned by construction; with ANY the
+  // other operands sit at another 16-byte phase and use element-aligned packs.
   Pack<T>* prow = reinterpret_cast<Pack<T>*>(pbase + head) + t0 / kPack;
-  const Pack<T>* grow = reinterpret_cast<const Pack<T>*>(gbase + head) + t0 / kPack;
-  Pack<S>* srow[SS];
+  const Packs<ANY, T> grow(const_cast<T*>(gbase) + head + t0);
+  Packs<ANY, S> srow[SS];
 #pragma unroll
-  for (int b = 0; b < NS; ++b) {
-    srow[b] = reinterpret_cast<Pack<S>*>(sbase[b] + head) + t0 / kPack;
-  }
+  for (int b = 0; b < NS; ++b) srow[b] = Packs<ANY, S>(sbase[b] + head + t0);
   const int64_t packs_left = packs_row - t0 / kPack;
 
   Pack<T> vp[U], vg[U];
@@ -445,11 +490,11 @@ __global__ __launch_bounds__(kStreamThreads) void stream_kernel(KArgs<P> a) {
     const int64_t i = int64_t(u) * kStreamThreads + threadIdx.x;
     if (i < packs_left) {
       vp[u] = load_stream(prow + i);
-      vg[u] = load_stream(grow + i);
+      vg[u] = grow.load(i);
       if (load_state) {
 #pragma unroll
         for (int b = 0; b < NS; ++b) {
-          vs[b][u] = load_stream(srow[b] + i);
+          vs[b][u] = srow[b].load(i);
         }
       }
     }
@@ -470,7 +515,7 @@ __global__ __launch_bounds__(kStreamThreads) void stream_kernel(KArgs<P> a) {
       store_stream(prow + i, vp[u]);
 #pragma unroll
       for (int b = 0; b < NS; ++b) {
-        store_stream(srow[b] + i, vs[b][u]);
+        srow[b].store(i, vs[b][u]);
       }
     }
   }
@@ -722,21 +767,7 @@ __device__ __forceinline__ void seg_singles(const SegTile& t, int64_t numel, Fn&
   }
 }
 
-// Packs from element-aligned addresses (a per-parameter gradient's row need
-// not share the (R, T) layout's 16-byte boundaries). gfx950 code runs in
-// unaligned access mode, and hipcc emits the same single global_load_dwordx4
-// (dwordx2 for 16-bit types) for this type as for an aligned pack.
-template <typename T>
-using PackBitsU = uint32_t
-    __attribute__((ext_vector_type(sizeof(T) * kPack / 4), aligned(sizeof(T))));
-
-template <typename T>
-__device__ __forceinline__ Pack<T> load_stream_any(const T* p) {
-  return __builtin_bit_cast(
-      Pack<T>, __builtin_nontemporal_load(reinterpret_cast<const PackBitsU<T>*>(p)));
-}
-
-template <typename P>
+template <typename P, bool ANY>
 __global__ __launch_bounds__(kThreads) void segment_kernel(SegArgs<P> a) {
   using T = typename P::T;
   using S = typename P::S;
@@ -782,8 +813,7 @@ __global__ __launch_bounds__(kThreads) void segment_kernel(SegArgs<P> a) {
       for (int u = 0; u < U; ++u) {
         const int64_t i = int64_t(u) * kThreads + threadIdx.x;
         if (i < t.packs) {
-          store_stream(reinterpret_cast<Pack<T>*>(g_dst + t.first) + i,
-                       load_stream_any(g_src + t.first + i * kPack));
+          Packs<ANY, T>(g_dst + t.first).store(i, load_stream_any(g_src + t.first + i * kPack));
         }
       }
       seg_singles(t, numel, [&](int64_t j) { g_dst[j] = g_src[j]; });
@@ -832,12 +862,14 @@ __global__ __launch_bounds__(kThreads) void segment_kernel(SegArgs<P> a) {
     return;
   }
 
-  // Vector walk (unit inner strides): the (R, T) operands' packs are aligned.
+  // Vector walk (unit inner strides): the parameters' packs are aligned; with
+  // ANY the other operands sit at another 16-byte phase (element-aligned packs).
   const SegTile t = seg_tile<T, kSegTile>(a.k.g.res0, a.k.g.rmod, r, col, numel, j0);
   Pack<T>* const pp = reinterpret_cast<Pack<T>*>(prow + t.first);
-  Pack<S>* sp[SS];
+  Packs<ANY, S> sp[SS];
 #pragma unroll
-  for (int b = 0; b < NS; ++b) sp[b] = reinterpret_cast<Pack<S>*>(srow[b] + t.first);
+  for (int b = 0; b < NS; ++b) sp[b] = Packs<ANY, S>(srow[b] + t.first);
+  const Packs<ANY, T> gout(g_dst != nullptr ? g_dst + t.first : nullptr);
   Pack<T> vp[U], vg[U];
   Pack<S> vs[SS][U];
 #pragma unroll
@@ -847,7 +879,7 @@ __global__ __launch_bounds__(kThreads) void segment_kernel(SegArgs<P> a) {
       vp[u] = load_stream(pp + i);
       if (gap) {
         if (g_src != nullptr) {
-          vg[u] = load_stream(reinterpret_cast<const Pack<T>*>(g_src + t.first) + i);
+          vg[u] = gout.load(i);  // a gap reads the consolidated gradient
         } else {
 #pragma unroll
           for (int k = 0; k < kPack; ++k) vg[u].v[k] = zero;
@@ -857,7 +889,7 @@ __global__ __launch_bounds__(kThreads) void segment_kernel(SegArgs<P> a) {
       }
       if (load_state) {
 #pragma unroll
-        for (int b = 0; b < NS; ++b) vs[b][u] = load_stream(sp[b] + i);
+        for (int b = 0; b < NS; ++b) vs[b][u] = sp[b].load(i);
       }
     }
   }
@@ -866,7 +898,7 @@ __global__ __launch_bounds__(kThreads) void segment_kernel(SegArgs<P> a) {
     const int64_t i = int64_t(u) * kThreads + threadIdx.x;
     if (i < t.packs) {
       if (store_grad) {
-        store_stream(reinterpret_cast<Pack<T>*>(g_dst + t.first) + i, vg[u]);
+        gout.store(i, vg[u]);
       }
 #pragma unroll
       for (int k = 0; k < kPack; ++k) {
@@ -879,7 +911,7 @@ __global__ __launch_bounds__(kThreads) void segment_kernel(SegArgs<P> a) {
       }
       store_stream(pp + i, vp[u]);
 #pragma unroll
-      for (int b = 0; b < NS; ++b) store_stream(sp[b] + i, vs[b][u]);
+      for (int b = 0; b < NS; ++b) sp[b].store(i, vs[b][u]);
     }
   }
   seg_singles(t, numel, one);
@@ -970,32 +1002,41 @@ bool fill_operands(const ts_rt_buf* bufs, int n, Operands<T>& x, bool grad_optio
   return true;
 }
 
-// The streaming driver takes any unit-inner-stride operands whose 16-byte
-// boundaries fall on the same element index in every row of every operand:
-// element-aligned bases with one common base residue (element offset modulo 4)
-// and row strides congruent modulo 4. Sets res0 / rmod (the parameter's phase
-// modulo 256 bytes) for the grid.
+// The streaming drivers take any operands with unit inner stride and
+// element-aligned bases. The walk follows the parameters' 256-byte boundaries
+// (res0 / rmod: their phase modulo 256 bytes, for the grid); operands at
+// another phase use element-aligned packs.
 template <typename P>
 bool rows_streamable(const Operands<typename P::T>& x, int n, uint32_t& res0, uint32_t& rmod) {
   constexpr uint32_t A = align_elems<typename P::T>();
-  bool first = true;
-  uint32_t res4 = 0, mod4 = 0;
   for (int b = 0; b < n; ++b) {
     if (x.data[b] == nullptr) continue;
     const size_t elem = b < 2 ? sizeof(typename P::T) : sizeof(typename P::S);
     const uintptr_t addr = reinterpret_cast<uintptr_t>(x.data[b]);
     if (x.stride_t[b] != 1 || addr % elem != 0) return false;
-    const uint32_t res = static_cast<uint32_t>((addr / elem) % kPack);
-    const uint32_t mod = static_cast<uint32_t>(((x.stride_r[b] % kPack) + kPack) % kPack);
-    if (first) {
-      res4 = res;
-      mod4 = mod;
-      res0 = static_cast<uint32_t>((addr / elem) % A);
-      rmod = static_cast<uint32_t>(((x.stride_r[b] % A) + A) % A);
-      first = false;
-    } else if (res != res4 || mod != mod4) {
-      return false;
-    }
+  }
+  const uintptr_t p0 = reinterpret_cast<uintptr_t>(x.data[0]);
+  res0 = static_cast<uint32_t>((p0 / sizeof(typename P::T)) % A);
+  rmod = static_cast<uint32_t>(((x.stride_r[0] % A) + A) % A);
+  return true;
+}
+
+// Whether every present operand's 16-byte boundaries fall on the same element
+// index as the parameters' in every row (common base residue and row stride
+// modulo 4): then all packs are aligned and the drivers' ANY = false variants
+// run.
+template <typename P>
+bool rows_same_phase(const Operands<typename P::T>& x, int n) {
+  const auto residue = [&](int b) {
+    const size_t elem = b < 2 ? sizeof(typename P::T) : sizeof(typename P::S);
+    return static_cast<uint32_t>((reinterpret_cast<uintptr_t>(x.data[b]) / elem) % kPack);
+  };
+  const auto mod = [&](int b) {
+    return static_cast<uint32_t>(((x.stride_r[b] % kPack) + kPack) % kPack);
+  };
+  for (int b = 1; b < n; ++b) {
+    if (x.data[b] == nullptr) continue;
+    if (residue(b) != residue(0) || mod(b) != mod(0)) return false;
   }
   return true;
 }
@@ -1229,7 +1270,13 @@ int launch_dense(const Call& c, int nbufs) {
     uint32_t col_blocks = 0;
     if (streamable) {
       const uint32_t lds = blocks >= kCapMinBlocks ? P::kStreamLds : 0u;
-      hipLaunchKernelGGL(stream_kernel<P>, grid, dim3(kStreamThreads), lds, c.stream, a);
+      if (rows_same_phase<P>(a.x, nbufs)) {
+        hipLaunchKernelGGL((stream_kernel<P, false>), grid, dim3(kStreamThreads), lds, c.stream,
+                           a);
+      } else {
+        hipLaunchKernelGGL((stream_kernel<P, true>), grid, dim3(kStreamThreads), lds, c.stream,
+                           a);
+      }
     } else if (replica_minor(a.x, nbufs) && make_col_grid(c.R, c.T, ca.g, col_blocks)) {
       ca.x = a.x;
       ca.vec = a.vec;
@@ -1263,8 +1310,12 @@ int launch_segments(const Call& c, int nbufs, const ts_segment* segs, int n_segs
     return walk_fits<T>(walk, c.R, segment_tile<P>(), vec_rows, a.seg);
   };
   return run_step<T>(c, prepare, [&]() -> int {
-    return launch_walk<T>(walk, c.R, segment_tile<P>(), vec_rows, a, a.seg, segment_kernel<P>,
-                          c.stream);
+    if (rows_same_phase<P>(a.k.x, nbufs)) {
+      return launch_walk<T>(walk, c.R, segment_tile<P>(), vec_rows, a, a.seg,
+                            segment_kernel<P, false>, c.stream);
+    }
+    return launch_walk<T>(walk, c.R, segment_tile<P>(), vec_rows, a, a.seg,
+                          segment_kernel<P, true>, c.stream);
   });
 }
 
