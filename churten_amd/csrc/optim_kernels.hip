@@ -14,7 +14,9 @@
 //                   non-temporal 16-byte loads and stores from each row's
 //                   first 256-byte boundary (tiles never share a cache line),
 //                   the few head and tail elements of a row one at a time;
-//                   large launches cap residency per CU.
+//                   large launches cap residency per CU. Operands at another
+//                   16-byte phase than the parameters take element-aligned
+//                   packs (the ANY variant).
 //   column_kernel   unit replica stride on every operand (transposed views,
 //                   as an outer vmap over a non-leading dimension gives): each
 //                   thread keeps one replica and walks columns, so the threads
@@ -34,7 +36,7 @@
 // Adagrad: state_sum). The dense drivers never write the grad; the segmented
 // driver may store the gradient it read into the consolidated buffer.
 //
-// Work decomposition. Rows are cut into tiles of kTile consecutive elements
+// Work decomposition. Rows are cut into tiles of consecutive elements
 // (segments into tiles of their own); a 1-D grid enumerates (replica, tile)
 // pairs replica-major, so blockIdx.x gives both and no grid dimension caps R.
 // A workgroup first reads its replica's active flag: a frozen replica is a
