@@ -401,6 +401,13 @@ bool bf16_state(const at::Tensor& params, const at::Tensor& state) {
   return params.scalar_type() == at::kFloat && state.scalar_type() == at::kBFloat16;
 }
 
+// A float32 working copy of bfloat16 state, always row-major: whether a row
+// takes the vector formulation then depends on the params' and grads' layout
+// only, not on how the bfloat16 buffer happens to be stored.
+at::Tensor widen(const at::Tensor& state) {
+  return state.to(at::kFloat, false, false, at::MemoryFormat::Contiguous);
+}
+
 // Rounds the active rows of a widened state copy back into the bfloat16
 // buffer; frozen rows keep their bits.
 void store_active_rows(at::Tensor& dst, const at::Tensor& src, const at::Tensor& active_mask) {
@@ -431,9 +438,9 @@ at::Tensor adam_step_cpu(at::Tensor params, at::Tensor grads, at::Tensor exp_avg
     check_bf16_state(params, exp_avgs, op, "exp_avgs");
     check_bf16_state(params, exp_avg_sqs, op, "exp_avg_sqs");
     if (amsgrad) check_bf16_state(params, *max_exp_avg_sqs, op, "max_exp_avg_sqs");
-    at::Tensor m = exp_avgs.to(at::kFloat), v = exp_avg_sqs.to(at::kFloat);
+    at::Tensor m = widen(exp_avgs), v = widen(exp_avg_sqs);
     std::optional<at::Tensor> mx;
-    if (amsgrad) mx = max_exp_avg_sqs->to(at::kFloat);
+    if (amsgrad) mx = widen(*max_exp_avg_sqs);
     at::Tensor out = adam_step_cpu(params, grads, m, v, mx, state_steps, lr, beta1, beta2, eps,
                                    weight_decay, active_mask, amsgrad, maximize,
                                    decoupled_weight_decay);
@@ -481,7 +488,7 @@ at::Tensor sgd_step_cpu(at::Tensor params, at::Tensor grads,
   TORCH_CHECK(!nesterov || momentum_buffers.has_value(), "nesterov=True requires momentum_buffers");
   if (momentum_buffers.has_value() && bf16_state(params, *momentum_buffers)) {
     check_bf16_state(params, *momentum_buffers, op, "momentum_buffers");
-    std::optional<at::Tensor> mb = momentum_buffers->to(at::kFloat);
+    std::optional<at::Tensor> mb = widen(*momentum_buffers);
     at::Tensor out = sgd_step_cpu(params, grads, mb, state_steps, lr, momentum, dampening,
                                   weight_decay, active_mask, nesterov, maximize);
     store_active_rows(*momentum_buffers, *mb, active_mask);
@@ -518,7 +525,7 @@ at::Tensor adagrad_step_cpu(at::Tensor params, at::Tensor grads, at::Tensor stat
   TORCH_CHECK(params.dim() == 2, op, ": params must be a 2-D (R, T) buffer");
   if (bf16_state(params, state_sums)) {
     check_bf16_state(params, state_sums, op, "state_sums");
-    at::Tensor s32 = state_sums.to(at::kFloat);
+    at::Tensor s32 = widen(state_sums);
     at::Tensor out = adagrad_step_cpu(params, grads, s32, state_steps, lr, lr_decay,
                                       weight_decay, eps, active_mask, maximize);
     store_active_rows(state_sums, s32, active_mask);
