@@ -610,10 +610,20 @@ __global__ __launch_bounds__(kThreads) void element_kernel(KArgs<P> a) {
 // replica blocks would leave over a quarter of the threads idle, workgroups
 // have 128 threads: R = 257 / 300 ran at 4.3 / 4.7 TB/s instead of 3.3, while
 // R = 600 / 1000 / 2000 keep 256 (4.7 / 4.7 / 4.7; 128 gave 4.8 / 4.4 / 4.8).
+//
+// Non-temporal accesses where no cache line is shared between workgroups (one
+// replica block, or replica blocks, columns and bases on 128-byte boundaries)
+// and the wavefront has no frozen replica: +6-9% there (R = 8..256: 5.3 -> 5.8
+// TB/s; R = 4096: 4.8 -> 5.1). Where replica blocks split lines (R = 257..2000)
+// plain accesses let L2 merge the two halves: non-temporal ones ran at 2.6-3.9
+// TB/s instead of 4.4-4.8. (Threads that keep four replicas and move them as
+// one pack, so that a column of up to 1024 replicas has one workgroup, measured
+// 0.1-0.9 TB/s slower at every R.)
 constexpr int kColThreads = 256;
 constexpr int kColThreadsNarrow = 128;
 constexpr int kColIters = 32;  // columns per thread per workgroup
 constexpr int kColUnroll = 4;
+constexpr uint32_t kLineBytes = 128;
 
 struct ColGrid {
   int64_t R, T;
@@ -631,32 +641,42 @@ struct ColArgs {
   bool maximize;
 };
 
-template <typename P>
-__global__ __launch_bounds__(kColThreads) void column_kernel(ColArgs<P> a) {
+// One element of any storage type, plain or non-temporal.
+template <typename T>
+using ElemBits = std::conditional_t<sizeof(T) == 2, uint16_t,
+                                    std::conditional_t<sizeof(T) == 4, uint32_t, uint64_t>>;
+template <bool NT, typename T>
+__device__ __forceinline__ T load_one(const T* p) {
+  if constexpr (NT) {
+    return __builtin_bit_cast(
+        T, __builtin_nontemporal_load(reinterpret_cast<const ElemBits<T>*>(p)));
+  } else {
+    return *p;
+  }
+}
+template <bool NT, typename T>
+__device__ __forceinline__ void store_one(T* p, T v) {
+  if constexpr (NT) {
+    __builtin_nontemporal_store(__builtin_bit_cast(ElemBits<T>, v),
+                                reinterpret_cast<ElemBits<T>*>(p));
+  } else {
+    *p = v;
+  }
+}
+
+// One thread's walk over its replica's columns, plain or non-temporal.
+template <typename P, bool NT>
+__device__ __forceinline__ void column_walk(const ColArgs<P>& a, int64_t r, int64_t t_first,
+                                            const typename P::Rep& rep, bool load_state) {
   using T = typename P::T;
   using S = typename P::S;
   constexpr int NS = P::NS;
   constexpr int SS = state_slots<P>();
-  const uint32_t rblk = blockIdx.x % a.g.n_rblocks;
-  const uint32_t cblk = blockIdx.x / a.g.n_rblocks;
-  const uint32_t rr = threadIdx.x % a.g.rb;
-  const uint32_t cc = threadIdx.x / a.g.rb;
-  const int64_t r = int64_t(rblk) * a.g.rb + rr;
-  // Threads past the last replica or column lane, and frozen replicas, have
-  // nothing to do (the workgroup has no barrier).
-  if (cc >= a.g.cpi || r >= a.g.R || !a.vec.mask[r]) {
-    return;
-  }
-  typename P::Rep rep;
-  P::prologue(a.vec, static_cast<uint32_t>(r), rep);
-  const bool load_state = P::reads_state(rep);
-
   T* const pcol = a.x.data[0] + r;
   const T* const gcol = a.x.data[1] + r;
   S* scol[SS];
 #pragma unroll
   for (int b = 0; b < NS; ++b) scol[b] = reinterpret_cast<S*>(a.x.data[2 + b]) + r;
-  const int64_t t_first = int64_t(cblk) * a.g.cpi * kColIters + cc;
 
   for (int j = 0; j < kColIters; j += kColUnroll) {
     T vp[kColUnroll], vg[kColUnroll];
@@ -665,11 +685,11 @@ __global__ __launch_bounds__(kColThreads) void column_kernel(ColArgs<P> a) {
     for (int u = 0; u < kColUnroll; ++u) {
       const int64_t t = t_first + int64_t(j + u) * a.g.cpi;
       if (t < a.g.T) {
-        vp[u] = pcol[t * a.x.stride_t[0]];
-        vg[u] = gcol[t * a.x.stride_t[1]];
+        vp[u] = load_one<NT>(pcol + t * a.x.stride_t[0]);
+        vg[u] = load_one<NT>(gcol + t * a.x.stride_t[1]);
         if (load_state) {
 #pragma unroll
-          for (int b = 0; b < NS; ++b) vs[b][u] = scol[b][t * a.x.stride_t[2 + b]];
+          for (int b = 0; b < NS; ++b) vs[b][u] = load_one<NT>(scol[b] + t * a.x.stride_t[2 + b]);
         }
       }
     }
@@ -681,11 +701,45 @@ __global__ __launch_bounds__(kColThreads) void column_kernel(ColArgs<P> a) {
 #pragma unroll
         for (int b = 0; b < NS; ++b) st[b] = vs[b][u];
         apply_element<P>(vp[u], vg[u], st, load_state, rep, a.maximize);
-        pcol[t * a.x.stride_t[0]] = vp[u];
+        store_one<NT>(pcol + t * a.x.stride_t[0], vp[u]);
 #pragma unroll
-        for (int b = 0; b < NS; ++b) scol[b][t * a.x.stride_t[2 + b]] = st[b];
+        for (int b = 0; b < NS; ++b) store_one<NT>(scol[b] + t * a.x.stride_t[2 + b], st[b]);
       }
     }
+  }
+}
+
+// NT: the launch's lines are private to workgroups (col_lines_private); a
+// wavefront then goes non-temporal unless it has frozen replicas, whose
+// unwritten elements would leave partial lines (non-temporal partial lines ran
+// at 3.4-3.7 TB/s where plain ones ran at 4.7-4.9 with a tenth of the replicas
+// frozen).
+template <typename P, bool NT>
+__global__ __launch_bounds__(kColThreads) void column_kernel(ColArgs<P> a) {
+  const uint32_t rblk = blockIdx.x % a.g.n_rblocks;
+  const uint32_t cblk = blockIdx.x / a.g.n_rblocks;
+  const uint32_t rr = threadIdx.x % a.g.rb;
+  const uint32_t cc = threadIdx.x / a.g.rb;
+  const int64_t r = int64_t(rblk) * a.g.rb + rr;
+  const bool in_range = cc < a.g.cpi && r < a.g.R;
+  const bool active = in_range && a.vec.mask[r];
+  bool nt = false;
+  if constexpr (NT) {
+    nt = __ballot(in_range) == __ballot(active);
+  }
+  // Threads past the last replica or column lane, and frozen replicas, have
+  // nothing to do (the workgroup has no barrier).
+  if (!active) {
+    return;
+  }
+  typename P::Rep rep;
+  P::prologue(a.vec, static_cast<uint32_t>(r), rep);
+  const bool load_state = P::reads_state(rep);
+  const int64_t t_first = int64_t(cblk) * a.g.cpi * kColIters + cc;
+  if (nt) {
+    column_walk<P, true>(a, r, t_first, rep, load_state);
+  } else {
+    column_walk<P, false>(a, r, t_first, rep, load_state);
   }
 }
 
@@ -1075,6 +1129,23 @@ bool make_col_grid(int64_t R, int64_t T, ColGrid& g, uint32_t& blocks) {
   return true;
 }
 
+// No cache line of the column driver's operands is shared between two
+// workgroups: one replica block per column, or replica blocks, columns and
+// bases all on 128-byte boundaries.
+template <typename P>
+bool col_lines_private(const Operands<typename P::T>& x, int n, const ColGrid& g) {
+  if (g.n_rblocks == 1) return true;
+  for (int b = 0; b < n; ++b) {
+    if (x.data[b] == nullptr) continue;
+    const size_t es = b < 2 ? sizeof(typename P::T) : sizeof(typename P::S);
+    if (reinterpret_cast<uintptr_t>(x.data[b]) % kLineBytes != 0 ||
+        uint64_t(x.stride_t[b]) * es % kLineBytes != 0 || g.rb * es % kLineBytes != 0) {
+      return false;
+    }
+  }
+  return true;
+}
+
 bool make_grid(int64_t R, int64_t T, int64_t tile, Grid& g, uint32_t& blocks) {
   const int64_t tiles = (T + tile - 1) / tile;
   if (R <= 0 || T <= 0 || tiles > INT32_MAX || R > INT32_MAX / tiles) {
@@ -1283,8 +1354,13 @@ int launch_dense(const Call& c, int nbufs) {
       ca.x = a.x;
       ca.vec = a.vec;
       ca.maximize = a.maximize;
-      hipLaunchKernelGGL(column_kernel<P>, dim3(col_blocks), dim3(ca.g.threads), 0, c.stream,
-                         ca);
+      if (col_lines_private<P>(a.x, nbufs, ca.g)) {
+        hipLaunchKernelGGL((column_kernel<P, true>), dim3(col_blocks), dim3(ca.g.threads), 0,
+                           c.stream, ca);
+      } else {
+        hipLaunchKernelGGL((column_kernel<P, false>), dim3(col_blocks), dim3(ca.g.threads), 0,
+                           c.stream, ca);
+      }
     } else {
       hipLaunchKernelGGL(element_kernel<P>, grid, block, 0, c.stream, a);
     }

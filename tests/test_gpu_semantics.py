@@ -359,15 +359,19 @@ def _replica_minor(t: torch.Tensor, pad: int) -> torch.Tensor:
     return view
 
 
-@pytest.mark.parametrize("op", ["adam-amsgrad", "adamw", "sgd-nesterov", "sgd-first", "adagrad",
-                                "adagrad-f32", "adam-bf16", "adam-f64", "adam-f16", "adam-bf16p"])
-@pytest.mark.parametrize("R,T", [(2, 1), (3, 1000), (64, 33), (100, 517), (257, 40), (600, 9)])
+@pytest.mark.parametrize("op", ["adam-amsgrad", "adamw", "sgd-nesterov", "sgd-first", "sgd-mixed",
+                                "adagrad", "adagrad-f32", "adam-bf16", "adam-f64", "adam-f16",
+                                "adam-bf16p"])
+@pytest.mark.parametrize("R,T", [(2, 1), (3, 1000), (64, 33), (100, 517), (257, 40), (600, 9),
+                                 (1024, 5), (1030, 7), (2052, 3)])
 @pytest.mark.parametrize("pad", [0, 3])
 def test_replica_minor_views_bit_exact(op, R, T, pad):
     """Operands with unit replica stride ((T, R) buffers, optionally padded, seen
     as (R, T): what an outer vmap over a non-leading dimension hands over) take
     the column driver: the same bits as contiguous buffers, frozen replicas
-    untouched."""
+    untouched. Replica counts cover one and several replica blocks, packs cut
+    by the last replica, and (sgd-mixed) replicas on their first step next to
+    others that read their momentum buffer."""
     g = torch.Generator(device=DEV).manual_seed(R * 1000 + T)
     dt = {"adam-f64": torch.float64, "adam-f16": torch.float16,
           "adam-bf16p": torch.bfloat16}.get(op, torch.float32)
@@ -381,6 +385,8 @@ def test_replica_minor_views_bit_exact(op, R, T, pad):
                           generator=g).to(dt)
     if op == "sgd-first":
         steps.zero_()
+    if op == "sgd-mixed":
+        steps = torch.randint(0, 2, (R,), device=DEV, generator=g).to(dt)
     if op.startswith("adam"):
         ams = op == "adam-amsgrad"
         bufs = [rnd(), rnd(), rnd(st_dt), pos(st_dt)] + ([pos(st_dt)] if ams else [])
