@@ -370,6 +370,29 @@ def bf16_state_timing(cfg: int, launches: int):
             "step_equivalent_GBs": round(active * T * bytes_per_elem(cfg) / (ms * 1e-3) / 1e9, 1)}
 
 
+def replica_minor_timing(cfg: int, launches: int):
+    """The same update with every (R, T) operand stored replica-minor (a (T, R)
+    buffer seen as (R, T): what vmap over a non-leading dimension hands over),
+    which the column driver serves: kernel-only time and effective GB/s."""
+    import torch
+
+    op_name, args, kw, nbytes = make_config(cfg)
+    args = list(args)
+    for i in range(len(args)):
+        t = args[i]
+        if t is not None and t.dim() == 2:
+            back = torch.empty(t.shape[1], t.shape[0], dtype=t.dtype, device=t.device)
+            back.copy_(t.t())
+            args[i] = back.t()
+            del t
+    ms = kernel_only_timing(op_name, tuple(args), kw, launches)
+    del args
+    torch.cuda.empty_cache()
+    return {"kernel": "column_kernel", "kernel_avg_ms": round(ms, 4),
+            "achieved_GBs": round(nbytes / (ms * 1e-3) / 1e9, 1),
+            "frac": round(nbytes / (ms * 1e-3) / 1e9 / HBM_PEAK_GBS, 4)}
+
+
 SNAPSHOT_N = 32
 
 
@@ -508,6 +531,8 @@ def main():
                          "state's size twice in pinned host memory)")
     ap.add_argument("--no-bf16-state", action="store_true",
                     help="skip the bfloat16-optimizer-state timing")
+    ap.add_argument("--no-replica-minor", action="store_true",
+                    help="skip the replica-minor (column driver) timing")
     ap.add_argument("--no-grad-scatter", action="store_true",
                     help="skip the scatter-then-update vs fused segmented timing")
     ap.add_argument("--calibrate-copy", action="store_true",
@@ -600,6 +625,9 @@ def main():
     if not args.no_bf16_state and args.config != 3:
         bf16 = bf16_state_timing(args.config, max(10, args.steps // 2))
 
+    minor = None if args.no_replica_minor else replica_minor_timing(args.config,
+                                                                    max(10, args.steps // 2))
+
     scatter = None
     if not args.no_grad_scatter and op_name == "adam":
         scatter = grad_scatter_timing(args.config, max(5, args.steps // 2))
@@ -642,6 +670,7 @@ def main():
         "python_loop_baseline": loop or None,
         "grad_scatter_step": scatter,
         "bf16_state": bf16,
+        "replica_minor": minor,
         "adagrad_f32": adagrad_f32,
         "fp64_roofline": fp64_roofline,
         "snapshot": snapshot,
