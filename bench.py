@@ -370,6 +370,30 @@ def bf16_state_timing(cfg: int, launches: int):
             "step_equivalent_GBs": round(active * T * bytes_per_elem(cfg) / (ms * 1e-3) / 1e9, 1)}
 
 
+def other_ops_timing(adam_args, launches: int):
+    """SGD with momentum and Adagrad on the config-5 buffers (kernel-only time,
+    20 B per active element each): the Adam state's moments serve as the
+    momentum buffer and as Adagrad's sums. HBM-bound, unlike configs 3 and 4."""
+    import torch
+
+    p, gr, m, v = adam_args[:4]
+    steps, lr, mask = adam_args[5], adam_args[6], adam_args[11]
+    N, T = p.shape
+    nbytes = int(mask.sum().item()) * T * 20
+    full = lambda x: torch.full((N,), x, dtype=p.dtype, device=p.device)  # noqa: E731
+    out = {}
+    for name, op, args, kw, kernel in (
+            ("sgd", "sgd", (p, gr, m, steps, lr, full(0.9), full(0.0), full(0.0), mask),
+             dict(nesterov=False), "stream_kernel<SgdPolicy<float, true, false>>"),
+            ("adagrad", "adagrad", (p, gr, v, steps, lr, full(1e-4), full(0.0), full(1e-10), mask),
+             {}, "stream_kernel<AdagradPolicy<float>>")):
+        ms = kernel_only_timing(op, args, kw, launches)
+        gbs = nbytes / (ms * 1e-3) / 1e9
+        out[name] = {"kernel": kernel, "kernel_avg_ms": round(ms, 4), "bytes_per_elem": 20,
+                     "achieved_GBs": round(gbs, 1), "frac": round(gbs / HBM_PEAK_GBS, 4)}
+    return out
+
+
 def replica_minor_timing(cfg: int, launches: int):
     """The same update with every (R, T) operand stored replica-minor (a (T, R)
     buffer seen as (R, T): what vmap over a non-leading dimension hands over),
@@ -531,6 +555,8 @@ def main():
                          "state's size twice in pinned host memory)")
     ap.add_argument("--no-bf16-state", action="store_true",
                     help="skip the bfloat16-optimizer-state timing")
+    ap.add_argument("--no-other-ops", action="store_true",
+                    help="skip SGD and Adagrad on the config-5 buffers")
     ap.add_argument("--no-replica-minor", action="store_true",
                     help="skip the replica-minor (column driver) timing")
     ap.add_argument("--no-grad-scatter", action="store_true",
@@ -593,6 +619,8 @@ def main():
     median_ms = per_step[len(per_step) // 2]
 
     kern_ms = kernel_only_timing(op_name, op_args, kw, max(10, args.steps))
+    other_ops = (other_ops_timing(op_args, max(10, args.steps // 2))
+                 if args.config == 5 and not args.no_other_ops else None)
     achieved = nbytes / (kern_ms * 1e-3) / 1e9
     fp64_roofline = None
     adagrad_f32 = None
@@ -671,6 +699,7 @@ def main():
         "grad_scatter_step": scatter,
         "bf16_state": bf16,
         "replica_minor": minor,
+        "other_ops_cfg5_shape": other_ops,
         "adagrad_f32": adagrad_f32,
         "fp64_roofline": fp64_roofline,
         "snapshot": snapshot,
