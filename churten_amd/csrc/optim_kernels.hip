@@ -21,7 +21,10 @@
 //                   as an outer vmap over a non-leading dimension gives): each
 //                   thread keeps one replica and walks columns, so the threads
 //                   of a workgroup read consecutive replicas -- contiguous
-//                   memory.
+//                   memory. Non-temporal where workgroups own their cache
+//                   lines and a wavefront has no frozen replica; the replica
+//                   blocks of a column block share an XCD when there are
+//                   several.
 //   element_kernel  any other inner strides: one element per access.
 //   segment_kernel  the gradient arrives as one tensor per parameter (a segment
 //                   table) instead of the consolidated (R, T) gradient buffer:
@@ -47,8 +50,9 @@
 // All drivers inline the same per-element update, so the same element gives
 // the same bits whichever driver processed it.
 //
-// (column_kernel instead enumerates (column block, replica block) pairs and
-// tests the flag per thread.)
+// (column_kernel instead enumerates (column block, replica block) pairs, in
+// an XCD-aware order when a column has several replica blocks, and tests the
+// flag per thread.)
 //
 // Everything is enqueued on the caller's stream; nothing is allocated.
 
