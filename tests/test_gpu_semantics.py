@@ -423,6 +423,35 @@ def test_replica_minor_views_bit_exact(op, R, T, pad):
         assert torch.equal(a[~mask], before[i][~mask]), i
 
 
+@pytest.mark.parametrize("R,pad", [(64, 0), (256, 0), (300, 0), (1024, 0), (1024, 32), (1024, 3),
+                                   (2048, 0)])
+@pytest.mark.parametrize("frozen", [(), (70, 71, 75), (0, 1000)])
+def test_replica_minor_access_paths(R, pad, frozen):
+    """The column driver's access variants on one launch: wavefronts whose
+    replicas are all active next to ones with frozen replicas, one and several
+    replica blocks per column, with line-aligned column strides (pad 0 / 32)
+    and without (pad 3, R = 300), every workgroup order. Bit for bit against
+    contiguous buffers; frozen replicas untouched."""
+    T = 77
+    frozen = [r for r in frozen if r < R]
+    a = adam_args(R, T, seed=R + pad)
+    mask = torch.ones(R, dtype=torch.bool, device=DEV)
+    mask[frozen] = False
+    view = [_replica_minor(t, pad) for t in a[:4]]
+    dense = [t.clone() for t in a[:4]]
+    before = [t.clone() for t in a[:4]]
+    s_view, s_dense = a[5].clone(), a[5].clone()
+    kw = dict(amsgrad=False, maximize=False, decoupled_weight_decay=True)
+    for _ in range(2):
+        K.adam_step_(*view, None, s_view, *a[6:], mask, **kw)
+        K.adam_step_(*dense, None, s_dense, *a[6:], mask, **kw)
+    torch.cuda.synchronize()
+    assert torch.equal(s_view, s_dense)
+    for i, (x, y) in enumerate(zip(view, dense)):
+        assert torch.equal(x.view(torch.int32), y.view(torch.int32)), i
+        assert torch.equal(x[~mask], before[i][~mask]), i
+
+
 def test_noncontiguous_and_foreign_dtype_side_inputs():
     """(R,) inputs may be strided or float64 and steps float64, mask float:
     normalised like the reference (to the param dtype / bool)."""
