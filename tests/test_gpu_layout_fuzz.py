@@ -128,6 +128,24 @@ def test_random_layout_matches_contiguous(c):
     run_case(c)
 
 
+def _wide(rng: random.Random):
+    """Replica counts past one column-driver replica block (256), narrow rows."""
+    c = draw(rng)
+    c["R"] = rng.choice([257, 300, 512, 1000, 1024, 1030, 2048, 4096])
+    c["T"] = rng.choice([1, 3, 33, 64, 65, 129, 300])
+    return c
+
+
+WIDE_CASES = [_wide(random.Random(400000 + i)) for i in range(80)]
+
+
+@pytest.mark.parametrize("c", WIDE_CASES, ids=lambda c: (
+    f"{c['op']}-{str(c['dtype'])[6:]}{'-bf16s' if c['bf16_state'] else ''}-R{c['R']}-T{c['T']}-"
+    f"{'+'.join(c['kinds'])}-o{c['off']}-p{c['pad']}"))
+def test_random_layout_many_replicas_matches_contiguous(c):
+    run_case(c)
+
+
 def _seg_case(rng: random.Random):
     dtype = rng.choice([torch.float32, torch.float32, torch.float64, torch.float16,
                         torch.bfloat16])
