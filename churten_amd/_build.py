@@ -93,7 +93,9 @@ def build_library(verbose: bool = False) -> Path:
 CPU_KERNEL_FLAGS = ["-O3", "-mavx2", "-mfma", "-ffp-contract=off", "-fno-math-errno"]
 
 
-def build_extension(verbose: bool = False) -> Path:
+def build_extension(verbose: bool = False, sanitize: bool = False) -> Path:
+    """``sanitize``: host code with AddressSanitizer and UBSan (load it with
+    their runtimes preloaded; for the CPU tests)."""
     import torch
     from torch.utils import cpp_extension
 
@@ -112,6 +114,8 @@ def build_extension(verbose: bool = False) -> Path:
         "-DTORCH_EXTENSION_NAME=_C",
         *[f"-isystem{p}" for p in incs],
     ]
+    san = ["-fsanitize=address,undefined", "-fno-omit-frame-pointer", "-g"] if sanitize else []
+    common[1:1] = san
     build_dir = PKG / "_objs"
     build_dir.mkdir(exist_ok=True)
     objs = []
@@ -123,6 +127,7 @@ def build_extension(verbose: bool = False) -> Path:
     _run(
         [
             "g++",
+            *san,
             "-shared",
             *objs,
             "-o",
