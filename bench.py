@@ -394,6 +394,62 @@ def other_ops_timing(adam_args, launches: int):
     return out
 
 
+def lds_for_residency(n: int, lds_per_cu: int = 160 * 1024) -> int:
+    """Dynamic LDS that fits only n workgroups per CU (the streaming driver's
+    residency cap)."""
+    x = (lds_per_cu // n) // 256 * 256
+    while lds_per_cu // x > n:
+        x += 256
+    return x
+
+
+def ceiling_timing(adam_args, launches: int):
+    """The Adam step's traffic without its arithmetic on the same config-5
+    buffers (churten_amd/lib/libchurten_bench.so): 4 reads + 3 writes with the
+    update kernel's launch shape and residency cap (14 per CU) and at full
+    residency, the 4 reads alone and the 3 writes alone. `mix_bound` is the
+    rate a 16 B read + 12 B write element reaches if reads and writes each ran
+    at their own measured rate, one after the other. Runs last: the write-only
+    pass overwrites the buffers."""
+    import ctypes
+
+    import torch
+
+    lib = ctypes.CDLL(str(ROOT / "churten_amd" / "lib" / "libchurten_bench.so"))
+    p, gr, m, v = adam_args[:4]
+    mask = adam_args[11]
+    assert all(t.is_contiguous() and t.shape == p.shape and t.dtype == torch.float32
+               for t in (p, gr, m, v))
+    R, T = p.shape
+    active = int(mask.sum().item())
+    stream = torch.cuda.current_stream()
+    sink = torch.zeros(1, device=p.device)
+    vp = lambda t: ctypes.c_void_p(t.data_ptr())  # noqa: E731
+
+    def rate(mode, c, lds, per_elem):
+        call = lambda: lib.cb_traffic(  # noqa: E731
+            ctypes.c_int(mode), vp(p), vp(gr), vp(m), vp(v), vp(mask), ctypes.c_int64(R),
+            ctypes.c_int64(T), ctypes.c_float(c), ctypes.c_uint32(lds), vp(sink),
+            ctypes.c_void_p(stream.cuda_stream))
+        for _ in range(3):
+            assert call() == 0
+        e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        e0.record(stream)
+        for _ in range(launches):
+            call()
+        e1.record(stream)
+        torch.cuda.synchronize()
+        ms = e0.elapsed_time(e1) / launches
+        return round(active * T * per_elem / (ms * 1e-3) / 1e9, 1)
+
+    out = {"mix_4r3w_capped_GBs": rate(0, 0.0, lds_for_residency(14), 28),
+           "mix_4r3w_GBs": rate(0, 0.0, 0, 28),
+           "read_4_GBs": rate(1, -3.0e38, 0, 16),
+           "write_3_GBs": rate(2, 0.0, 0, 12)}
+    out["mix_bound_GBs"] = round(28 / (16 / out["read_4_GBs"] + 12 / out["write_3_GBs"]), 1)
+    return out
+
+
 def replica_minor_timing(cfg: int, launches: int):
     """The same update with every (R, T) operand stored replica-minor (a (T, R)
     buffer seen as (R, T): what vmap over a non-leading dimension hands over),
@@ -555,6 +611,8 @@ def main():
                          "state's size twice in pinned host memory)")
     ap.add_argument("--no-bf16-state", action="store_true",
                     help="skip the bfloat16-optimizer-state timing")
+    ap.add_argument("--no-ceiling", action="store_true",
+                    help="skip the traffic-only ceiling passes on the config-5 buffers")
     ap.add_argument("--no-other-ops", action="store_true",
                     help="skip SGD and Adagrad on the config-5 buffers")
     ap.add_argument("--no-replica-minor", action="store_true",
@@ -621,6 +679,12 @@ def main():
     kern_ms = kernel_only_timing(op_name, op_args, kw, max(10, args.steps))
     other_ops = (other_ops_timing(op_args, max(10, args.steps // 2))
                  if args.config == 5 and not args.no_other_ops else None)
+    ceiling = (ceiling_timing(op_args, max(10, args.steps // 2))
+               if args.config == 5 and not args.no_ceiling else None)
+    if ceiling is not None:
+        kern_gbs = nbytes / (kern_ms * 1e-3) / 1e9
+        ceiling["update_kernel_of_capped_mix"] = round(kern_gbs / ceiling["mix_4r3w_capped_GBs"], 4)
+        ceiling["update_kernel_of_mix_bound"] = round(kern_gbs / ceiling["mix_bound_GBs"], 4)
     achieved = nbytes / (kern_ms * 1e-3) / 1e9
     fp64_roofline = None
     adagrad_f32 = None
@@ -700,6 +764,7 @@ def main():
         "bf16_state": bf16,
         "replica_minor": minor,
         "other_ops_cfg5_shape": other_ops,
+        "traffic_ceiling": ceiling,
         "adagrad_f32": adagrad_f32,
         "fp64_roofline": fp64_roofline,
         "snapshot": snapshot,

@@ -29,6 +29,7 @@ LIB_DIR = PKG / "lib"
 KERNELS_DIR = PKG / "kernels"
 
 LIB = LIB_DIR / "libchurten_optim.so"
+BENCH_LIB = LIB_DIR / "libchurten_bench.so"
 EXT = KERNELS_DIR / "_C.so"
 
 ARCH = "gfx950"
@@ -148,8 +149,18 @@ def build_extension(verbose: bool = False, sanitize: bool = False) -> Path:
     return EXT
 
 
+def build_bench_library(verbose: bool = False) -> Path:
+    """The measurement aid bench.py loads (bench_kernels.hip); not the product ABI."""
+    LIB_DIR.mkdir(parents=True, exist_ok=True)
+    tmp = BENCH_LIB.with_suffix(".so.tmp")
+    _run([_hipcc(), *HIPCC_FLAGS, str(CSRC / "bench_kernels.hip"), "-o", str(tmp)], verbose)
+    os.replace(tmp, BENCH_LIB)
+    return BENCH_LIB
+
+
 def build(verbose: bool = False) -> None:
     build_library(verbose)
+    build_bench_library(verbose)
     build_extension(verbose)
 
 

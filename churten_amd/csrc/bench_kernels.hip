@@ -1,0 +1,112 @@
+// bench_kernels.hip -- measurement aid for bench.py, not part of the C ABI in
+// include/: the Adam step's HBM access pattern without its arithmetic, so the
+// update kernel's rate can be set against what the same traffic reaches on
+// the same buffers in the same process.
+//
+// Same decomposition as the streaming driver at float32: one-wave workgroups,
+// 512-element tiles of (replica, tile) pairs, frozen replicas skipped, two
+// non-temporal 16-byte packs per thread per operand. Modes:
+//   0  read params, grads, exp_avg, exp_avg_sq; write params, exp_avg,
+//      exp_avg_sq (28 B per active element, the Adam step's traffic)
+//   1  the four reads only (16 B)
+//   2  the three writes only (12 B; the written values are `c`)
+// Mode 0 writes x + g * c, so with c = 0 it leaves finite values unchanged.
+
+#include <hip/hip_runtime.h>
+
+#include <stdint.h>
+
+namespace {
+
+constexpr int kThreads = 64;
+constexpr int kUnroll = 2;
+constexpr int64_t kTile = int64_t(kThreads) * 4 * kUnroll;
+
+using F4 = float __attribute__((ext_vector_type(4)));
+
+__device__ __forceinline__ F4 ld(const F4* p) { return __builtin_nontemporal_load(p); }
+__device__ __forceinline__ void st(F4* p, F4 v) { __builtin_nontemporal_store(v, p); }
+
+template <int MODE>
+__global__ __launch_bounds__(kThreads) void traffic_kernel(float* p, const float* g, float* m,
+                                                           float* v, const uint8_t* mask,
+                                                           int64_t T, uint32_t tiles, float c,
+                                                           float* sink) {
+  const uint32_t b = blockIdx.x;
+  const uint32_t r = b / tiles;
+  const int64_t t0 = int64_t(b - r * tiles) * kTile;
+  if (!mask[r]) return;
+  const int64_t base = int64_t(r) * T + t0;
+  F4* const P = reinterpret_cast<F4*>(p + base);
+  const F4* const G = reinterpret_cast<const F4*>(g + base);
+  F4* const M = reinterpret_cast<F4*>(m + base);
+  F4* const V = reinterpret_cast<F4*>(v + base);
+  const int64_t left = (T - t0) / 4;
+  F4 a[kUnroll], bb[kUnroll], cc[kUnroll], d[kUnroll];
+  if constexpr (MODE != 2) {
+#pragma unroll
+    for (int u = 0; u < kUnroll; ++u) {
+      const int64_t i = int64_t(u) * kThreads + threadIdx.x;
+      if (i < left) {
+        a[u] = ld(P + i);
+        bb[u] = ld(G + i);
+        cc[u] = ld(M + i);
+        d[u] = ld(V + i);
+      }
+    }
+  }
+  F4 acc = F4(0.0f);
+#pragma unroll
+  for (int u = 0; u < kUnroll; ++u) {
+    const int64_t i = int64_t(u) * kThreads + threadIdx.x;
+    if (i < left) {
+      if constexpr (MODE == 0) {
+        st(P + i, a[u] + bb[u] * c);
+        st(M + i, cc[u] + bb[u] * c);
+        st(V + i, d[u] + bb[u] * c);
+      } else if constexpr (MODE == 1) {
+        acc += a[u] + bb[u] + cc[u] + d[u];
+      } else {
+        const F4 k = F4(c);
+        st(P + i, k);
+        st(M + i, k);
+        st(V + i, k);
+      }
+    }
+  }
+  if constexpr (MODE == 1) {
+    // keeps the reads: the host passes a `c` no sum of the data reaches
+    if (acc.x + acc.y + acc.z + acc.w == c) sink[0] = acc.x;
+  }
+}
+
+}  // namespace
+
+// The pattern over the active rows of four row-major (R, T) float32 buffers:
+// T a multiple of 4, every base 16-byte aligned, `mask` R bytes. `lds` is the
+// dynamic LDS per workgroup (a residency cap, as the streaming driver's).
+// Returns 0, 1 on bad arguments, or the HIP error code.
+extern "C" int cb_traffic(int mode, float* p, const float* g, float* m, float* v,
+                          const uint8_t* mask, int64_t R, int64_t T, float c, uint32_t lds,
+                          float* sink, hipStream_t stream) {
+  if (R <= 0 || T <= 0 || T % 4 != 0 || mode < 0 || mode > 2) return 1;
+  for (const void* q : {static_cast<const void*>(p), static_cast<const void*>(g),
+                        static_cast<const void*>(m), static_cast<const void*>(v)}) {
+    if (reinterpret_cast<uintptr_t>(q) % 16 != 0) return 1;
+  }
+  const int64_t tiles = (T + kTile - 1) / kTile;
+  if (tiles > INT32_MAX || R > INT32_MAX / tiles) return 1;
+  const dim3 grid(static_cast<uint32_t>(R * tiles)), block(kThreads);
+  const uint32_t t32 = static_cast<uint32_t>(tiles);
+  if (mode == 0) {
+    hipLaunchKernelGGL(traffic_kernel<0>, grid, block, lds, stream, p, g, m, v, mask, T, t32, c,
+                       sink);
+  } else if (mode == 1) {
+    hipLaunchKernelGGL(traffic_kernel<1>, grid, block, lds, stream, p, g, m, v, mask, T, t32, c,
+                       sink);
+  } else {
+    hipLaunchKernelGGL(traffic_kernel<2>, grid, block, lds, stream, p, g, m, v, mask, T, t32, c,
+                       sink);
+  }
+  return static_cast<int>(hipGetLastError());
+}
