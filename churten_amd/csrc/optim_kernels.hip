@@ -739,6 +739,9 @@ __device__ __forceinline__ void column_walk(const ColArgs<P>& a, int64_t r, int6
 // unwritten elements would leave partial lines (non-temporal partial lines ran
 // at 3.4-3.7 TB/s where plain ones ran at 4.7-4.9 with a tenth of the replicas
 // frozen; non-temporal loads with plain stores were no better, 2.8-3.4).
+// Storing after all four unrolled columns' arithmetic (the streaming driver's
+// late stores) moved the column driver by -3% (non-temporal) to +2% (plain):
+// not adopted.
 template <typename P, bool NT>
 __global__ __launch_bounds__(kColThreads) void column_kernel(ColArgs<P> a) {
   uint32_t blk = blockIdx.x;
