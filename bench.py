@@ -148,8 +148,13 @@ def make_config(cfg: int, device="cuda", seed=None, N=None):
 CPU_SAMPLE_N = 8
 
 
-def cpu_worker(cfg: int, steps: int) -> None:
-    """Child process: time the reference CPU kernel on N = CPU_SAMPLE_N replicas."""
+def cpu_worker(cfg: int, steps: int, seconds: float = 10.0) -> None:
+    """Child process: time the reference CPU kernel on N = CPU_SAMPLE_N replicas,
+    at least `steps` steps and at least `seconds` of CPU work. Waits for a line
+    on stdin first (end of input: exit without work), so the parent can start it
+    before touching the GPU and let it run after the GPU measurements."""
+    if not sys.stdin.readline():
+        return
     import torch
 
     threads = min(16, len(os.sched_getaffinity(0)))
@@ -167,11 +172,15 @@ def cpu_worker(cfg: int, steps: int) -> None:
         kind, threads = "port", 1
         op_name, args, kw, nbytes = make_config(cfg, device="cpu", N=CPU_SAMPLE_N)
         a = [t.numpy() if t is not None else None for t in args]
-        run = lambda: O.adam_step(O.CPU, *a, **kw)  # noqa: E731
+        step_fn = getattr(O, f"{op_name}_step")
+        run = lambda: step_fn(O.CPU, *a, **kw)  # noqa: E731
     run()  # warm
     t0 = time.perf_counter()
-    for _ in range(steps):
+    done = 0
+    while done < steps or time.perf_counter() - t0 < seconds:
         run()
+        done += 1
+    steps = done
     dt = (time.perf_counter() - t0) / steps
     print(json.dumps({"value": round(nbytes / dt / 1e9, 3), "unit": "GB/s",
                       "cores": threads, "kind": kind, "us_per_step": round(dt * 1e6, 1),
@@ -181,19 +190,32 @@ def cpu_worker(cfg: int, steps: int) -> None:
                                 f"{bytes_per_elem(cfg)} B x active elements"}))
 
 
-def cpu_baseline(cfg: int, steps: int):
+def cpu_baseline_start(cfg: int, steps: int, seconds: float):
+    """Starts the CPU-baseline child before this process touches the GPU; it
+    idles until cpu_baseline_finish, so no CPU sample runs just before the GPU
+    timings. (On one box, three processes that ran the 10 s sample first timed
+    the GPU at frac 0.71 against 0.77 for three without it; on another box four
+    such pairs showed no difference.)"""
     cmd = [sys.executable, str(Path(__file__).resolve()), "--cpu-worker",
-           "--config", str(cfg), "--steps", str(steps)]
+           "--config", str(cfg), "--steps", str(steps), "--cpu-seconds", str(seconds)]
     env = dict(os.environ, HIP_VISIBLE_DEVICES="", CUDA_VISIBLE_DEVICES="")
+    return subprocess.Popen(cmd, stdin=subprocess.PIPE, stdout=subprocess.PIPE,
+                            stderr=subprocess.PIPE, text=True, env=env)
+
+
+def cpu_baseline_finish(proc):
+    """Lets the child run its timing now and returns its result."""
     try:
-        out = subprocess.run(cmd, capture_output=True, text=True, timeout=600, env=env)
-        line = [ln for ln in out.stdout.splitlines() if ln.startswith("{")]
-        if out.returncode != 0 or not line:
-            sys.stderr.write(out.stderr[-2000:])
-            return None
-        return json.loads(line[-1])
+        out, err = proc.communicate("go\n", timeout=600)
     except subprocess.TimeoutExpired:
+        proc.kill()
+        proc.communicate()
         return None
+    line = [ln for ln in out.splitlines() if ln.startswith("{")]
+    if proc.returncode != 0 or not line:
+        sys.stderr.write(err[-2000:])
+        return None
+    return json.loads(line[-1])
 
 
 # ---------------------------------------------------------------------------
@@ -603,7 +625,10 @@ def main():
     ap.add_argument("--steps", type=int, default=100)
     ap.add_argument("--warmup", type=int, default=10)
     ap.add_argument("--config", type=int, default=5, choices=sorted(CONFIGS))
-    ap.add_argument("--cpu-steps", type=int, default=5)
+    ap.add_argument("--cpu-steps", type=int, default=5,
+                    help="CPU baseline: at least this many steps ...")
+    ap.add_argument("--cpu-seconds", type=float, default=10.0,
+                    help="... and at least this many seconds of CPU work")
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--no-loop-baseline", action="store_true")
     ap.add_argument("--snapshot", action="store_true",
@@ -626,7 +651,7 @@ def main():
     args = ap.parse_args()
 
     if args.cpu_worker:
-        cpu_worker(args.config, args.steps)
+        cpu_worker(args.config, args.steps, args.cpu_seconds)
         return
     if args.calibrate_copy:
         calibrate_copy()
@@ -638,8 +663,10 @@ def main():
               file=sys.stderr)
         sys.exit(2)
 
-    # CPU baseline first, before this process touches the GPU.
-    cpu = None if args.no_cpu_baseline else cpu_baseline(args.config, args.cpu_steps)
+    # The CPU-baseline child starts before this process touches the GPU and
+    # runs its timing after the GPU measurements.
+    cpu_proc = (None if args.no_cpu_baseline
+                else cpu_baseline_start(args.config, args.cpu_steps, args.cpu_seconds))
 
     import torch
 
@@ -728,6 +755,8 @@ def main():
     if not args.no_loop_baseline and op_name == "adam":
         loop["fused_ms"] = round(loop_baseline(args.config, 3, fused=True), 3)
         loop["foreach_ms"] = round(loop_baseline(args.config, 3, fused=False), 3)
+
+    cpu = None if cpu_proc is None else cpu_baseline_finish(cpu_proc)
 
     value = nbytes / (step_ms * 1e-3) / 1e9
     c = CONFIGS[args.config]
