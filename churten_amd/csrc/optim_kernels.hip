@@ -254,9 +254,11 @@ constexpr uint32_t kCapMinBlocks = 8192;
 // kLateStores (per policy): the streaming driver stores a thread's packs
 // after all of its arithmetic instead of each pack right after its own.
 // Measured interleaved on the config-5 buffers: Adam +0.6-0.9% (three boxes),
-// Adam with bfloat16 moments +1.9-2.0%, SGD +0.2-0.3%, Adagrad -1.2% (Adagrad
-// keeps the per-pack stores). The segmented driver keeps per-pack stores for
-// every policy: late ones lost 0.6-0.8% there.
+// Adam with bfloat16 moments +1.9-2.0%, SGD +0.2-0.3%, Adagrad -1.2%; Adam
+// with amsgrad -2.2% (config 2 scaled to 1200 replicas; -0.8% at config 2)
+// against +2.8% for Adam at config 1. Adagrad and amsgrad keep the per-pack
+// stores. The segmented driver keeps per-pack stores for every policy: late
+// ones lost 0.6-0.8% there.
 template <typename T, typename S>
 constexpr int stream_unroll(int fp32, int bf16_state, int narrow, int wide) {
   return std::is_same<T, double>::value ? wide
@@ -281,7 +283,7 @@ struct AdamPolicy {
   static constexpr uint32_t kStreamLds = residency_lds<T, S>(AMSGRAD ? 12 : 14);
   static constexpr int kStreamUnroll = stream_unroll<T, S>(2, 4, 4, 2);
   static constexpr int kSegmentUnroll = stream_unroll<T, S>(2, 4, 4, 2);
-  static constexpr bool kLateStores = true;
+  static constexpr bool kLateStores = !AMSGRAD;
   struct Rep {
     AdamHyper h;
     M bc1, bc2s;
