@@ -256,8 +256,10 @@ constexpr uint32_t kCapMinBlocks = 8192;
 // Measured interleaved on the config-5 buffers: Adam +0.6-0.9% (three boxes),
 // Adam with bfloat16 moments +1.9-2.0%, SGD +0.2-0.3%, Adagrad -1.2%; Adam
 // with amsgrad -2.2% (config 2 scaled to 1200 replicas; -0.8% at config 2)
-// against +2.8% for Adam at config 1. Adagrad and amsgrad keep the per-pack
-// stores. The segmented driver keeps per-pack stores for every policy: late
+// against +2.8% for Adam at config 1; float64 Adam -31% (5.06 -> 3.47 TB/s),
+// float16 Adam -2%, bfloat16-parameter Adam +1.4%. So only float32 parameters
+// (with float32 or bfloat16 state) of Adam without amsgrad and of SGD store
+// late. The segmented driver keeps per-pack stores for every policy: late
 // ones lost 0.6-0.8% there.
 template <typename T, typename S>
 constexpr int stream_unroll(int fp32, int bf16_state, int narrow, int wide) {
@@ -283,7 +285,7 @@ struct AdamPolicy {
   static constexpr uint32_t kStreamLds = residency_lds<T, S>(AMSGRAD ? 12 : 14);
   static constexpr int kStreamUnroll = stream_unroll<T, S>(2, 4, 4, 2);
   static constexpr int kSegmentUnroll = stream_unroll<T, S>(2, 4, 4, 2);
-  static constexpr bool kLateStores = !AMSGRAD;
+  static constexpr bool kLateStores = !AMSGRAD && std::is_same<T_, float>::value;
   struct Rep {
     AdamHyper h;
     M bc1, bc2s;
@@ -320,7 +322,7 @@ struct SgdPolicy {
   static constexpr uint32_t kStreamLds = HAS_BUF ? residency_lds<T, S>(14) : 0u;
   static constexpr int kStreamUnroll = stream_unroll<T, S>(2, 1, 8, 2);
   static constexpr int kSegmentUnroll = 2;
-  static constexpr bool kLateStores = true;
+  static constexpr bool kLateStores = std::is_same<T_, float>::value;
   struct Rep {
     SgdHyper<double> h;
     bool first;
