@@ -1,7 +1,9 @@
-// bench_kernels.hip -- measurement aid for bench.py, not part of the C ABI in
-// include/: the Adam step's HBM access pattern without its arithmetic, so the
-// update kernel's rate can be set against what the same traffic reaches on
-// the same buffers in the same process.
+// bench_kernels.hip -- measurement and test aids, not part of the C ABI in
+// include/. cb_traffic: the Adam step's HBM access pattern without its
+// arithmetic, so bench.py can set the update kernel's rate against what the
+// same traffic reaches on the same buffers in the same process. cb_narrow_bf16:
+// the kernels' float -> bfloat16 narrowing over an array, for the test that
+// checks it against torch's conversion on every float bit pattern.
 //
 // Same decomposition as the streaming driver at float32: one-wave workgroups,
 // 512-element tiles of (replica, tile) pairs, frozen replicas skipped, two
@@ -15,6 +17,8 @@
 #include <hip/hip_runtime.h>
 
 #include <stdint.h>
+
+#include "optim_math.h"
 
 namespace {
 
@@ -80,7 +84,22 @@ __global__ __launch_bounds__(kThreads) void traffic_kernel(float* p, const float
   }
 }
 
+__global__ __launch_bounds__(256) void narrow_bf16_kernel(const float* in, uint16_t* out,
+                                                          int64_t n) {
+  const int64_t i = int64_t(blockIdx.x) * 256 + threadIdx.x;
+  if (i < n) out[i] = churten::narrow<churten::bf16_t>(in[i]).bits;
+}
+
 }  // namespace
+
+// out[i] = the bfloat16 bits the update kernels store for the float in[i].
+// Returns 0, 1 on bad arguments, or the HIP error code.
+extern "C" int cb_narrow_bf16(const float* in, uint16_t* out, int64_t n, hipStream_t stream) {
+  if (n <= 0 || n > int64_t(UINT32_MAX) * 256) return 1;
+  const uint32_t blocks = static_cast<uint32_t>((n + 255) / 256);
+  hipLaunchKernelGGL(narrow_bf16_kernel, dim3(blocks), dim3(256), 0, stream, in, out, n);
+  return static_cast<int>(hipGetLastError());
+}
 
 // The pattern over the active rows of four row-major (R, T) float32 buffers:
 // T a multiple of 4, every base 16-byte aligned, `mask` R bytes. `lds` is the

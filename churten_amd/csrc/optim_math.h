@@ -61,14 +61,14 @@ template <> __device__ __forceinline__ _Float16 narrow<_Float16>(float x) {
   asm("" : "+v"(x));
   return static_cast<_Float16>(x);
 }
+// Round to nearest even, as torch's float -> bfloat16: gfx950 converts in
+// hardware (v_cvt_pk_bf16_f32); NaN becomes torch's canonical 0x7FC0. The
+// empty asm keeps the float rounding of the value, as for half.
 template <> __device__ __forceinline__ bf16_t narrow<bf16_t>(float x) {
+  asm("" : "+v"(x));
   bf16_t out;
-  if (x != x) {
-    out.bits = 0x7FC0u;
-  } else {
-    const uint32_t u = __float_as_uint(x);
-    out.bits = static_cast<uint16_t>((u + 0x7FFFu + ((u >> 16) & 1u)) >> 16);
-  }
+  out.bits = x != x ? static_cast<uint16_t>(0x7FC0u)
+                    : __builtin_bit_cast(uint16_t, static_cast<__bf16>(x));
   return out;
 }
 
