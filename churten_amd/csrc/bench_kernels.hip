@@ -1,9 +1,10 @@
 // bench_kernels.hip -- measurement and test aids, not part of the C ABI in
 // include/. cb_traffic: the Adam step's HBM access pattern without its
 // arithmetic, so bench.py can set the update kernel's rate against what the
-// same traffic reaches on the same buffers in the same process. cb_narrow_bf16:
-// the kernels' float -> bfloat16 narrowing over an array, for the test that
-// checks it against torch's conversion on every float bit pattern.
+// same traffic reaches on the same buffers in the same process.
+// cb_narrow_bf16 / cb_narrow_f16: the kernels' float -> bfloat16 / half
+// narrowing over an array, for the tests that check them against torch's
+// conversions on every float bit pattern.
 //
 // Same decomposition as the streaming driver at float32: one-wave workgroups,
 // 512-element tiles of (replica, tile) pairs, frozen replicas skipped, two
@@ -90,7 +91,21 @@ __global__ __launch_bounds__(256) void narrow_bf16_kernel(const float* in, uint1
   if (i < n) out[i] = churten::narrow<churten::bf16_t>(in[i]).bits;
 }
 
+__global__ __launch_bounds__(256) void narrow_f16_kernel(const float* in, uint16_t* out,
+                                                         int64_t n) {
+  const int64_t i = int64_t(blockIdx.x) * 256 + threadIdx.x;
+  if (i < n) out[i] = __builtin_bit_cast(uint16_t, churten::narrow<_Float16>(in[i]));
+}
+
 }  // namespace
+
+// out[i] = the half bits the update kernels store for the float in[i].
+extern "C" int cb_narrow_f16(const float* in, uint16_t* out, int64_t n, hipStream_t stream) {
+  if (n <= 0 || n > int64_t(UINT32_MAX) * 256) return 1;
+  const uint32_t blocks = static_cast<uint32_t>((n + 255) / 256);
+  hipLaunchKernelGGL(narrow_f16_kernel, dim3(blocks), dim3(256), 0, stream, in, out, n);
+  return static_cast<int>(hipGetLastError());
+}
 
 // out[i] = the bfloat16 bits the update kernels store for the float in[i].
 // Returns 0, 1 on bad arguments, or the HIP error code.

@@ -1,8 +1,8 @@
-"""The kernels' float -> bfloat16 narrowing (the store of bfloat16 parameters
-and of bfloat16 optimizer state) against torch's own conversion on the GPU, on
-every one of the 2^32 float bit patterns: normals, subnormals, ties, the
-largest values that round to infinity, infinities and NaNs (torch's canonical
-0x7FC0)."""
+"""The kernels' float -> bfloat16 and float -> half narrowing (the store of
+16-bit parameters and of bfloat16 optimizer state) against torch's own
+conversions on the GPU, on every one of the 2^32 float bit patterns: normals,
+subnormals, ties, the largest values that round to infinity, infinities and
+NaNs."""
 
 from __future__ import annotations
 
@@ -18,19 +18,20 @@ LIB = Path(__file__).resolve().parents[1] / "churten_amd" / "lib" / "libchurten_
 CHUNK = 1 << 30
 
 
+@pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float16])
 @pytest.mark.parametrize("part", range(4))
-def test_narrow_matches_torch_on_every_float(part):
+def test_narrow_matches_torch_on_every_float(part, dtype):
     lib = ctypes.CDLL(str(LIB))
     start = part * CHUNK - (1 << 31)  # int32 range, as the float bit patterns
     bits = torch.arange(start, start + CHUNK, dtype=torch.int64, device="cuda").to(torch.int32)
     x = bits.view(torch.float32)
     del bits
     out = torch.empty(CHUNK, dtype=torch.int16, device="cuda")
-    rc = lib.cb_narrow_bf16(ctypes.c_void_p(x.data_ptr()), ctypes.c_void_p(out.data_ptr()),
-                            ctypes.c_int64(CHUNK),
-                            ctypes.c_void_p(torch.cuda.current_stream().cuda_stream))
+    fn = lib.cb_narrow_bf16 if dtype == torch.bfloat16 else lib.cb_narrow_f16
+    rc = fn(ctypes.c_void_p(x.data_ptr()), ctypes.c_void_p(out.data_ptr()), ctypes.c_int64(CHUNK),
+            ctypes.c_void_p(torch.cuda.current_stream().cuda_stream))
     assert rc == 0
-    want = x.to(torch.bfloat16).view(torch.int16)
+    want = x.to(dtype).view(torch.int16)
     bad = (out != want).nonzero()
     if bad.numel():
         i = int(bad[0])
