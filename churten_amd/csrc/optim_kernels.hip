@@ -250,7 +250,8 @@ constexpr uint32_t kCapMinBlocks = 8192;
 // Measured per policy on config-5-sized state (1/2/4/8 packs, one process per
 // sweep, two sweeps): float32 keeps 2 (under its residency cap); bfloat16
 // state wants 4 for Adam (+13%) but 1 for SGD and Adagrad (+8-15%); 16-bit
-// params 4-8 (+12-22%); float64 is flat.
+// params 4-8 (+12-22%); float64 is flat. 16-bit Adam moved from 4 to 8 once
+// bfloat16 narrowing became one instruction: +6% (half), +10% (bfloat16).
 // kLateStores (per policy): the streaming driver stores a thread's packs
 // after all of its arithmetic instead of each pack right after its own.
 // Measured interleaved on the config-5 buffers: Adam +0.6-0.9% (three boxes),
@@ -283,7 +284,7 @@ struct AdamPolicy {
   using M = op_t<T>;
   static constexpr int NS = AMSGRAD ? 3 : 2;
   static constexpr uint32_t kStreamLds = residency_lds<T, S>(AMSGRAD ? 12 : 14);
-  static constexpr int kStreamUnroll = stream_unroll<T, S>(2, 4, 4, 2);
+  static constexpr int kStreamUnroll = stream_unroll<T, S>(2, 4, 8, 2);
   static constexpr int kSegmentUnroll = stream_unroll<T, S>(2, 4, 4, 2);
   static constexpr bool kLateStores = !AMSGRAD && std::is_same<T_, float>::value;
   struct Rep {
