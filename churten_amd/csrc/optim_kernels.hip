@@ -250,8 +250,9 @@ constexpr uint32_t kCapMinBlocks = 8192;
 // Measured per policy on config-5-sized state (1/2/4/8 packs, one process per
 // sweep, two sweeps): float32 keeps 2 (under its residency cap); bfloat16
 // state wants 4 for Adam (+13%) but 1 for SGD and Adagrad (+8-15%); 16-bit
-// params 4-8 (+12-22%); float64 is flat. 16-bit Adam moved from 4 to 8 once
-// bfloat16 narrowing became one instruction: +6% (half), +10% (bfloat16).
+// params 4-8 (+12-22%); float64 is flat. 16-bit Adam and Adagrad moved from
+// 4 to 8 once bfloat16 narrowing became one instruction: Adam +6% (half), +10%
+// (bfloat16); Adagrad +4% (half), +5.5% (bfloat16).
 // kLateStores (per policy): the streaming driver stores a thread's packs
 // after all of its arithmetic instead of each pack right after its own.
 // Measured interleaved on the config-5 buffers: Adam +0.6-0.9% (three boxes),
@@ -354,7 +355,7 @@ struct AdagradPolicy {
   using M = op_t<T>;
   static constexpr int NS = 1;
   static constexpr uint32_t kStreamLds = residency_lds<T, S>(16);
-  static constexpr int kStreamUnroll = stream_unroll<T, S>(2, 1, 4, 2);
+  static constexpr int kStreamUnroll = stream_unroll<T, S>(2, 1, 8, 2);
   static constexpr int kSegmentUnroll = 2;
   static constexpr bool kLateStores = false;
   struct Rep {
