@@ -1613,7 +1613,7 @@ using churten::make_call;
 
 extern "C" {
 
-int ts_version(void) { return 141; }
+int ts_version(void) { return 142; }
 
 int ts_bump_steps(ts_dtype dtype, void* state_steps, const uint8_t* active_mask,
                   int64_t R, void* out_zero, void* stream) {

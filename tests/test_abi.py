@@ -56,7 +56,7 @@ def test_library_exports_every_declared_symbol():
     lib = ctypes.CDLL(str(LIB))
     for name in declared_symbols():
         assert hasattr(lib, name), name
-    assert lib.ts_version() == 141
+    assert lib.ts_version() == 142
 
 
 def test_invalid_arguments_rejected_before_any_launch():
