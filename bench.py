@@ -221,7 +221,8 @@ def cpu_baseline_finish(proc):
 # ---------------------------------------------------------------------------
 # GPU measurements
 # ---------------------------------------------------------------------------
-def kernel_only_timing(op_name, args, kw, launches: int, extra_flags: int = 0) -> float:
+def kernel_only_timing(op_name, args, kw, launches: int, extra_flags: int = 0,
+                       dtype_code: int = 0) -> float:
     """Average duration (ms) of the update kernel alone: the C ABI is called
     without the step bump, bracketed by HIP events on the launch stream."""
     import ctypes
@@ -246,20 +247,20 @@ def kernel_only_timing(op_name, args, kw, launches: int, extra_flags: int = 0) -
         flags = ((1 if kw["amsgrad"] else 0) | (2 if kw["decoupled_weight_decay"] else 0)
                  | extra_flags)
         call = lambda: lib.ts_adam_step(  # noqa: E731
-            bufs, 0, vp(args[5]), *[vp(t) for t in args[6:11]], vp(args[11]),
+            bufs, dtype_code, vp(args[5]), *[vp(t) for t in args[6:11]], vp(args[11]),
             ctypes.c_int64(R), ctypes.c_int64(T), ctypes.c_uint32(flags),
             ctypes.c_void_p(0), ctypes.c_void_p(stream.cuda_stream))
     elif op_name == "sgd":
         bufs = (RtBuf * 3)(*[buf(t) for t in args[:3]])
         flags = (8 if kw["nesterov"] else 0) | extra_flags
         call = lambda: lib.ts_sgd_step(  # noqa: E731
-            bufs, 0, vp(args[3]), *[vp(t) for t in args[4:8]], vp(args[8]),
+            bufs, dtype_code, vp(args[3]), *[vp(t) for t in args[4:8]], vp(args[8]),
             ctypes.c_int64(R), ctypes.c_int64(T), ctypes.c_uint32(flags),
             ctypes.c_void_p(0), ctypes.c_void_p(stream.cuda_stream))
     elif op_name == "adagrad":
         bufs = (RtBuf * 3)(*[buf(t) for t in args[:3]])
         call = lambda: lib.ts_adagrad_step(  # noqa: E731
-            bufs, 0, vp(args[3]), *[vp(t) for t in args[4:8]], vp(args[8]),
+            bufs, dtype_code, vp(args[3]), *[vp(t) for t in args[4:8]], vp(args[8]),
             ctypes.c_int64(R), ctypes.c_int64(T), ctypes.c_uint32(extra_flags),
             ctypes.c_void_p(0), ctypes.c_void_p(stream.cuda_stream))
     else:
@@ -472,6 +473,29 @@ def ceiling_timing(adam_args, launches: int):
     return out
 
 
+def low_precision_timing(launches: int):
+    """Adam with float16 and with bfloat16 parameters (state in the parameter
+    dtype, as torch keeps it) at the config-5 shape and mask: kernel-only time
+    and effective GB/s of 14 B per active element. The buffers are the config's
+    float32 values narrowed, one dtype at a time."""
+    import torch
+
+    out = {}
+    for name, dt, code in (("f16", torch.float16, 2), ("bf16", torch.bfloat16, 3)):
+        op_name, args, kw, nbytes = make_config(5)
+        args = [t.to(dt) if t is not None and t.is_floating_point() else t for t in args]
+        T = args[0].shape[1]
+        active = int(args[-1].sum().item())
+        nb = active * T * 14
+        ms = kernel_only_timing(op_name, tuple(args), kw, launches, dtype_code=code)
+        gbs = nb / (ms * 1e-3) / 1e9
+        out[name] = {"kernel_avg_ms": round(ms, 4), "bytes_per_elem": 14,
+                     "achieved_GBs": round(gbs, 1), "frac": round(gbs / HBM_PEAK_GBS, 4)}
+        del args
+        torch.cuda.empty_cache()
+    return out
+
+
 def replica_minor_timing(cfg: int, launches: int):
     """The same update with every (R, T) operand stored replica-minor (a (T, R)
     buffer seen as (R, T): what vmap over a non-leading dimension hands over),
@@ -640,6 +664,8 @@ def main():
                     help="skip the traffic-only ceiling passes on the config-5 buffers")
     ap.add_argument("--no-other-ops", action="store_true",
                     help="skip SGD and Adagrad on the config-5 buffers")
+    ap.add_argument("--no-low-precision", action="store_true",
+                    help="skip Adam with float16 / bfloat16 parameters at the config-5 shape")
     ap.add_argument("--no-replica-minor", action="store_true",
                     help="skip the replica-minor (column driver) timing")
     ap.add_argument("--no-grad-scatter", action="store_true",
@@ -746,6 +772,8 @@ def main():
 
     minor = None if args.no_replica_minor else replica_minor_timing(args.config,
                                                                     max(10, args.steps // 2))
+    low_prec = (low_precision_timing(max(10, args.steps // 2))
+                if args.config == 5 and not args.no_low_precision else None)
 
     scatter = None
     if not args.no_grad_scatter and op_name == "adam":
@@ -792,6 +820,7 @@ def main():
         "grad_scatter_step": scatter,
         "bf16_state": bf16,
         "replica_minor": minor,
+        "low_precision_params": low_prec,
         "other_ops_cfg5_shape": other_ops,
         "traffic_ceiling": ceiling,
         "adagrad_f32": adagrad_f32,
