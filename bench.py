@@ -222,14 +222,20 @@ def cpu_baseline_finish(proc):
 # GPU measurements
 # ---------------------------------------------------------------------------
 def kernel_only_timing(op_name, args, kw, launches: int, extra_flags: int = 0,
-                       dtype_code: int = 0) -> float:
-    """Average duration (ms) of the update kernel alone: the C ABI is called
-    without the step bump, bracketed by HIP events on the launch stream."""
+                       dtype_code: int = 0, workspace: bool = True) -> float:
+    """Average duration (ms) of the update: the C ABI is called without the
+    step bump, bracketed by HIP events on the launch stream. Adam and Adagrad
+    go through the workspace entry points, as the operator does; their
+    preparation launch (the per-replica constants, one tiny kernel) is inside
+    the bracket, a few microseconds against the update's milliseconds at
+    config 5. workspace=False times the entry points without one."""
     import ctypes
 
     import torch
 
     lib = ctypes.CDLL(str(ROOT / "churten_amd" / "lib" / "libchurten_optim.so"))
+    ws = torch.empty(16 * args[0].shape[0], dtype=torch.uint8, device=args[0].device)
+    ws_args = (ctypes.c_void_p(ws.data_ptr()), ctypes.c_size_t(ws.numel()))
 
     class RtBuf(ctypes.Structure):
         _fields_ = [("data", ctypes.c_void_p), ("stride_r", ctypes.c_int64),
@@ -246,10 +252,13 @@ def kernel_only_timing(op_name, args, kw, launches: int, extra_flags: int = 0,
         bufs = (RtBuf * 5)(*[buf(t) for t in args[:5]])
         flags = ((1 if kw["amsgrad"] else 0) | (2 if kw["decoupled_weight_decay"] else 0)
                  | extra_flags)
-        call = lambda: lib.ts_adam_step(  # noqa: E731
-            bufs, dtype_code, vp(args[5]), *[vp(t) for t in args[6:11]], vp(args[11]),
-            ctypes.c_int64(R), ctypes.c_int64(T), ctypes.c_uint32(flags),
-            ctypes.c_void_p(0), ctypes.c_void_p(stream.cuda_stream))
+        head = (bufs, dtype_code, vp(args[5]), *[vp(t) for t in args[6:11]], vp(args[11]),
+                ctypes.c_int64(R), ctypes.c_int64(T), ctypes.c_uint32(flags), ctypes.c_void_p(0))
+        if workspace:
+            call = lambda: lib.ts_adam_step_ws(  # noqa: E731
+                *head, *ws_args, ctypes.c_void_p(stream.cuda_stream))
+        else:
+            call = lambda: lib.ts_adam_step(*head, ctypes.c_void_p(stream.cuda_stream))  # noqa: E731
     elif op_name == "sgd":
         bufs = (RtBuf * 3)(*[buf(t) for t in args[:3]])
         flags = (8 if kw["nesterov"] else 0) | extra_flags
@@ -259,10 +268,14 @@ def kernel_only_timing(op_name, args, kw, launches: int, extra_flags: int = 0,
             ctypes.c_void_p(0), ctypes.c_void_p(stream.cuda_stream))
     elif op_name == "adagrad":
         bufs = (RtBuf * 3)(*[buf(t) for t in args[:3]])
-        call = lambda: lib.ts_adagrad_step(  # noqa: E731
-            bufs, dtype_code, vp(args[3]), *[vp(t) for t in args[4:8]], vp(args[8]),
-            ctypes.c_int64(R), ctypes.c_int64(T), ctypes.c_uint32(extra_flags),
-            ctypes.c_void_p(0), ctypes.c_void_p(stream.cuda_stream))
+        head = (bufs, dtype_code, vp(args[3]), *[vp(t) for t in args[4:8]], vp(args[8]),
+                ctypes.c_int64(R), ctypes.c_int64(T), ctypes.c_uint32(extra_flags),
+                ctypes.c_void_p(0))
+        if workspace:
+            call = lambda: lib.ts_adagrad_step_ws(  # noqa: E731
+                *head, *ws_args, ctypes.c_void_p(stream.cuda_stream))
+        else:
+            call = lambda: lib.ts_adagrad_step(*head, ctypes.c_void_p(stream.cuda_stream))  # noqa: E731
     else:
         raise ValueError(op_name)
     for _ in range(3):
@@ -730,6 +743,10 @@ def main():
     median_ms = per_step[len(per_step) // 2]
 
     kern_ms = kernel_only_timing(op_name, op_args, kw, max(10, args.steps))
+    # the same update through the entry points without a workspace (every
+    # workgroup derives its replica's constants): what the workspace buys
+    nows_ms = (kernel_only_timing(op_name, op_args, kw, max(10, args.steps), workspace=False)
+               if op_name in ("adam", "adagrad") else None)
     other_ops = (other_ops_timing(op_args, max(10, args.steps // 2))
                  if args.config == 5 and not args.no_other_ops else None)
     ceiling = (ceiling_timing(op_args, max(10, args.steps // 2))
@@ -814,7 +831,11 @@ def main():
                      "peak": HBM_PEAK_GBS, "unit": "GB/s",
                      "frac": round(achieved / HBM_PEAK_GBS, 4),
                      "kernel_avg_ms": round(kern_ms, 4),
-                     "traffic": read_traffic(profile_key)},
+                     "traffic": read_traffic(profile_key),
+                     "without_workspace": (None if nows_ms is None else {
+                         "kernel_avg_ms": round(nows_ms, 4),
+                         "achieved": round(nbytes / (nows_ms * 1e-3) / 1e9, 1),
+                         "frac": round(nbytes / (nows_ms * 1e-3) / 1e9 / HBM_PEAK_GBS, 4)})},
         "cpu_baseline": cpu,
         "python_loop_baseline": loop or None,
         "grad_scatter_step": scatter,

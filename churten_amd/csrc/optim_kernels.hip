@@ -178,12 +178,19 @@ struct Operands {
 };
 
 // (R,) inputs: the step counter, up to five hyperparameter vectors and the mask.
+// `pre`: the call's per-replica constants (kPreWords doubles per replica,
+// replica r at pre + kPreStride * r), written by the preparation launch; null
+// when the workgroups derive them themselves.
 template <typename T>
 struct Vectors {
   const T* steps;
   const T* h[5];
   const uint8_t* mask;
+  const double* pre;
 };
+
+// Doubles per replica in a workspace of per-replica constants.
+constexpr int kPreStride = 2;
 
 // Tiles of a driver's tile size per row. For the streaming driver, row r's first
 // 256-byte boundary lies head(r) = (A - (res0 + r * rmod) % A) % A elements in
@@ -227,9 +234,10 @@ __device__ __forceinline__ double hyper_at(const T* h, uint32_t r) {
 // parameters and the other drivers keep full residency. The cap is dynamic
 // LDS that the kernel never touches (the smallest 256-byte multiple that fits
 // only n workgroups in the CU's 160 KiB), so it changes residency and nothing
-// else. `kStreamLds` is each policy's reservation; small grids (under
-// kCapMinBlocks workgroups) launch without it, since there the cap would only
-// serialise the launch. The segmented driver keeps full residency: caps of 6-10
+// else. `kStreamLds` is each policy's reservation; small launches (under
+// kCapMinElems elements of the (R, T) operands, 8192 tiles of 512) launch
+// without it, since there the cap would only serialise the launch (config 1
+// lost 16% with one). The segmented driver keeps full residency: caps of 6-10
 // workgroups per CU moved it by -3% to +2% depending on the process.
 constexpr uint32_t kLdsPerCU = 160 * 1024;
 constexpr uint32_t lds_for_residency(uint32_t n) {
@@ -243,7 +251,7 @@ template <typename T, typename S>
 constexpr uint32_t residency_lds(uint32_t n) {
   return kFp32State<T, S> ? lds_for_residency(n) : 0u;
 }
-constexpr uint32_t kCapMinBlocks = 8192;
+constexpr int64_t kCapMinElems = int64_t(8192) * 512;
 
 // Packs per thread of the streaming driver, by operand types: float32
 // throughout, float32 params with bfloat16 state, 16-bit params, float64.
@@ -276,6 +284,23 @@ constexpr int stream_unroll(int fp32, int bf16_state, int narrow, int wide) {
 // moments (momentum buffers, sums) in bfloat16 while the element math and the
 // parameters stay in float32 (the state is widened on load and rounded to
 // nearest-even on store).
+//
+// Per-replica constants. `prologue<false>` derives a replica's constants in
+// every workgroup (Adam: two fp64 pow; Adagrad: an fp64 divide);
+// `prologue<true>` reads them from the call's workspace, where the preparation
+// launch (`precompute`, once per replica and call, after the step bump) put
+// them. Both give the same bits: the workspace holds the math-type values
+// widened to double. kPreWords is the number of such doubles (0: nothing worth
+// hoisting, the policy never reads a workspace). `reads_state` is decided from
+// the (R,) vectors alone, so the drivers issue their loads before the prologue.
+//
+// Streaming shape with a workspace (kStreamUnrollPre, kStreamLdsPre). Without
+// the pow in every workgroup, float32 Adam runs fastest with one pack per
+// thread (256-element tiles) under the same cap of 14 workgroups per CU:
+// 6.51 against 6.15 TB/s for the per-workgroup form (two boxes, config-5
+// buffers, interleaved); two packs with precomputed constants reached 6.22
+// at that cap and 6.36 at 8, and a workgroup walking 2-8 consecutive tiles
+// with one prologue 6.10-6.22.
 
 // Adam / AdamW: h = {lr, beta1, beta2, eps, weight_decay}.
 template <typename T_, bool ADAMW, bool AMSGRAD, typename S_ = T_>
@@ -286,22 +311,39 @@ struct AdamPolicy {
   static constexpr int NS = AMSGRAD ? 3 : 2;
   static constexpr uint32_t kStreamLds = residency_lds<T, S>(AMSGRAD ? 12 : 14);
   static constexpr int kStreamUnroll = stream_unroll<T, S>(2, 4, 8, 2);
+  static constexpr uint32_t kStreamLdsPre = kStreamLds;
+  static constexpr int kStreamUnrollPre = stream_unroll<T, S>(AMSGRAD ? 2 : 1, 4, 8, 2);
   static constexpr int kSegmentUnroll = stream_unroll<T, S>(2, 4, 8, 2);
   static constexpr bool kLateStores = !AMSGRAD && std::is_same<T_, float>::value;
+  static constexpr int kPreWords = 2;
   struct Rep {
     AdamHyper h;
     M bc1, bc2s;
   };
+  // bias_correction1 and sqrt(bias_correction2) of the bumped step.
+  __device__ static void precompute(const Vectors<T>& v, uint32_t r, double* out) {
+    M bc1, bc2s;
+    adam_bias_corrections<M>(hyper_at(v.h[1], r), hyper_at(v.h[2], r), hyper_at(v.steps, r),
+                             bc1, bc2s);
+    out[0] = static_cast<double>(bc1);
+    out[1] = static_cast<double>(bc2s);
+  }
+  template <bool PRE>
   __device__ static void prologue(const Vectors<T>& v, uint32_t r, Rep& rep) {
     rep.h.lr = hyper_at(v.h[0], r);
     rep.h.beta1 = hyper_at(v.h[1], r);
     rep.h.beta2 = hyper_at(v.h[2], r);
     rep.h.eps = hyper_at(v.h[3], r);
     rep.h.weight_decay = hyper_at(v.h[4], r);
-    adam_bias_corrections<M>(rep.h.beta1, rep.h.beta2, hyper_at(v.steps, r), rep.bc1,
-                             rep.bc2s);
+    if constexpr (PRE) {
+      rep.bc1 = static_cast<M>(v.pre[kPreStride * r]);
+      rep.bc2s = static_cast<M>(v.pre[kPreStride * r + 1]);
+    } else {
+      adam_bias_corrections<M>(rep.h.beta1, rep.h.beta2, hyper_at(v.steps, r), rep.bc1,
+                               rep.bc2s);
+    }
   }
-  __device__ static bool reads_state(const Rep&) { return true; }
+  __device__ static bool reads_state(const Vectors<T>&, uint32_t) { return true; }
   __device__ static void update(M& p, M g, M (&s)[NS], const Rep& rep, bool maximize) {
     M mx = M(0);
     if constexpr (AMSGRAD) mx = s[2];
@@ -314,7 +356,8 @@ struct AdamPolicy {
 // SGD: h = {lr, momentum, dampening, weight_decay}. The hyperparameters are
 // carried as double inside the element math, as torch's ROCm `_fused_sgd_`
 // takes them (checked on the MI355X: carrying them as float instead changes
-// params and buffers by up to a few ulp).
+// params and buffers by up to a few ulp). Its prologue is four loads and a
+// compare: nothing to precompute.
 template <typename T_, bool HAS_BUF, bool NESTEROV, typename S_ = T_>
 struct SgdPolicy {
   using T = T_;
@@ -323,12 +366,17 @@ struct SgdPolicy {
   static constexpr int NS = HAS_BUF ? 1 : 0;
   static constexpr uint32_t kStreamLds = HAS_BUF ? residency_lds<T, S>(14) : 0u;
   static constexpr int kStreamUnroll = stream_unroll<T, S>(2, 1, 8, 2);
+  static constexpr uint32_t kStreamLdsPre = kStreamLds;
+  static constexpr int kStreamUnrollPre = kStreamUnroll;
   static constexpr int kSegmentUnroll = 2;
   static constexpr bool kLateStores = std::is_same<T_, float>::value;
+  static constexpr int kPreWords = 0;
   struct Rep {
     SgdHyper<double> h;
     bool first;
   };
+  __device__ static void precompute(const Vectors<T>&, uint32_t, double*) {}
+  template <bool PRE>
   __device__ static void prologue(const Vectors<T>& v, uint32_t r, Rep& rep) {
     rep.h.lr = hyper_at(v.h[0], r);
     rep.h.momentum = hyper_at(v.h[1], r);
@@ -338,7 +386,9 @@ struct SgdPolicy {
   }
   // On a replica's first step the buffer is overwritten by the gradient
   // without being read, so it is not fetched.
-  __device__ static bool reads_state(const Rep& rep) { return !rep.first; }
+  __device__ static bool reads_state(const Vectors<T>& v, uint32_t r) {
+    return widen(v.steps[r]) != M(1);
+  }
   __device__ static void update(M& p, M g, M (&s)[NS > 0 ? NS : 1], const Rep& rep,
                                 bool maximize) {
     M buf = s[0];
@@ -356,18 +406,31 @@ struct AdagradPolicy {
   static constexpr int NS = 1;
   static constexpr uint32_t kStreamLds = residency_lds<T, S>(16);
   static constexpr int kStreamUnroll = stream_unroll<T, S>(2, 1, 8, 2);
+  static constexpr uint32_t kStreamLdsPre = kStreamLds;
+  static constexpr int kStreamUnrollPre = kStreamUnroll;
   static constexpr int kSegmentUnroll = 2;
   static constexpr bool kLateStores = false;
+  static constexpr int kPreWords = 1;
   struct Rep {
     AdagradHyper h;
   };
+  // corrected_lr of the bumped step.
+  __device__ static void precompute(const Vectors<T>& v, uint32_t r, double* out) {
+    out[0] = adagrad_corrected_lr(hyper_at(v.h[0], r), hyper_at(v.h[1], r),
+                                  static_cast<float>(widen(v.steps[r])));
+  }
+  template <bool PRE>
   __device__ static void prologue(const Vectors<T>& v, uint32_t r, Rep& rep) {
     rep.h.weight_decay = hyper_at(v.h[2], r);
     rep.h.eps = hyper_at(v.h[3], r);
-    rep.h.corrected_lr = adagrad_corrected_lr(hyper_at(v.h[0], r), hyper_at(v.h[1], r),
-                                              static_cast<float>(widen(v.steps[r])));
+    if constexpr (PRE) {
+      rep.h.corrected_lr = v.pre[kPreStride * r];
+    } else {
+      rep.h.corrected_lr = adagrad_corrected_lr(hyper_at(v.h[0], r), hyper_at(v.h[1], r),
+                                                static_cast<float>(widen(v.steps[r])));
+    }
   }
-  __device__ static bool reads_state(const Rep&) { return true; }
+  __device__ static bool reads_state(const Vectors<T>&, uint32_t) { return true; }
   __device__ static void update(M& p, M g, M (&s)[NS], const Rep& rep, bool maximize) {
     adagrad_element<M>(p, g, s[0], rep.h, maximize);
   }
@@ -384,20 +447,32 @@ struct AdagradF32Policy {
   static constexpr int NS = 1;
   static constexpr uint32_t kStreamLds = residency_lds<T, S>(16);
   static constexpr int kStreamUnroll = stream_unroll<T, S>(2, 1, 4, 2);
+  static constexpr uint32_t kStreamLdsPre = kStreamLds;
+  static constexpr int kStreamUnrollPre = kStreamUnroll;
   static constexpr int kSegmentUnroll = 2;
   static constexpr bool kLateStores = false;
+  static constexpr int kPreWords = 1;
   struct Rep {
     AdagradF32Hyper h;
   };
+  __device__ static void precompute(const Vectors<T>& v, uint32_t r, double* out) {
+    out[0] = static_cast<double>(
+        adagrad_corrected_lr_f32(hyper_at(v.h[0], r), hyper_at(v.h[1], r), hyper_at(v.steps, r)));
+  }
+  template <bool PRE>
   __device__ static void prologue(const Vectors<T>& v, uint32_t r, Rep& rep) {
     const double wd = hyper_at(v.h[2], r);
     rep.h.weight_decay = static_cast<float>(wd);
     rep.h.has_weight_decay = wd != 0.0;
     rep.h.eps = static_cast<float>(hyper_at(v.h[3], r));
-    rep.h.corrected_lr =
-        adagrad_corrected_lr_f32(hyper_at(v.h[0], r), hyper_at(v.h[1], r), hyper_at(v.steps, r));
+    if constexpr (PRE) {
+      rep.h.corrected_lr = static_cast<float>(v.pre[kPreStride * r]);
+    } else {
+      rep.h.corrected_lr = adagrad_corrected_lr_f32(hyper_at(v.h[0], r), hyper_at(v.h[1], r),
+                                                    hyper_at(v.steps, r));
+    }
   }
-  __device__ static bool reads_state(const Rep&) { return true; }
+  __device__ static bool reads_state(const Vectors<T>&, uint32_t) { return true; }
   __device__ static void update(M& p, M g, M (&s)[NS], const Rep& rep, bool maximize) {
     adagrad_element_f32(p, g, s[0], rep.h, maximize);
   }
@@ -408,10 +483,22 @@ constexpr int state_slots() {
   return P::NS > 0 ? P::NS : 1;
 }
 
+// Packs per thread and residency reservation of the streaming driver, with
+// the per-replica constants read from a workspace (PRE) or derived in every
+// workgroup.
+template <typename P, bool PRE>
+constexpr int stream_unroll_of() {
+  return PRE ? P::kStreamUnrollPre : P::kStreamUnroll;
+}
+template <typename P, bool PRE>
+constexpr uint32_t stream_lds_of() {
+  return PRE ? P::kStreamLdsPre : P::kStreamLds;
+}
+
 // Elements per streaming tile: one wavefront x the policy's packs per thread.
-template <typename P>
+template <typename P, bool PRE>
 constexpr int64_t stream_tile() {
-  return int64_t(kStreamThreads) * kPack * P::kStreamUnroll;
+  return int64_t(kStreamThreads) * kPack * stream_unroll_of<P, PRE>();
 }
 
 // Elements per segmented-driver tile (128 threads). Measured per policy at the
@@ -470,23 +557,24 @@ __device__ __forceinline__ typename P::S* state_row(const Operands<typename P::T
 // ---------------------------------------------------------------------------
 // Drivers
 // ---------------------------------------------------------------------------
-template <typename P, bool ANY>
+// PRE: the per-replica constants come from the call's workspace (a.vec.pre).
+// A thread's loads are issued before the replica's prologue, which then runs
+// while they are in flight.
+template <typename P, bool ANY, bool PRE>
 __global__ __launch_bounds__(kStreamThreads) void stream_kernel(KArgs<P> a) {
   using T = typename P::T;
   using S = typename P::S;
   constexpr int NS = P::NS;
   constexpr int SS = state_slots<P>();
-  constexpr int U = P::kStreamUnroll;
-  constexpr int64_t kStreamTile = stream_tile<P>();
+  constexpr int U = stream_unroll_of<P, PRE>();
+  constexpr int64_t kStreamTile = stream_tile<P, PRE>();
   uint32_t r;
   int64_t t0;
   tile_of_block<kStreamTile>(a.g, r, t0);
   if (!a.vec.mask[r]) {
     return;
   }
-  typename P::Rep rep;
-  P::prologue(a.vec, r, rep);
-  const bool load_state = P::reads_state(rep);
+  const bool load_state = P::reads_state(a.vec, r);
 
   constexpr uint32_t A = align_elems<T>();
   const int64_t width = a.g.T;
@@ -523,6 +611,8 @@ __global__ __launch_bounds__(kStreamThreads) void stream_kernel(KArgs<P> a) {
       }
     }
   }
+  typename P::Rep rep;
+  P::template prologue<PRE>(a.vec, r, rep);
   const auto store_packs = [&](int u, int64_t i) {
     store_stream(prow + i, vp[u]);
 #pragma unroll
@@ -589,8 +679,8 @@ __global__ __launch_bounds__(kThreads) void element_kernel(KArgs<P> a) {
     return;
   }
   typename P::Rep rep;
-  P::prologue(a.vec, r, rep);
-  const bool load_state = P::reads_state(rep);
+  P::template prologue<false>(a.vec, r, rep);
+  const bool load_state = P::reads_state(a.vec, r);
 
   T* const prow = pg_row<P>(a.x, 0, r);
   const T* const grow = pg_row<P>(a.x, 1, r);
@@ -783,8 +873,8 @@ __global__ __launch_bounds__(kColThreads) void column_kernel(ColArgs<P> a) {
     return;
   }
   typename P::Rep rep;
-  P::prologue(a.vec, static_cast<uint32_t>(r), rep);
-  const bool load_state = P::reads_state(rep);
+  P::template prologue<false>(a.vec, static_cast<uint32_t>(r), rep);
+  const bool load_state = P::reads_state(a.vec, static_cast<uint32_t>(r));
   const int64_t t_first = int64_t(cblk) * a.g.cpi * kColIters + cc;
   if (nt) {
     column_walk<P, true>(a, r, t_first, rep, load_state);
@@ -873,7 +963,8 @@ __device__ __forceinline__ void seg_singles(const SegTile& t, int64_t numel, Fn&
   }
 }
 
-template <typename P, bool ANY>
+// PRE: the per-replica constants come from the call's workspace (a.k.vec.pre).
+template <typename P, bool ANY, bool PRE>
 __global__ __launch_bounds__(kThreads) void segment_kernel(SegArgs<P> a) {
   using T = typename P::T;
   using S = typename P::S;
@@ -933,8 +1024,8 @@ __global__ __launch_bounds__(kThreads) void segment_kernel(SegArgs<P> a) {
   }
 
   typename P::Rep rep;
-  P::prologue(a.k.vec, r, rep);
-  const bool load_state = P::reads_state(rep);
+  P::template prologue<PRE>(a.k.vec, r, rep);
+  const bool load_state = P::reads_state(a.k.vec, r);
   const T zero = narrow<T>(op_t<T>(0));
 
   T* const prow = pg_row<P>(a.k.x, 0, r) + col * a.k.x.stride_t[0];
@@ -1078,6 +1169,32 @@ __global__ __launch_bounds__(kThreads) void bump_steps_kernel(
   if (r < R) {
     const op_t<T> one = mask[r] ? op_t<T>(1) : op_t<T>(0);
     steps[r] = narrow<T>(widen(steps[r]) + one);
+  }
+  if (out_zero != nullptr && r == 0) {
+    *out_zero = narrow<T>(op_t<T>(0));
+  }
+}
+
+// The preparation launch of a call with a workspace: the optional step bump
+// (as bump_steps_kernel), then each active replica's constants from the
+// stored, bumped step into pre + kPreStride * r (frozen replicas' entries are
+// neither written nor read), and the zero result. `v.steps` points at `steps`.
+template <typename P>
+__global__ __launch_bounds__(kThreads) void prep_kernel(Vectors<typename P::T> v,
+                                                        typename P::T* steps, int64_t R,
+                                                        bool bump, double* pre,
+                                                        typename P::T* out_zero) {
+  using T = typename P::T;
+  const int64_t r = int64_t(blockIdx.x) * kThreads + threadIdx.x;
+  if (r < R) {
+    const bool active = v.mask[r] != 0;
+    if (bump) {
+      const op_t<T> one = active ? op_t<T>(1) : op_t<T>(0);
+      steps[r] = narrow<T>(widen(steps[r]) + one);
+    }
+    if (active) {
+      P::precompute(v, static_cast<uint32_t>(r), pre + kPreStride * r);
+    }
   }
   if (out_zero != nullptr && r == 0) {
     *out_zero = narrow<T>(op_t<T>(0));
@@ -1315,7 +1432,8 @@ int launch_walk(SegmentWalk w, int64_t R, int64_t tile, bool vec_rows, Args& a, 
   return 0;
 }
 
-// A call: the (R, T) operand table, the (R,) vectors and the flags.
+// A call: the (R, T) operand table, the (R,) vectors, the flags and the
+// optional workspace for per-replica constants.
 struct Call {
   const ts_rt_buf* bufs;
   void* steps;
@@ -1325,8 +1443,16 @@ struct Call {
   int64_t R, T;
   uint32_t flags;
   void* out_zero;
+  void* ws;
+  size_t ws_bytes;
   hipStream_t stream;
 };
+
+// Whether policy P takes its per-replica constants from the call's workspace.
+template <typename P>
+bool uses_workspace(const Call& c) {
+  return P::kPreWords > 0 && c.ws != nullptr;
+}
 
 template <typename P>
 bool fill_kargs(const Call& c, int nbufs, KArgs<P>& a, bool grad_optional) {
@@ -1338,27 +1464,54 @@ bool fill_kargs(const Call& c, int nbufs, KArgs<P>& a, bool grad_optional) {
     if (i < c.nh && c.h[i] == nullptr) return false;
   }
   a.vec.mask = c.mask;
+  a.vec.pre = uses_workspace<P>(c) ? static_cast<const double*>(c.ws) : nullptr;
   a.maximize = (c.flags & TS_MAXIMIZE) != 0;
   return true;
 }
 
-// Validation, then the optional bump (which also writes the zero result),
-// then `launch` when there is any work. Every check happens before the first
-// enqueue, so an invalid call changes nothing. Empty tensors may carry null
-// data pointers, so operands are only required where they are dereferenced:
-// steps and mask when R > 0, the rest (checked by `prepare`, which also fills
-// the kernel arguments) when there is at least one element.
-template <typename T, typename Prepare, typename Launch>
-int run_step(const Call& c, Prepare&& prepare, Launch&& launch) {
+template <typename P>
+int launch_prep(const Call& c, const Vectors<typename P::T>& vec) {
+  using T = typename P::T;
+  const int64_t blocks = (c.R + kThreads - 1) / kThreads;
+  if (blocks > INT32_MAX) {
+    return kInvalid;
+  }
+  hipLaunchKernelGGL(prep_kernel<P>, dim3(static_cast<uint32_t>(blocks)), dim3(kThreads), 0,
+                     c.stream, vec, static_cast<T*>(c.steps), c.R,
+                     (c.flags & TS_BUMP_STEPS) != 0, static_cast<double*>(c.ws),
+                     static_cast<T*>(c.out_zero));
+  return static_cast<int>(hipGetLastError());
+}
+
+// Validation, then the preparation launch (the optional bump and the zero
+// result; with a workspace also the per-replica constants), then `launch`
+// when there is any work. Every check happens before the first enqueue, so an
+// invalid call changes nothing. Empty tensors may carry null data pointers, so
+// operands are only required where they are dereferenced: steps and mask when
+// R > 0, the rest (checked by `prepare`, which also fills the kernel arguments
+// in `vec`) when there is at least one element. A workspace must hold
+// kPreStride doubles per replica and be 8-byte aligned.
+template <typename P, typename Prepare, typename Launch>
+int run_step(const Call& c, const Vectors<typename P::T>& vec, Prepare&& prepare,
+             Launch&& launch) {
+  using T = typename P::T;
   if (c.bufs == nullptr || c.R < 0 || c.T < 0 ||
       (c.R > 0 && (c.steps == nullptr || c.mask == nullptr))) {
+    return kInvalid;
+  }
+  if (c.ws != nullptr &&
+      (reinterpret_cast<uintptr_t>(c.ws) % alignof(double) != 0 ||
+       c.ws_bytes / (kPreStride * sizeof(double)) < static_cast<uint64_t>(c.R))) {
     return kInvalid;
   }
   const bool work = c.R > 0 && c.T > 0;
   if (work && !prepare()) {
     return kInvalid;
   }
-  if ((c.flags & TS_BUMP_STEPS) != 0 && c.R > 0) {
+  if (work && uses_workspace<P>(c)) {
+    const int err = launch_prep<P>(c, vec);
+    if (err != 0) return err;
+  } else if ((c.flags & TS_BUMP_STEPS) != 0 && c.R > 0) {
     const int err = launch_bump<T>(c.steps, c.mask, c.R, c.out_zero, c.stream);
     if (err != 0) return err;
   } else if (c.out_zero != nullptr) {
@@ -1371,35 +1524,51 @@ int run_step(const Call& c, Prepare&& prepare, Launch&& launch) {
   return launch();
 }
 
+// The streaming driver over `blocks` tiles, capped when the launch is large.
+template <typename P, bool PRE>
+void launch_stream(const KArgs<P>& a, uint32_t blocks, bool same_phase, hipStream_t stream) {
+  const uint32_t lds =
+      int64_t(blocks) * stream_tile<P, PRE>() >= kCapMinElems ? stream_lds_of<P, PRE>() : 0u;
+  if (same_phase) {
+    hipLaunchKernelGGL((stream_kernel<P, false, PRE>), dim3(blocks), dim3(kStreamThreads), lds,
+                       stream, a);
+  } else {
+    hipLaunchKernelGGL((stream_kernel<P, true, PRE>), dim3(blocks), dim3(kStreamThreads), lds,
+                       stream, a);
+  }
+}
+
 // Consolidated-gradient update with policy P over `nbufs` operands.
 template <typename P>
 int launch_dense(const Call& c, int nbufs) {
-  using T = typename P::T;
   KArgs<P> a;
   uint32_t blocks = 0;
   bool streamable = false;
+  const bool pre = uses_workspace<P>(c);
   const auto prepare = [&] {
     if (!fill_kargs<P>(c, nbufs, a, false)) return false;
     uint32_t res0 = 0, rmod = 0;
     streamable = rows_streamable<P>(a.x, nbufs, res0, rmod);
-    if (!make_grid(c.R, c.T, streamable ? stream_tile<P>() : kTile, a.g, blocks)) return false;
+    const int64_t tile =
+        !streamable ? kTile : pre ? stream_tile<P, true>() : stream_tile<P, false>();
+    if (!make_grid(c.R, c.T, tile, a.g, blocks)) return false;
     a.g.res0 = res0;
     a.g.rmod = rmod;
     return true;
   };
-  return run_step<T>(c, prepare, [&]() -> int {
+  return run_step<P>(c, a.vec, prepare, [&]() -> int {
     const dim3 grid(blocks), block(kThreads);
     ColArgs<P> ca;
     uint32_t col_blocks = 0;
     if (streamable) {
-      const uint32_t lds = blocks >= kCapMinBlocks ? P::kStreamLds : 0u;
-      if (rows_same_phase<P>(a.x, nbufs)) {
-        hipLaunchKernelGGL((stream_kernel<P, false>), grid, dim3(kStreamThreads), lds, c.stream,
-                           a);
-      } else {
-        hipLaunchKernelGGL((stream_kernel<P, true>), grid, dim3(kStreamThreads), lds, c.stream,
-                           a);
+      const bool same_phase = rows_same_phase<P>(a.x, nbufs);
+      if constexpr (P::kPreWords > 0) {
+        if (pre) {
+          launch_stream<P, true>(a, blocks, same_phase, c.stream);
+          return static_cast<int>(hipGetLastError());
+        }
       }
+      launch_stream<P, false>(a, blocks, same_phase, c.stream);
     } else if (replica_minor(a.x, nbufs) && make_col_grid(c.R, c.T, ca.g, col_blocks)) {
       ca.x = a.x;
       ca.vec = a.vec;
@@ -1437,13 +1606,20 @@ int launch_segments(const Call& c, int nbufs, const ts_segment* segs, int n_segs
     vec_rows = rows_streamable<P>(a.k.x, nbufs, a.k.g.res0, a.k.g.rmod);
     return walk_fits<T>(walk, c.R, segment_tile<P>(), vec_rows, a.seg);
   };
-  return run_step<T>(c, prepare, [&]() -> int {
-    if (rows_same_phase<P>(a.k.x, nbufs)) {
-      return launch_walk<T>(walk, c.R, segment_tile<P>(), vec_rows, a, a.seg,
-                            segment_kernel<P, false>, c.stream);
+  return run_step<P>(c, a.k.vec, prepare, [&]() -> int {
+    const bool same_phase = rows_same_phase<P>(a.k.x, nbufs);
+    if constexpr (P::kPreWords > 0) {
+      if (uses_workspace<P>(c)) {
+        return same_phase ? launch_walk<T>(walk, c.R, segment_tile<P>(), vec_rows, a, a.seg,
+                                           segment_kernel<P, false, true>, c.stream)
+                          : launch_walk<T>(walk, c.R, segment_tile<P>(), vec_rows, a, a.seg,
+                                           segment_kernel<P, true, true>, c.stream);
+      }
     }
-    return launch_walk<T>(walk, c.R, segment_tile<P>(), vec_rows, a, a.seg,
-                          segment_kernel<P, true>, c.stream);
+    return same_phase ? launch_walk<T>(walk, c.R, segment_tile<P>(), vec_rows, a, a.seg,
+                                       segment_kernel<P, false, false>, c.stream)
+                      : launch_walk<T>(walk, c.R, segment_tile<P>(), vec_rows, a, a.seg,
+                                       segment_kernel<P, true, false>, c.stream);
   });
 }
 
@@ -1587,8 +1763,10 @@ struct BumpBody {
 
 Call make_call(const ts_rt_buf* bufs, void* steps, std::initializer_list<const void*> h,
                const uint8_t* mask, int64_t R, int64_t T, uint32_t flags, void* out_zero,
-               void* stream) {
+               void* stream, void* ws = nullptr, size_t ws_bytes = 0) {
   Call c;
+  c.ws = ws;
+  c.ws_bytes = ws_bytes;
   c.bufs = bufs;
   c.steps = steps;
   c.nh = 0;
@@ -1613,7 +1791,11 @@ using churten::make_call;
 
 extern "C" {
 
-int ts_version(void) { return 142; }
+int ts_version(void) { return 200; }
+
+size_t ts_workspace_bytes(int64_t R) {
+  return R > 0 ? static_cast<size_t>(R) * churten::kPreStride * sizeof(double) : 0;
+}
 
 int ts_bump_steps(ts_dtype dtype, void* state_steps, const uint8_t* active_mask,
                   int64_t R, void* out_zero, void* stream) {
@@ -1683,6 +1865,54 @@ int ts_adagrad_step_segments(const ts_rt_buf* bufs, const ts_segment* grads, int
                              int64_t T, uint32_t flags, void* out_zero, void* stream) {
   const auto c = make_call(bufs, state_steps, {lr, lr_decay, weight_decay, eps},
                            active_mask, R, T, flags, out_zero, stream);
+  return by_dtype<churten::AdagradBody>(dtype, c, grads, n_grads, true);
+}
+
+int ts_adam_step_ws(const ts_rt_buf* bufs, ts_dtype dtype, void* state_steps, const void* lr,
+                    const void* beta1, const void* beta2, const void* eps,
+                    const void* weight_decay, const uint8_t* active_mask, int64_t R, int64_t T,
+                    uint32_t flags, void* out_zero, void* workspace, size_t workspace_bytes,
+                    void* stream) {
+  if (workspace == nullptr) return churten::kInvalid;
+  const auto c = make_call(bufs, state_steps, {lr, beta1, beta2, eps, weight_decay},
+                           active_mask, R, T, flags, out_zero, stream, workspace,
+                           workspace_bytes);
+  return by_dtype<churten::AdamBody>(dtype, c, nullptr, 0, false);
+}
+
+int ts_adagrad_step_ws(const ts_rt_buf* bufs, ts_dtype dtype, void* state_steps,
+                       const void* lr, const void* lr_decay, const void* weight_decay,
+                       const void* eps, const uint8_t* active_mask, int64_t R, int64_t T,
+                       uint32_t flags, void* out_zero, void* workspace, size_t workspace_bytes,
+                       void* stream) {
+  if (workspace == nullptr) return churten::kInvalid;
+  const auto c = make_call(bufs, state_steps, {lr, lr_decay, weight_decay, eps}, active_mask,
+                           R, T, flags, out_zero, stream, workspace, workspace_bytes);
+  return by_dtype<churten::AdagradBody>(dtype, c, nullptr, 0, false);
+}
+
+int ts_adam_step_segments_ws(const ts_rt_buf* bufs, const ts_segment* grads, int n_grads,
+                             ts_dtype dtype, void* state_steps, const void* lr,
+                             const void* beta1, const void* beta2, const void* eps,
+                             const void* weight_decay, const uint8_t* active_mask, int64_t R,
+                             int64_t T, uint32_t flags, void* out_zero, void* workspace,
+                             size_t workspace_bytes, void* stream) {
+  if (workspace == nullptr) return churten::kInvalid;
+  const auto c = make_call(bufs, state_steps, {lr, beta1, beta2, eps, weight_decay},
+                           active_mask, R, T, flags, out_zero, stream, workspace,
+                           workspace_bytes);
+  return by_dtype<churten::AdamBody>(dtype, c, grads, n_grads, true);
+}
+
+int ts_adagrad_step_segments_ws(const ts_rt_buf* bufs, const ts_segment* grads, int n_grads,
+                                ts_dtype dtype, void* state_steps, const void* lr,
+                                const void* lr_decay, const void* weight_decay,
+                                const void* eps, const uint8_t* active_mask, int64_t R,
+                                int64_t T, uint32_t flags, void* out_zero, void* workspace,
+                                size_t workspace_bytes, void* stream) {
+  if (workspace == nullptr) return churten::kInvalid;
+  const auto c = make_call(bufs, state_steps, {lr, lr_decay, weight_decay, eps}, active_mask,
+                           R, T, flags, out_zero, stream, workspace, workspace_bytes);
   return by_dtype<churten::AdagradBody>(dtype, c, grads, n_grads, true);
 }
 

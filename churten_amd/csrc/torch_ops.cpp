@@ -30,8 +30,9 @@
 // params (all of them, TS_STATE_BF16); the reference rejects mixed dtypes.
 //
 // The common case (steps in the param dtype, a bool mask, contiguous (R,)
-// vectors) costs two launches: the step bump (which also writes the zero
-// result) and the update. Anything else is first normalised with ATen ops.
+// vectors) costs two launches: the preparation (step bump, zero result and,
+// for Adam and Adagrad, the per-replica constants into a workspace) and the
+// update. Anything else is first normalised with ATen ops.
 
 #include <Python.h>
 
@@ -137,7 +138,10 @@ hipStream_t current_stream(const at::Tensor& params) {
 
 // Everything a launcher needs besides the (R, T) operand table: the step
 // counter (bumped by the launcher when TS_BUMP_STEPS is set), the mask, the
-// normalised hyperparameter vectors and the fresh zero result.
+// normalised hyperparameter vectors, the fresh zero result and, when there is
+// work, the workspace for the per-replica constants (ts_workspace_bytes(R)
+// bytes from torch's caching allocator on the current stream: no device
+// allocation once the allocator is warm, and stream-ordered reuse).
 struct Prepared {
   ts_dtype dtype;
   uint32_t flags;
@@ -145,16 +149,21 @@ struct Prepared {
   at::Tensor mask;
   std::vector<at::Tensor> hyp;
   at::Tensor out;
+  at::Tensor ws;
   int64_t R, T;
   hipStream_t stream;
 
   const void* h(size_t i) const { return hyp[i].data_ptr(); }
   const uint8_t* m() const { return static_cast<const uint8_t*>(mask.data_ptr()); }
+  bool has_ws() const { return ws.defined(); }
+  void* ws_ptr() const { return ws.data_ptr(); }
+  size_t ws_bytes() const { return static_cast<size_t>(ws.numel()); }
 };
 
 Prepared prepare(const at::Tensor& params, at::Tensor& state_steps,
                  const at::Tensor& active_mask, std::initializer_list<const at::Tensor*> hyp,
-                 std::initializer_list<const char*> names, uint32_t flags, const char* op) {
+                 std::initializer_list<const char*> names, uint32_t flags, const char* op,
+                 bool want_ws = true) {
   check_vec(params, state_steps, op, "state_steps");
   check_vec(params, active_mask, op, "active_mask");
   auto name = names.begin();
@@ -177,6 +186,10 @@ Prepared prepare(const at::Tensor& params, at::Tensor& state_steps,
   p.out = at::empty({}, params.options());
   p.R = params.size(0);
   p.T = params.size(1);
+  if (want_ws && p.R > 0 && p.T > 0) {
+    p.ws = at::empty({static_cast<int64_t>(ts_workspace_bytes(p.R))},
+                     params.options().dtype(at::kByte));
+  }
   p.stream = current_stream(params);
   return p;
 }
@@ -252,9 +265,14 @@ at::Tensor adam_step_gpu(at::Tensor params, at::Tensor grads, at::Tensor exp_avg
   const ts_rt_buf bufs[5] = {rt_buf(params), rt_buf(grads), rt_buf(exp_avgs),
                              rt_buf(exp_avg_sqs),
                              amsgrad ? rt_buf(*max_exp_avg_sqs) : kNoBuf};
-  check_status(ts_adam_step(bufs, p.dtype, p.steps.data_ptr(), p.h(0), p.h(1), p.h(2), p.h(3),
-                            p.h(4), p.m(), p.R, p.T, p.flags, p.out.data_ptr(), p.stream),
-               op);
+  check_status(
+      p.has_ws()
+          ? ts_adam_step_ws(bufs, p.dtype, p.steps.data_ptr(), p.h(0), p.h(1), p.h(2), p.h(3),
+                            p.h(4), p.m(), p.R, p.T, p.flags, p.out.data_ptr(), p.ws_ptr(),
+                            p.ws_bytes(), p.stream)
+          : ts_adam_step(bufs, p.dtype, p.steps.data_ptr(), p.h(0), p.h(1), p.h(2), p.h(3),
+                         p.h(4), p.m(), p.R, p.T, p.flags, p.out.data_ptr(), p.stream),
+      op);
   return p.out;
 }
 
@@ -278,7 +296,7 @@ at::Tensor sgd_step_gpu(at::Tensor params, at::Tensor grads,
                              {"lr", "momentum", "dampening", "weight_decay"},
                              sflag | (nesterov ? TS_NESTEROV : 0u) |
                                  (maximize ? TS_MAXIMIZE : 0u),
-                             op);
+                             op, /*want_ws=*/false);
   const ts_rt_buf bufs[3] = {rt_buf(params), rt_buf(grads),
                              momentum_buffers.has_value() ? rt_buf(*momentum_buffers) : kNoBuf};
   check_status(ts_sgd_step(bufs, p.dtype, p.steps.data_ptr(), p.h(0), p.h(1), p.h(2), p.h(3),
@@ -305,9 +323,14 @@ at::Tensor adagrad_gpu(at::Tensor params, at::Tensor grads, at::Tensor state_sum
                                  (fp32_math ? TS_ADAGRAD_F32 : 0u),
                              op);
   const ts_rt_buf bufs[3] = {rt_buf(params), rt_buf(grads), rt_buf(state_sums)};
-  check_status(ts_adagrad_step(bufs, p.dtype, p.steps.data_ptr(), p.h(0), p.h(1), p.h(2),
-                               p.h(3), p.m(), p.R, p.T, p.flags, p.out.data_ptr(), p.stream),
-               op);
+  check_status(
+      p.has_ws()
+          ? ts_adagrad_step_ws(bufs, p.dtype, p.steps.data_ptr(), p.h(0), p.h(1), p.h(2),
+                               p.h(3), p.m(), p.R, p.T, p.flags, p.out.data_ptr(), p.ws_ptr(),
+                               p.ws_bytes(), p.stream)
+          : ts_adagrad_step(bufs, p.dtype, p.steps.data_ptr(), p.h(0), p.h(1), p.h(2), p.h(3),
+                            p.m(), p.R, p.T, p.flags, p.out.data_ptr(), p.stream),
+      op);
   return p.out;
 }
 
@@ -370,11 +393,17 @@ at::Tensor adam_step_segments_gpu(at::Tensor params, at::TensorList grads, at::I
   const ts_rt_buf bufs[5] = {rt_buf(params), grads_out.has_value() ? rt_buf(*grads_out) : kNoBuf,
                              rt_buf(exp_avgs), rt_buf(exp_avg_sqs),
                              amsgrad ? rt_buf(*max_exp_avg_sqs) : kNoBuf};
-  check_status(ts_adam_step_segments(bufs, st.segs.data(), static_cast<int>(st.segs.size()),
-                                     p.dtype, p.steps.data_ptr(), p.h(0), p.h(1), p.h(2),
-                                     p.h(3), p.h(4), p.m(), p.R, p.T, p.flags, p.out.data_ptr(),
-                                     p.stream),
-               op);
+  const int n = static_cast<int>(st.segs.size());
+  check_status(
+      p.has_ws()
+          ? ts_adam_step_segments_ws(bufs, st.segs.data(), n, p.dtype, p.steps.data_ptr(),
+                                     p.h(0), p.h(1), p.h(2), p.h(3), p.h(4), p.m(), p.R, p.T,
+                                     p.flags, p.out.data_ptr(), p.ws_ptr(), p.ws_bytes(),
+                                     p.stream)
+          : ts_adam_step_segments(bufs, st.segs.data(), n, p.dtype, p.steps.data_ptr(), p.h(0),
+                                  p.h(1), p.h(2), p.h(3), p.h(4), p.m(), p.R, p.T, p.flags,
+                                  p.out.data_ptr(), p.stream),
+      op);
   return p.out;
 }
 
@@ -400,7 +429,7 @@ at::Tensor sgd_step_segments_gpu(at::Tensor params, at::TensorList grads, at::In
                              {"lr", "momentum", "dampening", "weight_decay"},
                              sflag | (nesterov ? TS_NESTEROV : 0u) |
                                  (maximize ? TS_MAXIMIZE : 0u),
-                             op);
+                             op, /*want_ws=*/false);
   const ts_rt_buf bufs[3] = {rt_buf(params), grads_out.has_value() ? rt_buf(*grads_out) : kNoBuf,
                              momentum_buffers.has_value() ? rt_buf(*momentum_buffers) : kNoBuf};
   check_status(ts_sgd_step_segments(bufs, st.segs.data(), static_cast<int>(st.segs.size()),
@@ -433,11 +462,17 @@ at::Tensor adagrad_step_segments_gpu(at::Tensor params, at::TensorList grads,
                              op);
   const ts_rt_buf bufs[3] = {rt_buf(params), grads_out.has_value() ? rt_buf(*grads_out) : kNoBuf,
                              rt_buf(state_sums)};
-  check_status(ts_adagrad_step_segments(bufs, st.segs.data(), static_cast<int>(st.segs.size()),
-                                        p.dtype, p.steps.data_ptr(), p.h(0), p.h(1), p.h(2),
-                                        p.h(3), p.m(), p.R, p.T, p.flags, p.out.data_ptr(),
-                                        p.stream),
-               op);
+  const int n = static_cast<int>(st.segs.size());
+  check_status(
+      p.has_ws()
+          ? ts_adagrad_step_segments_ws(bufs, st.segs.data(), n, p.dtype, p.steps.data_ptr(),
+                                        p.h(0), p.h(1), p.h(2), p.h(3), p.m(), p.R, p.T,
+                                        p.flags, p.out.data_ptr(), p.ws_ptr(), p.ws_bytes(),
+                                        p.stream)
+          : ts_adagrad_step_segments(bufs, st.segs.data(), n, p.dtype, p.steps.data_ptr(),
+                                     p.h(0), p.h(1), p.h(2), p.h(3), p.m(), p.R, p.T, p.flags,
+                                     p.out.data_ptr(), p.stream),
+      op);
   return p.out;
 }
 

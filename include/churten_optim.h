@@ -167,6 +167,49 @@ int ts_adagrad_step_segments(const ts_rt_buf* bufs, const ts_segment* grads, int
                              const void* eps, const uint8_t* active_mask, int64_t R,
                              int64_t T, uint32_t flags, void* out_zero, void* stream);
 
+/* Forms with a caller-provided workspace: the same updates, bit for bit, with
+ * each active replica's constants (Adam's two bias corrections, Adagrad's
+ * corrected learning rate: fp64 work every workgroup otherwise repeats) computed
+ * once per call by the launch that bumps the steps, and read by the update
+ * kernel. The update then runs a shorter tile per workgroup: the config-5 Adam
+ * step (128 x 25.2M float32) 6.51 TB/s against 6.15 for ts_adam_step on the
+ * same buffers.
+ *   workspace:       device memory of at least ts_workspace_bytes(R) bytes,
+ *                    8-byte aligned, not NULL. It is scratch: nothing is read
+ *                    from it before the call writes it, and its contents after
+ *                    the call mean nothing. It must not be shared with another
+ *                    call that may run at the same time (another stream).
+ *   workspace_bytes: its size; smaller than ts_workspace_bytes(R) is an
+ *                    invalid argument.
+ * Still two launches per call (preparation, update), as without a workspace.
+ * These replace the same reference interfaces as ts_adam_step, ts_adagrad_step
+ * and their segmented forms (stubs.cpp:25-41, 61-72; cuda/adam.cu:99-122 and
+ * cuda/adagrad.cu:141-148 are the per-block prologues whose constants the
+ * workspace hoists). */
+size_t ts_workspace_bytes(int64_t R);
+int ts_adam_step_ws(const ts_rt_buf* bufs, ts_dtype dtype, void* state_steps, const void* lr,
+                    const void* beta1, const void* beta2, const void* eps,
+                    const void* weight_decay, const uint8_t* active_mask, int64_t R, int64_t T,
+                    uint32_t flags, void* out_zero, void* workspace, size_t workspace_bytes,
+                    void* stream);
+int ts_adagrad_step_ws(const ts_rt_buf* bufs, ts_dtype dtype, void* state_steps,
+                       const void* lr, const void* lr_decay, const void* weight_decay,
+                       const void* eps, const uint8_t* active_mask, int64_t R, int64_t T,
+                       uint32_t flags, void* out_zero, void* workspace, size_t workspace_bytes,
+                       void* stream);
+int ts_adam_step_segments_ws(const ts_rt_buf* bufs, const ts_segment* grads, int n_grads,
+                             ts_dtype dtype, void* state_steps, const void* lr,
+                             const void* beta1, const void* beta2, const void* eps,
+                             const void* weight_decay, const uint8_t* active_mask, int64_t R,
+                             int64_t T, uint32_t flags, void* out_zero, void* workspace,
+                             size_t workspace_bytes, void* stream);
+int ts_adagrad_step_segments_ws(const ts_rt_buf* bufs, const ts_segment* grads, int n_grads,
+                                ts_dtype dtype, void* state_steps, const void* lr,
+                                const void* lr_decay, const void* weight_decay,
+                                const void* eps, const uint8_t* active_mask, int64_t R,
+                                int64_t T, uint32_t flags, void* out_zero, void* workspace,
+                                size_t workspace_bytes, void* stream);
+
 /* Gradient scatter in one launch per 64 segments: copies every segment, all R
  * rows, into its columns of the (R, cols) buffer dst (row stride dst_stride_r,
  * unit column stride); other columns are not written. Replaces the

@@ -57,7 +57,7 @@ def sgd_cases():
     for T, mom, damp, wd, nest, mx in itertools.product(_TS, (0.0, 0.9), (0.0, 0.3),
                                                         (0.0, 1e-2), (False, True),
                                                         (False, True)):
-        if nest and (mom == 0.0 or damp != 0.0):
+        if nest and mom == 0.0:  # nesterov needs momentum buffers
             continue
         out.append(dict(op="sgd", R=3, T=T, momentum=mom, dampening=damp, wd=wd,
                         nesterov=nest, maximize=mx, hypers="uniform", mask="one_frozen",
@@ -69,6 +69,14 @@ def sgd_cases():
     out.append(dict(op="sgd", R=4, T=16397, momentum="mixed", dampening=0.0, wd=0.0,
                     nesterov=True, maximize=False, hypers="distinct", mask="one_frozen",
                     steps0=0, nsteps=2, seed=2902))
+    # BASELINE config 3's flags: per-replica momentum {0, .5, .9, .99}, dampening
+    # 0.1 with nesterov, some replicas on their first step and some not
+    out.append(dict(op="sgd", R=6, T=1001, momentum="mixed", dampening=0.1, wd=0.0,
+                    nesterov=True, maximize=False, hypers="distinct", mask="one_frozen",
+                    steps0=[0, 3, 0, 7, 1, 0], nsteps=3, seed=2903))
+    out.append(dict(op="sgd", R=6, T=52, momentum="mixed", dampening=0.1, wd=1e-2,
+                    nesterov=True, maximize=True, hypers="distinct", mask="one_frozen",
+                    steps0=[2, 0, 0, 5, 0, 1], nsteps=2, seed=2904))
     return out
 
 
@@ -129,7 +137,10 @@ def _make_inputs(c):
     def n(*shape, scale=1.0):
         return (rng.standard_normal(shape) * scale).astype(F32)
 
-    x = {"mask": _mask(c, R), "steps": np.full(R, c["steps0"], dtype=F32)}
+    s0 = c["steps0"]  # one starting step for every replica, or one per replica
+    steps = (np.array(s0, dtype=F32) if isinstance(s0, (list, tuple))
+             else np.full(R, s0, dtype=F32))
+    x = {"mask": _mask(c, R), "steps": steps}
     x["p"] = n(R, T)
     if c["op"] == "adam":
         x["m"] = np.abs(n(R, T))
@@ -149,7 +160,8 @@ def _make_inputs(c):
     elif c["op"] == "sgd":
         mom = c["momentum"]
         if mom == "mixed":
-            x["momentum"] = np.array([0.0, 0.5, 0.9, 0.99][:R] + [0.9] * max(0, R - 4), F32)
+            x["momentum"] = np.array(([0.0, 0.5, 0.9, 0.99] * 2)[:R] + [0.9] * max(0, R - 8),
+                                     F32)
         else:
             x["momentum"] = np.full(R, mom, F32)
         has_buf = bool(np.any(x["momentum"] != 0))

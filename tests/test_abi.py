@@ -42,21 +42,22 @@ REFERENCE_SCHEMAS = {
 
 def declared_symbols():
     text = HEADER.read_text()
-    return sorted(set(re.findall(r"^\s*int\s+(ts_\w+)\s*\(", text, flags=re.M)))
+    return sorted(set(re.findall(r"^\s*(?:int|size_t)\s+(ts_\w+)\s*\(", text, flags=re.M)))
 
 
 def test_header_declares_the_entry_points():
     assert declared_symbols() == sorted(
         ["ts_adagrad_step", "ts_adam_step", "ts_bump_steps", "ts_sgd_step", "ts_version",
          "ts_adam_step_segments", "ts_sgd_step_segments", "ts_adagrad_step_segments",
-         "ts_scatter_segments", "ts_copy_rows"])
+         "ts_scatter_segments", "ts_copy_rows", "ts_workspace_bytes", "ts_adam_step_ws",
+         "ts_adagrad_step_ws", "ts_adam_step_segments_ws", "ts_adagrad_step_segments_ws"])
 
 
 def test_library_exports_every_declared_symbol():
     lib = ctypes.CDLL(str(LIB))
     for name in declared_symbols():
         assert hasattr(lib, name), name
-    assert lib.ts_version() == 142
+    assert lib.ts_version() == 200
 
 
 def test_invalid_arguments_rejected_before_any_launch():
@@ -73,6 +74,36 @@ def test_invalid_arguments_rejected_before_any_launch():
     # unknown dtype, negative R
     assert lib.ts_bump_steps(7, null, null, i64(0), null, null) == 1
     assert lib.ts_bump_steps(0, null, null, i64(-1), null, null) == 1
+
+
+def test_workspace_size_and_bad_workspaces_rejected_before_any_launch():
+    """A workspace holds two doubles per replica; a missing, short or
+    misaligned one is an invalid argument before anything is enqueued (the
+    fake device pointers would fault otherwise)."""
+    lib = ctypes.CDLL(str(LIB))
+    lib.ts_workspace_bytes.restype = ctypes.c_size_t
+    assert lib.ts_workspace_bytes(ctypes.c_int64(0)) == 0
+    assert lib.ts_workspace_bytes(ctypes.c_int64(-3)) == 0
+    assert lib.ts_workspace_bytes(ctypes.c_int64(5)) == 80
+    assert lib.ts_workspace_bytes(ctypes.c_int64(65535)) == 65535 * 16
+    fake = ctypes.c_void_p(0x10000)
+    bufs = (RTBuf * 5)(*[RTBuf(0x10000 * (i + 1), 16, 1) for i in range(5)])
+    seg = (Segment * 1)(Segment(0x90000, 16, 0, 16))
+    R, T = ctypes.c_int64(4), ctypes.c_int64(16)
+    flags = ctypes.c_uint32(0x10)
+    sz = ctypes.c_size_t
+    for ws, nbytes in ((None, 64), (0x80000, 63), (0x80004, 64)):
+        ws = ctypes.c_void_p(ws)
+        assert lib.ts_adam_step_ws(bufs, 0, fake, fake, fake, fake, fake, fake, fake, R, T,
+                                   flags, None, ws, sz(nbytes), None) == 1
+        assert lib.ts_adagrad_step_ws(bufs, 0, fake, fake, fake, fake, fake, fake, R, T,
+                                      flags, None, ws, sz(nbytes), None) == 1
+        assert lib.ts_adam_step_segments_ws(bufs, seg, 1, 0, fake, fake, fake, fake, fake,
+                                            fake, fake, R, T, flags, None, ws, sz(nbytes),
+                                            None) == 1
+        assert lib.ts_adagrad_step_segments_ws(bufs, seg, 1, 0, fake, fake, fake, fake, fake,
+                                               fake, R, T, flags, None, ws, sz(nbytes),
+                                               None) == 1
 
 
 class Segment(ctypes.Structure):

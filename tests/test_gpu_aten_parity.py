@@ -92,7 +92,7 @@ def test_adam_rows_bit_identical_to_aten(T, amsgrad, maximize, decoupled, wd, dt
 @pytest.mark.parametrize("momentum,dampening,wd,nesterov,maximize", [
     c for c in itertools.product([0.0, 0.9], [0.0, 0.3], [0.0, 1e-2], [False, True],
                                  [False, True])
-    if not (c[3] and (c[0] == 0.0 or c[1] != 0.0))])
+    if not (c[3] and c[0] == 0.0)])  # nesterov needs momentum buffers
 @pytest.mark.parametrize("dtype", DTYPES, ids=str)
 def test_sgd_rows_bit_identical_to_aten(T, momentum, dampening, wd, nesterov,
                                         maximize, dtype, R=2):
@@ -125,6 +125,58 @@ def test_sgd_rows_bit_identical_to_aten(T, momentum, dampening, wd, nesterov,
         if has_buf:
             same(f"momentum_buffers[{r}]", mb[r], ref[r][1])
     assert torch.equal(steps, torch.full((R,), 3.0, device=DEV, dtype=steps.dtype))
+
+
+# BASELINE config 3's combination in one call: per-replica momentum
+# {0.5, 0.9, 0.99} and a momentum-0 replica next to buffered ones, dampening
+# 0.1 with nesterov, replicas on their first step next to later ones, and a
+# frozen replica. Each buffered row against its own torch._fused_sgd_ call
+# (is_first_step from that row's bumped step); the momentum-0 row's params
+# against the buffer-less ATen step, which is what nesterov and a zero
+# momentum reduce to (its buffer, which ATen does not keep, is checked against
+# the oracle by the golden-case tests).
+@pytest.mark.filterwarnings("ignore:`is_first_step` argument has no effect")
+@pytest.mark.parametrize("T", [45, 70001])
+@pytest.mark.parametrize("maximize,wd", [(False, 0.0), (True, 1e-2)])
+@pytest.mark.parametrize("dtype", DTYPES, ids=str)
+def test_sgd_config3_flags_bit_identical_to_aten(T, maximize, wd, dtype):
+    R = 6
+    g = torch.Generator(device=DEV).manual_seed(T + 3)
+    rnd = lambda: torch.randn(R, T, device=DEV, generator=g, dtype=dtype)
+    p, mb = rnd(), rnd()
+    (lr, mom) = _vecs(R, [1e-2, 3e-2, 2e-2, 5e-3, 1e-2, 4e-2],
+                      [0.5, 0.9, 0.99, 0.0, 0.9, 0.5], dtype=dtype)
+    damp = torch.full((R,), f32(0.1), device=DEV, dtype=dtype)
+    wdv = torch.full((R,), f32(wd), device=DEV, dtype=dtype)
+    steps = torch.tensor([0, 3, 0, 1, 7, 0], device=DEV, dtype=torch.float32).to(dtype)
+    mask = torch.tensor([1, 1, 1, 1, 1, 0], dtype=torch.bool, device=DEV)
+    p0, mb0 = p.clone(), mb.clone()
+    ref = [(p[r].clone(), mb[r].clone()) for r in range(R)]
+    ref_steps = steps.clone()
+    for _ in range(3):
+        grad = rnd()
+        ref_steps += mask.to(dtype)
+        for r in range(R):
+            if not mask[r]:
+                continue
+            m_r = mom[r].item()
+            torch._fused_sgd_([ref[r][0]], [grad[r].clone()], [ref[r][1]] if m_r != 0 else [],
+                              weight_decay=wdv[r].item(), momentum=m_r, lr=lr[r].item(),
+                              dampening=damp[r].item(), nesterov=m_r != 0, maximize=maximize,
+                              is_first_step=bool(ref_steps[r].item() == 1),
+                              grad_scale=None, found_inf=None)
+        K.sgd_step_(p, grad, mb, steps, lr, mom, damp, wdv, mask, nesterov=True,
+                    maximize=maximize)
+    torch.cuda.synchronize()
+    for r in range(R):
+        if not mask[r]:
+            same(f"frozen params[{r}]", p[r], p0[r])
+            same(f"frozen momentum_buffers[{r}]", mb[r], mb0[r])
+            continue
+        same(f"params[{r}]", p[r], ref[r][0])
+        if mom[r].item() != 0:
+            same(f"momentum_buffers[{r}]", mb[r], ref[r][1])
+    assert torch.equal(steps, ref_steps)
 
 
 @pytest.mark.parametrize("T", [64, 45, 70001])
