@@ -108,17 +108,35 @@ template <typename T>
 using PackBits = uint32_t __attribute__((ext_vector_type(sizeof(T) * kPack / 4)));
 
 // Streaming accesses: every byte of the optimizer state is touched exactly
-// once per step, so the loads and stores carry the non-temporal hint.
-template <typename T>
-__device__ __forceinline__ Pack<T> load_stream(const Pack<T>* p) {
-  return __builtin_bit_cast(
-      Pack<T>, __builtin_nontemporal_load(reinterpret_cast<const PackBits<T>*>(p)));
+// once per step, so the loads and stores carry the non-temporal hint (NT).
+// Launches whose operands fit the 256 MB MALL several times over take plain,
+// cache-allocating accesses instead (NT = false): back-to-back steps then hit
+// the MALL (see the streaming driver's launch).
+template <bool NT, typename V>
+__device__ __forceinline__ V load_bits(const V* p) {
+  if constexpr (NT) {
+    return __builtin_nontemporal_load(p);
+  } else {
+    return *p;
+  }
+}
+template <bool NT, typename V>
+__device__ __forceinline__ void store_bits(V* p, V v) {
+  if constexpr (NT) {
+    __builtin_nontemporal_store(v, p);
+  } else {
+    *p = v;
+  }
 }
 
-template <typename T>
+template <bool NT = true, typename T>
+__device__ __forceinline__ Pack<T> load_stream(const Pack<T>* p) {
+  return __builtin_bit_cast(Pack<T>, load_bits<NT>(reinterpret_cast<const PackBits<T>*>(p)));
+}
+
+template <bool NT = true, typename T>
 __device__ __forceinline__ void store_stream(Pack<T>* p, const Pack<T>& v) {
-  __builtin_nontemporal_store(__builtin_bit_cast(PackBits<T>, v),
-                              reinterpret_cast<PackBits<T>*>(p));
+  store_bits<NT>(reinterpret_cast<PackBits<T>*>(p), __builtin_bit_cast(PackBits<T>, v));
 }
 
 // Packs at addresses that are only element-aligned: operands whose 16-byte
@@ -131,40 +149,40 @@ template <typename T>
 using PackBitsU = uint32_t
     __attribute__((ext_vector_type(sizeof(T) * kPack / 4), aligned(sizeof(T))));
 
-template <typename T>
+template <bool NT = true, typename T>
 __device__ __forceinline__ Pack<T> load_stream_any(const T* p) {
-  return __builtin_bit_cast(
-      Pack<T>, __builtin_nontemporal_load(reinterpret_cast<const PackBitsU<T>*>(p)));
+  return __builtin_bit_cast(Pack<T>, load_bits<NT>(reinterpret_cast<const PackBitsU<T>*>(p)));
 }
 
-template <typename T>
+template <bool NT = true, typename T>
 __device__ __forceinline__ void store_stream_any(T* p, const Pack<T>& v) {
-  __builtin_nontemporal_store(__builtin_bit_cast(PackBitsU<T>, v),
-                              reinterpret_cast<PackBitsU<T>*>(p));
+  store_bits<NT>(reinterpret_cast<PackBitsU<T>*>(p), __builtin_bit_cast(PackBitsU<T>, v));
 }
 
 // The packs of an operand from a given element on: 16-byte aligned wherever
 // the parameters' packs are (ANY = false, the usual case: the compiler knows
 // the alignment) or only element-aligned (ANY = true). Indexed by pack.
-template <bool ANY, typename T>
+template <bool ANY, typename T, bool NT = true>
 struct Packs;
 
-template <typename T>
-struct Packs<false, T> {
+template <typename T, bool NT>
+struct Packs<false, T, NT> {
   Pack<T>* p = nullptr;
   Packs() = default;
   __device__ explicit Packs(T* e) : p(reinterpret_cast<Pack<T>*>(e)) {}
-  __device__ Pack<T> load(int64_t i) const { return load_stream(p + i); }
-  __device__ void store(int64_t i, const Pack<T>& v) const { store_stream(p + i, v); }
+  __device__ Pack<T> load(int64_t i) const { return load_stream<NT>(p + i); }
+  __device__ void store(int64_t i, const Pack<T>& v) const { store_stream<NT>(p + i, v); }
 };
 
-template <typename T>
-struct Packs<true, T> {
+template <typename T, bool NT>
+struct Packs<true, T, NT> {
   T* p = nullptr;
   Packs() = default;
   __device__ explicit Packs(T* e) : p(e) {}
-  __device__ Pack<T> load(int64_t i) const { return load_stream_any(p + i * kPack); }
-  __device__ void store(int64_t i, const Pack<T>& v) const { store_stream_any(p + i * kPack, v); }
+  __device__ Pack<T> load(int64_t i) const { return load_stream_any<NT>(p + i * kPack); }
+  __device__ void store(int64_t i, const Pack<T>& v) const {
+    store_stream_any<NT>(p + i * kPack, v);
+  }
 };
 
 constexpr int kMaxOperands = 5;
@@ -228,17 +246,20 @@ __device__ __forceinline__ double hyper_at(const T* h, uint32_t r) {
 // Residency cap of the streaming driver. A large streaming launch runs faster
 // with fewer one-wave workgroups resident per CU than the register budget
 // allows (24): measured on the MI355X over config-5-sized fp32 state (same
-// buffers, interleaved, several processes), 14 per CU for Adam, 12 with
-// amsgrad, 14 for SGD with momentum and 16 for Adagrad, +3-10% over no cap.
-// bfloat16 state lost with any cap and fp64 gained nothing; those, 16-bit
-// parameters and the other drivers keep full residency. The cap is dynamic
-// LDS that the kernel never touches (the smallest 256-byte multiple that fits
-// only n workgroups in the CU's 160 KiB), so it changes residency and nothing
-// else. `kStreamLds` is each policy's reservation; small launches (under
-// kCapMinElems elements of the (R, T) operands, 8192 tiles of 512) launch
-// without it, since there the cap would only serialise the launch (config 1
-// lost 16% with one). The segmented driver keeps full residency: caps of 6-10
-// workgroups per CU moved it by -3% to +2% depending on the process.
+// buffers, interleaved, several processes), with every workgroup deriving its
+// replica's constants: 14 per CU for Adam, 12 with amsgrad and 16 for
+// Adagrad, +3-10% over no cap; bfloat16 state lost with any cap and fp64
+// gained nothing. With the constants precomputed the caps move (below, next to
+// the policies). The cap is dynamic LDS that the kernel never touches (the
+// smallest 256-byte multiple that fits only n workgroups in the CU's 160 KiB),
+// so it changes residency and nothing else. `kStreamLds` / `kStreamLdsPre` are
+// each policy's reservations; small launches (under kCapMinElems elements of
+// the (R, T) operands, 8192 tiles of 512) launch without them, since there the
+// cap would only serialise the launch (config 1 lost 16% with one). The
+// segmented driver (`kSegmentLds`) runs uncapped when workgroups derive their
+// constants (caps of 6-10 moved it by -3% to +2%); with a workspace, float32
+// Adam there runs at 8 workgroups (16 waves) per CU: 6.46-6.47 against
+// 6.38 TB/s uncapped.
 constexpr uint32_t kLdsPerCU = 160 * 1024;
 constexpr uint32_t lds_for_residency(uint32_t n) {
   uint32_t x = (kLdsPerCU / n) / 256 * 256;
@@ -251,7 +272,19 @@ template <typename T, typename S>
 constexpr uint32_t residency_lds(uint32_t n) {
   return kFp32State<T, S> ? lds_for_residency(n) : 0u;
 }
+template <typename T, typename S>
+constexpr bool kBf16State = std::is_same<T, float>::value && std::is_same<S, bf16_t>::value;
 constexpr int64_t kCapMinElems = int64_t(8192) * 512;
+
+// Launches whose (R, T) operands take at most this many bytes run the SMALL
+// streaming shape (plain accesses, the policy's kStreamUnrollSmall, no cap):
+// the MI355X's 256 MB MALL then keeps them between back-to-back steps.
+// Measured on configs 1-4 (prep + update through the C ABI, 200 launches, 5
+// rounds): config 1 (34 MB of Adam operands) 11.7 us plain with 2 packs
+// against 13.0 non-temporal; config 3 (209 MB, SGD) 32.0 us plain with 1 pack
+// (2 / 4 / 8 packs: 33.9 / 32.6 / 32.2) against 35.8; configs 2 and 4 (531 /
+// 419 MB) lose 11-16% with plain accesses, so they stay non-temporal.
+constexpr int64_t kMallBytes = int64_t(256) << 20;
 
 // Packs per thread of the streaming driver, by operand types: float32
 // throughout, float32 params with bfloat16 state, 16-bit params, float64.
@@ -300,7 +333,18 @@ constexpr int stream_unroll(int fp32, int bf16_state, int narrow, int wide) {
 // 6.51 against 6.15 TB/s for the per-workgroup form (two boxes, config-5
 // buffers, interleaved); two packs with precomputed constants reached 6.22
 // at that cap and 6.36 at 8, and a workgroup walking 2-8 consecutive tiles
-// with one prologue 6.10-6.22.
+// with one prologue 6.10-6.22. The same sweep per policy (config-5 shape,
+// 3 interleaved rounds, two boxes; one pack against the old two):
+//   Adam with amsgrad    1 pack, cap 12: 6.34-6.36 TB/s (2 packs: 5.85)
+//   Adagrad (fp64 math)  1 pack, cap 20: 6.45-6.49 (2 packs, cap 16: 5.70;
+//                        caps 18-24 within 0.7% of each other)
+//   Adagrad, fp32 math   1 pack, cap 20: 6.52 (2 packs, cap 16: 5.84)
+//   Adam, bf16 moments   4 packs, cap 12: 6.15-6.31 (uncapped: 5.90-6.23)
+// SGD has no workspace, but with its loads issued before the prologue its
+// buffered float32 form also runs one pack per thread, cap 20: 6.46-6.60
+// against 6.13 for two packs at cap 14. 16-bit parameters (8 packs,
+// uncapped), bfloat16-state SGD and Adagrad (1 pack, uncapped) and float64
+// (2 packs) kept their shapes: nothing else in the sweep beat them.
 
 // Adam / AdamW: h = {lr, beta1, beta2, eps, weight_decay}.
 template <typename T_, bool ADAMW, bool AMSGRAD, typename S_ = T_>
@@ -311,9 +355,13 @@ struct AdamPolicy {
   static constexpr int NS = AMSGRAD ? 3 : 2;
   static constexpr uint32_t kStreamLds = residency_lds<T, S>(AMSGRAD ? 12 : 14);
   static constexpr int kStreamUnroll = stream_unroll<T, S>(2, 4, 8, 2);
-  static constexpr uint32_t kStreamLdsPre = kStreamLds;
-  static constexpr int kStreamUnrollPre = stream_unroll<T, S>(AMSGRAD ? 2 : 1, 4, 8, 2);
+  static constexpr uint32_t kStreamLdsPre =
+      kBf16State<T, S> ? lds_for_residency(12) : kStreamLds;
+  static constexpr int kStreamUnrollPre = stream_unroll<T, S>(1, 4, 8, 2);
+  static constexpr int kStreamUnrollSmall = stream_unroll<T, S>(2, 4, 8, 2);
+  static constexpr int64_t kStreamSmallBytes = kMallBytes;
   static constexpr int kSegmentUnroll = stream_unroll<T, S>(2, 4, 8, 2);
+  static constexpr uint32_t kSegmentLds = residency_lds<T, S>(8);
   static constexpr bool kLateStores = !AMSGRAD && std::is_same<T_, float>::value;
   static constexpr int kPreWords = 2;
   struct Rep {
@@ -364,11 +412,14 @@ struct SgdPolicy {
   using S = S_;
   using M = op_t<T>;
   static constexpr int NS = HAS_BUF ? 1 : 0;
-  static constexpr uint32_t kStreamLds = HAS_BUF ? residency_lds<T, S>(14) : 0u;
-  static constexpr int kStreamUnroll = stream_unroll<T, S>(2, 1, 8, 2);
+  static constexpr uint32_t kStreamLds = HAS_BUF ? residency_lds<T, S>(20) : 0u;
+  static constexpr int kStreamUnroll = stream_unroll<T, S>(HAS_BUF ? 1 : 2, 1, 8, 2);
   static constexpr uint32_t kStreamLdsPre = kStreamLds;
   static constexpr int kStreamUnrollPre = kStreamUnroll;
+  static constexpr int kStreamUnrollSmall = stream_unroll<T, S>(1, 1, 8, 2);
+  static constexpr int64_t kStreamSmallBytes = kMallBytes;
   static constexpr int kSegmentUnroll = 2;
+  static constexpr uint32_t kSegmentLds = 0;
   static constexpr bool kLateStores = std::is_same<T_, float>::value;
   static constexpr int kPreWords = 0;
   struct Rep {
@@ -406,9 +457,12 @@ struct AdagradPolicy {
   static constexpr int NS = 1;
   static constexpr uint32_t kStreamLds = residency_lds<T, S>(16);
   static constexpr int kStreamUnroll = stream_unroll<T, S>(2, 1, 8, 2);
-  static constexpr uint32_t kStreamLdsPre = kStreamLds;
-  static constexpr int kStreamUnrollPre = kStreamUnroll;
+  static constexpr uint32_t kStreamLdsPre = residency_lds<T, S>(20);
+  static constexpr int kStreamUnrollPre = stream_unroll<T, S>(1, 1, 8, 2);
+  static constexpr int kStreamUnrollSmall = stream_unroll<T, S>(2, 1, 8, 2);
+  static constexpr int64_t kStreamSmallBytes = kMallBytes;
   static constexpr int kSegmentUnroll = 2;
+  static constexpr uint32_t kSegmentLds = 0;
   static constexpr bool kLateStores = false;
   static constexpr int kPreWords = 1;
   struct Rep {
@@ -447,9 +501,12 @@ struct AdagradF32Policy {
   static constexpr int NS = 1;
   static constexpr uint32_t kStreamLds = residency_lds<T, S>(16);
   static constexpr int kStreamUnroll = stream_unroll<T, S>(2, 1, 4, 2);
-  static constexpr uint32_t kStreamLdsPre = kStreamLds;
-  static constexpr int kStreamUnrollPre = kStreamUnroll;
+  static constexpr uint32_t kStreamLdsPre = residency_lds<T, S>(20);
+  static constexpr int kStreamUnrollPre = stream_unroll<T, S>(1, 1, 4, 2);
+  static constexpr int kStreamUnrollSmall = stream_unroll<T, S>(2, 1, 4, 2);
+  static constexpr int64_t kStreamSmallBytes = kMallBytes;
   static constexpr int kSegmentUnroll = 2;
+  static constexpr uint32_t kSegmentLds = 0;
   static constexpr bool kLateStores = false;
   static constexpr int kPreWords = 1;
   struct Rep {
@@ -485,20 +542,28 @@ constexpr int state_slots() {
 
 // Packs per thread and residency reservation of the streaming driver, with
 // the per-replica constants read from a workspace (PRE) or derived in every
-// workgroup.
-template <typename P, bool PRE>
+// workgroup, for large launches and for SMALL ones (operands that fit the
+// MALL: plain accesses, no cap).
+template <typename P, bool PRE, bool SMALL>
 constexpr int stream_unroll_of() {
-  return PRE ? P::kStreamUnrollPre : P::kStreamUnroll;
+  return SMALL ? P::kStreamUnrollSmall : PRE ? P::kStreamUnrollPre : P::kStreamUnroll;
 }
-template <typename P, bool PRE>
+template <typename P, bool PRE, bool SMALL>
 constexpr uint32_t stream_lds_of() {
-  return PRE ? P::kStreamLdsPre : P::kStreamLds;
+  return SMALL ? 0u : PRE ? P::kStreamLdsPre : P::kStreamLds;
 }
 
 // Elements per streaming tile: one wavefront x the policy's packs per thread.
-template <typename P, bool PRE>
+template <typename P, bool PRE, bool SMALL>
 constexpr int64_t stream_tile() {
-  return int64_t(kStreamThreads) * kPack * stream_unroll_of<P, PRE>();
+  return int64_t(kStreamThreads) * kPack * stream_unroll_of<P, PRE, SMALL>();
+}
+
+// Bytes of (R, T) operands a launch reads (all rows): params and grads in
+// the parameter type, the state buffers in the state type.
+template <typename P>
+constexpr int64_t operand_bytes_per_elem() {
+  return 2 * int64_t(sizeof(typename P::T)) + P::NS * int64_t(sizeof(typename P::S));
 }
 
 // Elements per segmented-driver tile (128 threads). Measured per policy at the
@@ -560,14 +625,17 @@ __device__ __forceinline__ typename P::S* state_row(const Operands<typename P::T
 // PRE: the per-replica constants come from the call's workspace (a.vec.pre).
 // A thread's loads are issued before the replica's prologue, which then runs
 // while they are in flight.
-template <typename P, bool ANY, bool PRE>
+// SMALL: the launch's operands fit the MALL; plain accesses and the small-launch
+// tile instead of non-temporal ones.
+template <typename P, bool ANY, bool PRE, bool SMALL>
 __global__ __launch_bounds__(kStreamThreads) void stream_kernel(KArgs<P> a) {
   using T = typename P::T;
   using S = typename P::S;
   constexpr int NS = P::NS;
   constexpr int SS = state_slots<P>();
-  constexpr int U = stream_unroll_of<P, PRE>();
-  constexpr int64_t kStreamTile = stream_tile<P, PRE>();
+  constexpr bool NT = !SMALL;
+  constexpr int U = stream_unroll_of<P, PRE, SMALL>();
+  constexpr int64_t kStreamTile = stream_tile<P, PRE, SMALL>();
   uint32_t r;
   int64_t t0;
   tile_of_block<kStreamTile>(a.g, r, t0);
@@ -589,10 +657,10 @@ __global__ __launch_bounds__(kStreamThreads) void stream_kernel(KArgs<P> a) {
   // The parameters' packs are 16-byte aligned by construction; with ANY the
   // other operands sit at another 16-byte phase and use element-aligned packs.
   Pack<T>* prow = reinterpret_cast<Pack<T>*>(pbase + head) + t0 / kPack;
-  const Packs<ANY, T> grow(const_cast<T*>(gbase) + head + t0);
-  Packs<ANY, S> srow[SS];
+  const Packs<ANY, T, NT> grow(const_cast<T*>(gbase) + head + t0);
+  Packs<ANY, S, NT> srow[SS];
 #pragma unroll
-  for (int b = 0; b < NS; ++b) srow[b] = Packs<ANY, S>(sbase[b] + head + t0);
+  for (int b = 0; b < NS; ++b) srow[b] = Packs<ANY, S, NT>(sbase[b] + head + t0);
   const int64_t packs_left = packs_row - t0 / kPack;
 
   Pack<T> vp[U], vg[U];
@@ -601,7 +669,7 @@ __global__ __launch_bounds__(kStreamThreads) void stream_kernel(KArgs<P> a) {
   for (int u = 0; u < U; ++u) {
     const int64_t i = int64_t(u) * kStreamThreads + threadIdx.x;
     if (i < packs_left) {
-      vp[u] = load_stream(prow + i);
+      vp[u] = load_stream<NT>(prow + i);
       vg[u] = grow.load(i);
       if (load_state) {
 #pragma unroll
@@ -614,7 +682,7 @@ __global__ __launch_bounds__(kStreamThreads) void stream_kernel(KArgs<P> a) {
   typename P::Rep rep;
   P::template prologue<PRE>(a.vec, r, rep);
   const auto store_packs = [&](int u, int64_t i) {
-    store_stream(prow + i, vp[u]);
+    store_stream<NT>(prow + i, vp[u]);
 #pragma unroll
     for (int b = 0; b < NS; ++b) {
       srow[b].store(i, vs[b][u]);
@@ -1419,12 +1487,12 @@ bool walk_fits(SegmentWalk w, int64_t R, int64_t tile, bool vec_rows, Segments<T
 // Launches `kernel` once per chunk of the walk.
 template <typename T, typename Args, typename Kernel>
 int launch_walk(SegmentWalk w, int64_t R, int64_t tile, bool vec_rows, Args& a, Segments<T>& seg,
-                Kernel kernel, hipStream_t stream) {
+                Kernel kernel, hipStream_t stream, uint32_t lds = 0) {
   int64_t blocks;
   while ((blocks = next_chunk<T>(w, R, tile, vec_rows, seg)) != 0 || seg.n > 0) {
     if (blocks < 0) return kInvalid;
     if (blocks == 0) continue;
-    hipLaunchKernelGGL(kernel, dim3(static_cast<uint32_t>(blocks)), dim3(kThreads), 0, stream,
+    hipLaunchKernelGGL(kernel, dim3(static_cast<uint32_t>(blocks)), dim3(kThreads), lds, stream,
                        a);
     const int err = static_cast<int>(hipGetLastError());
     if (err != 0) return err;
@@ -1525,16 +1593,17 @@ int run_step(const Call& c, const Vectors<typename P::T>& vec, Prepare&& prepare
 }
 
 // The streaming driver over `blocks` tiles, capped when the launch is large.
-template <typename P, bool PRE>
+template <typename P, bool PRE, bool SMALL>
 void launch_stream(const KArgs<P>& a, uint32_t blocks, bool same_phase, hipStream_t stream) {
-  const uint32_t lds =
-      int64_t(blocks) * stream_tile<P, PRE>() >= kCapMinElems ? stream_lds_of<P, PRE>() : 0u;
+  const uint32_t lds = int64_t(blocks) * stream_tile<P, PRE, SMALL>() >= kCapMinElems
+                           ? stream_lds_of<P, PRE, SMALL>()
+                           : 0u;
   if (same_phase) {
-    hipLaunchKernelGGL((stream_kernel<P, false, PRE>), dim3(blocks), dim3(kStreamThreads), lds,
-                       stream, a);
+    hipLaunchKernelGGL((stream_kernel<P, false, PRE, SMALL>), dim3(blocks), dim3(kStreamThreads),
+                       lds, stream, a);
   } else {
-    hipLaunchKernelGGL((stream_kernel<P, true, PRE>), dim3(blocks), dim3(kStreamThreads), lds,
-                       stream, a);
+    hipLaunchKernelGGL((stream_kernel<P, true, PRE, SMALL>), dim3(blocks), dim3(kStreamThreads),
+                       lds, stream, a);
   }
 }
 
@@ -1545,12 +1614,20 @@ int launch_dense(const Call& c, int nbufs) {
   uint32_t blocks = 0;
   bool streamable = false;
   const bool pre = uses_workspace<P>(c);
+  // Operands that fit the MALL (R, T and the types say so, before any launch).
+  // The small shape is built for the forms the operators run: with a
+  // workspace where the policy has one, and for SGD, which has none.
+  const bool small =
+      (pre || P::kPreWords == 0) &&
+      c.R <= P::kStreamSmallBytes / operand_bytes_per_elem<P>() / std::max<int64_t>(c.T, 1);
   const auto prepare = [&] {
     if (!fill_kargs<P>(c, nbufs, a, false)) return false;
     uint32_t res0 = 0, rmod = 0;
     streamable = rows_streamable<P>(a.x, nbufs, res0, rmod);
-    const int64_t tile =
-        !streamable ? kTile : pre ? stream_tile<P, true>() : stream_tile<P, false>();
+    const int64_t tile = !streamable ? kTile
+                         : small     ? stream_tile<P, false, true>()
+                         : pre       ? stream_tile<P, true, false>()
+                                     : stream_tile<P, false, false>();
     if (!make_grid(c.R, c.T, tile, a.g, blocks)) return false;
     a.g.res0 = res0;
     a.g.rmod = rmod;
@@ -1564,11 +1641,21 @@ int launch_dense(const Call& c, int nbufs) {
       const bool same_phase = rows_same_phase<P>(a.x, nbufs);
       if constexpr (P::kPreWords > 0) {
         if (pre) {
-          launch_stream<P, true>(a, blocks, same_phase, c.stream);
+          if (small) {
+            launch_stream<P, true, true>(a, blocks, same_phase, c.stream);
+          } else {
+            launch_stream<P, true, false>(a, blocks, same_phase, c.stream);
+          }
           return static_cast<int>(hipGetLastError());
         }
       }
-      launch_stream<P, false>(a, blocks, same_phase, c.stream);
+      if constexpr (P::kPreWords == 0) {
+        if (small) {
+          launch_stream<P, false, true>(a, blocks, same_phase, c.stream);
+          return static_cast<int>(hipGetLastError());
+        }
+      }
+      launch_stream<P, false, false>(a, blocks, same_phase, c.stream);
     } else if (replica_minor(a.x, nbufs) && make_col_grid(c.R, c.T, ca.g, col_blocks)) {
       ca.x = a.x;
       ca.vec = a.vec;
@@ -1608,12 +1695,15 @@ int launch_segments(const Call& c, int nbufs, const ts_segment* segs, int n_segs
   };
   return run_step<P>(c, a.k.vec, prepare, [&]() -> int {
     const bool same_phase = rows_same_phase<P>(a.k.x, nbufs);
+    // with precomputed constants, large launches take the policy's residency
+    // reservation (kSegmentLds)
+    const uint32_t lds = c.R * c.T >= kCapMinElems ? P::kSegmentLds : 0u;
     if constexpr (P::kPreWords > 0) {
       if (uses_workspace<P>(c)) {
         return same_phase ? launch_walk<T>(walk, c.R, segment_tile<P>(), vec_rows, a, a.seg,
-                                           segment_kernel<P, false, true>, c.stream)
+                                           segment_kernel<P, false, true>, c.stream, lds)
                           : launch_walk<T>(walk, c.R, segment_tile<P>(), vec_rows, a, a.seg,
-                                           segment_kernel<P, true, true>, c.stream);
+                                           segment_kernel<P, true, true>, c.stream, lds);
       }
     }
     return same_phase ? launch_walk<T>(walk, c.R, segment_tile<P>(), vec_rows, a, a.seg,
@@ -1638,13 +1728,16 @@ int adam_dispatch(uint32_t flags, Launch&& launch) {
 }
 
 template <typename T, typename S, typename Launch>
-int sgd_dispatch(uint32_t flags, bool has_buf, Launch&& launch) {
+int sgd_dispatch(uint32_t flags, bool has_buf, bool work, Launch&& launch) {
   const bool nesterov = (flags & TS_NESTEROV) != 0;
   if (has_buf) {
     if (nesterov) return launch(SgdPolicy<T, true, true, S>{}, 3);
     return launch(SgdPolicy<T, true, false, S>{}, 3);
   }
-  if (nesterov) return kInvalid;
+  // Nesterov needs momentum buffers -- when there is an element to update: an
+  // empty (R, T) buffer may come with a NULL data pointer, and a call with R
+  // or T of 0 only bumps the steps, as the reference's does.
+  if (nesterov && work) return kInvalid;
   return launch(SgdPolicy<T, false, false, S>{}, 2);
 }
 
@@ -1709,9 +1802,10 @@ template <typename T>
 struct SgdBody {
   static int run(const Call& c, const ts_segment* segs, int n_segs, bool segmented) {
     const bool has_buf = c.bufs != nullptr && c.bufs[2].data != nullptr;
+    const bool work = c.R > 0 && c.T > 0;
     return with_state_type<T>(c.flags, [&](auto state) {
       using S = typename decltype(state)::type;
-      return sgd_dispatch<T, S>(c.flags, has_buf, [&](auto policy, int nbufs) {
+      return sgd_dispatch<T, S>(c.flags, has_buf, work, [&](auto policy, int nbufs) {
         return launch_any<decltype(policy)>(c, nbufs, segs, n_segs, segmented);
       });
     });
