@@ -210,6 +210,23 @@ int ts_adagrad_step_segments_ws(const ts_rt_buf* bufs, const ts_segment* grads, 
                                 int64_t T, uint32_t flags, void* out_zero, void* workspace,
                                 size_t workspace_bytes, void* stream);
 
+/* ts_adam_step_ws without a workspace argument, allocating nothing: the
+ * per-replica constants go to a scratch array inside the library (1 MiB per
+ * device, held until the process ends; its device address is looked up on the
+ * first call on each device). No counterpart in the reference: it is for
+ * callers that cannot allocate device memory at call time -- code under HIP
+ * graph capture, tight serving loops, harnesses that forbid allocation.
+ * Limits: R <= 65536 (larger R is hipErrorInvalidValue, before anything is
+ * enqueued). Every call on one device shares that device's scratch: calls that
+ * can overlap on one GPU (several streams, several threads) race and must be
+ * serialised by the caller. Nothing in the scratch needs to start at zero:
+ * each call writes every active replica's constants before its update reads
+ * them. Results are bit-identical to ts_adam_step_ws. */
+int ts_adam_step_noalloc(const ts_rt_buf* bufs, ts_dtype dtype, void* state_steps,
+                         const void* lr, const void* beta1, const void* beta2, const void* eps,
+                         const void* weight_decay, const uint8_t* active_mask, int64_t R,
+                         int64_t T, uint32_t flags, void* out_zero, void* stream);
+
 /* Gradient scatter in one launch per 64 segments: copies every segment, all R
  * rows, into its columns of the (R, cols) buffer dst (row stride dst_stride_r,
  * unit column stride); other columns are not written. Replaces the

@@ -50,7 +50,8 @@ def test_header_declares_the_entry_points():
         ["ts_adagrad_step", "ts_adam_step", "ts_bump_steps", "ts_sgd_step", "ts_version",
          "ts_adam_step_segments", "ts_sgd_step_segments", "ts_adagrad_step_segments",
          "ts_scatter_segments", "ts_copy_rows", "ts_workspace_bytes", "ts_adam_step_ws",
-         "ts_adagrad_step_ws", "ts_adam_step_segments_ws", "ts_adagrad_step_segments_ws"])
+         "ts_adagrad_step_ws", "ts_adam_step_segments_ws", "ts_adagrad_step_segments_ws",
+         "ts_adam_step_noalloc"])
 
 
 def test_library_exports_every_declared_symbol():
@@ -104,6 +105,9 @@ def test_workspace_size_and_bad_workspaces_rejected_before_any_launch():
         assert lib.ts_adagrad_step_segments_ws(bufs, seg, 1, 0, fake, fake, fake, fake, fake,
                                                fake, R, T, flags, None, ws, sz(nbytes),
                                                None) == 1
+    # the allocation-free form holds at most 65536 replicas' constants
+    assert lib.ts_adam_step_noalloc(bufs, 0, fake, fake, fake, fake, fake, fake, fake,
+                                    ctypes.c_int64(65537), T, flags, None, None) == 1
 
 
 class Segment(ctypes.Structure):
