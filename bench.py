@@ -146,6 +146,7 @@ def make_config(cfg: int, device="cuda", seed=None, N=None):
 # CPU baseline: the reference's CPU kernel (oracle/_ref), in a child process
 # ---------------------------------------------------------------------------
 CPU_SAMPLE_N = 8
+CPU_SHARE = 16
 
 
 def cpu_worker(cfg: int, steps: int, seconds: float = 10.0) -> None:
@@ -157,7 +158,10 @@ def cpu_worker(cfg: int, steps: int, seconds: float = 10.0) -> None:
         return
     import torch
 
-    threads = min(16, len(os.sched_getaffinity(0)))
+    # The GPU box gives one GPU's job a share of 16 host CPUs (its thread and
+    # job-size limits are set to 16), whatever the machine has; the baseline
+    # uses that whole share, or the affinity set if smaller.
+    threads = min(CPU_SHARE, len(os.sched_getaffinity(0)))
     torch.set_num_threads(threads)
     ref = ROOT / "oracle" / "_ref" / "torchstrap_ref_C.so"
     kind = "reference"
@@ -184,6 +188,7 @@ def cpu_worker(cfg: int, steps: int, seconds: float = 10.0) -> None:
     dt = (time.perf_counter() - t0) / steps
     print(json.dumps({"value": round(nbytes / dt / 1e9, 3), "unit": "GB/s",
                       "cores": threads, "kind": kind, "us_per_step": round(dt * 1e6, 1),
+                      "host": cpu_info(threads),
                       "sample": f"config {cfg} at N={CPU_SAMPLE_N} of {CONFIGS[cfg]['N']} "
                                 f"replicas (same T, same per-replica hyperparameters), "
                                 f"{steps} steps after 1 warm-up, effective bytes "
@@ -289,23 +294,46 @@ def kernel_only_timing(op_name, args, kw, launches: int, extra_flags: int = 0,
     return e0.elapsed_time(e1) / launches
 
 
-def loop_baseline(cfg: int, steps: int, fused: bool):
-    """N independent torch.optim.Adam instances stepped in a Python loop
-    (the reference's 'vanilla' baseline, bench_inplace_adam.py:66-96)."""
+def loop_baseline(cfg: int, steps: int, fused: bool, hyper):
+    """N independent torch.optim optimizers stepped in a Python loop on the
+    same GPU (the reference's 'vanilla' baselines: bench_inplace_adam.py:66-96,
+    bench_sgd.py:83-102, bench_adagrad.py:96-115), like for like with the
+    fused step: the config's optimizer and flags, each replica with its own
+    hyperparameters (`hyper`: the op's (N,) vectors on the host), and only the
+    active replicas stepped (the fused op skips frozen ones). Returns ms per
+    step of the whole loop."""
     import torch
 
     c = CONFIGS[cfg]
-    N = c["N"]
     dev = torch.device("cuda")
     g = torch.Generator(device=dev).manual_seed(7)
+    mask = hyper["mask"]
+    active = [r for r in range(len(mask)) if bool(mask[r])]
     opts, params = [], []
-    for _ in range(N):
+    for r in active:
         ps = [torch.randn(*s, device=dev, generator=g).mul_(0.02).requires_grad_()
               for s in c["layout"]]
         for t in ps:
             t.grad = torch.randn(t.shape, device=dev, generator=g).mul_(1e-3)
         params.append(ps)
-        opts.append(torch.optim.Adam(ps, lr=1e-3, fused=fused, foreach=None if fused else True))
+        h = {k: float(v[r]) for k, v in hyper.items() if k != "mask"}
+        impl = dict(fused=True) if fused else dict(foreach=True)
+        if c["op"] == "adam":
+            cls = torch.optim.AdamW if c["decoupled"] else torch.optim.Adam
+            opts.append(cls(ps, lr=h["lr"], betas=(h["beta1"], h["beta2"]), eps=h["eps"],
+                            weight_decay=h["weight_decay"], amsgrad=c["amsgrad"], **impl))
+        elif c["op"] == "sgd":
+            # torch.optim.SGD rejects nesterov with dampening != 0: nesterov
+            # replicas run with dampening 0, momentum-0 replicas as plain SGD
+            nest = h["momentum"] > 0
+            opts.append(torch.optim.SGD(ps, lr=h["lr"], momentum=h["momentum"],
+                                        dampening=0.0 if nest else h["dampening"],
+                                        nesterov=nest, weight_decay=h["weight_decay"],
+                                        **impl))
+        else:
+            opts.append(torch.optim.Adagrad(ps, lr=h["lr"], lr_decay=h["lr_decay"],
+                                            weight_decay=h["weight_decay"], eps=h["eps"],
+                                            initial_accumulator_value=0.1, **impl))
     for o in opts:
         o.step()
     torch.cuda.synchronize()
@@ -318,6 +346,54 @@ def loop_baseline(cfg: int, steps: int, fused: bool):
     del opts, params
     torch.cuda.empty_cache()
     return dt * 1e3
+
+
+HYPER_NAMES = {"adam": ("lr", "beta1", "beta2", "eps", "weight_decay"),
+               "sgd": ("lr", "momentum", "dampening", "weight_decay"),
+               "adagrad": ("lr", "lr_decay", "weight_decay", "eps")}
+
+
+def host_hypers(op_name, args):
+    """The op's (N,) hyperparameter vectors and mask, on the host."""
+    first = 6 if op_name == "adam" else 4
+    names = HYPER_NAMES[op_name]
+    out = {k: args[first + i].cpu() for i, k in enumerate(names)}
+    out["mask"] = args[first + len(names)].cpu()
+    return out
+
+
+def cpu_info(threads: int):
+    """The host the CPU baseline ran on: logical CPUs, the affinity set,
+    physical cores, the vector ISA torch detects and the one the timed kernel
+    is built for."""
+    import torch
+
+    phys, model, flags = set(), "", set()
+    try:
+        cur = {}
+        for line in Path("/proc/cpuinfo").read_text().splitlines():
+            k, _, v = line.partition(":")
+            k, v = k.strip(), v.strip()
+            if k == "physical id":
+                cur["p"] = v
+            elif k == "core id":
+                cur["c"] = v
+            elif k == "model name" and not model:
+                model = v
+            elif k == "flags" and not flags:
+                flags = set(v.split())
+            elif not line.strip() and cur:
+                phys.add((cur.get("p"), cur.get("c")))
+                cur = {}
+        if cur:
+            phys.add((cur.get("p"), cur.get("c")))
+    except OSError:
+        pass
+    isa = [f for f in ("avx2", "fma", "f16c", "avx512f", "avx512_bf16", "amx_tile") if f in flags]
+    return {"os_cpu_count": os.cpu_count(), "affinity": len(os.sched_getaffinity(0)),
+            "physical_cores": len(phys) or None, "threads": threads, "model": model,
+            "isa_flags": isa, "torch_cpu_capability": torch.backends.cpu.get_cpu_capability(),
+            "kernel_isa": "AVX2/FMA/F16C (the reference's setup.py:49-60 flags)"}
 
 
 def grad_scatter_timing(cfg: int, steps: int):
@@ -490,20 +566,25 @@ def low_precision_timing(launches: int):
     """Adam with float16 and with bfloat16 parameters (state in the parameter
     dtype, as torch keeps it) at the config-5 shape and mask: kernel-only time
     and effective GB/s of 14 B per active element. The buffers are the config's
-    float32 values narrowed, one dtype at a time."""
+    float32 values narrowed, one dtype at a time; for float16 eps is 1e-4 (the
+    config's 1e-8 is 0 in half precision, which turns lanes with a zero
+    exp_avg_sq into NaN)."""
     import torch
 
     out = {}
     for name, dt, code in (("f16", torch.float16, 2), ("bf16", torch.bfloat16, 3)):
         op_name, args, kw, nbytes = make_config(5)
         args = [t.to(dt) if t is not None and t.is_floating_point() else t for t in args]
+        if dt == torch.float16:
+            args[9].fill_(1e-4)  # eps
         T = args[0].shape[1]
         active = int(args[-1].sum().item())
         nb = active * T * 14
         ms = kernel_only_timing(op_name, tuple(args), kw, launches, dtype_code=code)
         gbs = nb / (ms * 1e-3) / 1e9
         out[name] = {"kernel_avg_ms": round(ms, 4), "bytes_per_elem": 14,
-                     "achieved_GBs": round(gbs, 1), "frac": round(gbs / HBM_PEAK_GBS, 4)}
+                     "achieved_GBs": round(gbs, 1), "frac": round(gbs / HBM_PEAK_GBS, 4),
+                     "eps": float(args[9][0])}
         del args
         torch.cuda.empty_cache()
     return out
@@ -777,6 +858,7 @@ def main():
               "adagrad": "AdagradPolicy<float>"}[op_name]
     kernel = f"stream_kernel<{policy}>"
     profile_key = f"{op_name}_stream_kernel_cfg{args.config}"
+    hypers = host_hypers(op_name, op_args)
     del op_args
     torch.cuda.empty_cache()
 
@@ -797,9 +879,10 @@ def main():
         scatter = grad_scatter_timing(args.config, max(5, args.steps // 2))
 
     loop = {}
-    if not args.no_loop_baseline and op_name == "adam":
-        loop["fused_ms"] = round(loop_baseline(args.config, 3, fused=True), 3)
-        loop["foreach_ms"] = round(loop_baseline(args.config, 3, fused=False), 3)
+    if not args.no_loop_baseline:
+        if op_name != "adagrad":  # torch.optim.Adagrad(fused=True) rejects GPU tensors
+            loop["fused_ms"] = round(loop_baseline(args.config, 3, True, hypers), 3)
+        loop["foreach_ms"] = round(loop_baseline(args.config, 3, False, hypers), 3)
 
     cpu = None if cpu_proc is None else cpu_baseline_finish(cpu_proc)
 
@@ -850,6 +933,10 @@ def main():
         "graph_replay": graphed,
         "speedup_vs_python_loop": ({k: round(v / step_ms, 2) for k, v in loop.items()}
                                    if loop else None),
+        "python_loop_note": ("torch.optim per replica, own hyperparameters, active replicas "
+                             "only" + ("; nesterov replicas with dampening 0 (torch.optim.SGD "
+                                       "rejects nesterov with dampening)"
+                                       if op_name == "sgd" else "")) if loop else None,
     }
     print(json.dumps(out), flush=True)
 

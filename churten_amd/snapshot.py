@@ -34,6 +34,7 @@ from __future__ import annotations
 import ctypes
 import json
 import shutil
+from contextlib import suppress
 from pathlib import Path
 from typing import Any, Callable
 
@@ -270,10 +271,27 @@ class Checkpoint:
             self._snapshot.to_file(self.root_dir, self.fn_prefix + self.f_state)
             if history is not None:
                 history.to_file(self.root_dir / (self.fn_prefix + self.f_history))
-            if self.verbose:
-                self.sink(f"Checkpoint saved ({int(improved.sum())} replica(s) improved).")
+            self._sink(f"Checkpoint saved ({int(improved.sum())} replica(s) improved).")
         return improved
 
-    def load_best(self, state: State) -> None:
-        """Restore every row of the saved checkpoint into the live state."""
-        Snapshot.from_file(self.root_dir, self.fn_prefix + self.f_state).restore_to_live(state)
+    @torch.no_grad()
+    def load_best(self, state: State, history=None) -> None:
+        """Restore every row of the saved checkpoint into the live state, and
+        the saved history into ``history`` when one is given (an object with
+        the reference History's ``from_file`` / ``clear`` / ``update``). A
+        checkpoint or history that was never written is not an error: nothing
+        is restored (training.py:203-214)."""
+        with suppress(FileNotFoundError):
+            snap = Snapshot.from_file(self.root_dir, self.fn_prefix + self.f_state)
+            snap.restore_to_live(state)
+            self._sink("Loaded best checkpoint.")
+        if history is not None:
+            with suppress(FileNotFoundError):
+                loaded = type(history).from_file(self.root_dir / (self.fn_prefix + self.f_history))
+                history.clear()
+                history.update(loaded)
+
+    def _sink(self, text: str) -> None:
+        # a custom sink always receives the message; print only when verbose
+        if self.sink is not print or self.verbose:
+            self.sink(text)

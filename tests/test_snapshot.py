@@ -12,6 +12,7 @@ identically. The GPU cases also cover the row-transfer entry point directly
 from __future__ import annotations
 
 import ctypes
+import json
 from copy import deepcopy
 from pathlib import Path
 
@@ -141,6 +142,43 @@ def test_checkpoint_keeps_per_replica_best(device, tmp_path):
     want = first.clone()
     want[[0, 3]] += 1.0
     assert torch.equal(state.params.cpu(), want)
+
+
+class _History(dict):
+    """A stand-in with the reference History's file interface (history.py)."""
+
+    def to_file(self, path):
+        Path(path).write_text(json.dumps(self))
+
+    @classmethod
+    def from_file(cls, path):
+        return cls(json.loads(Path(path).read_text()))
+
+
+@pytest.mark.parametrize("device", DEVICES)
+def test_load_best_without_checkpoint_restores_nothing(device, tmp_path):
+    """As training.py:203-214: a checkpoint (or history) that was never
+    written is not an error; the live state and the history stay as they are."""
+    state = trained_state(device)
+    before = state.params.clone()
+    msgs = []
+    ckpt = Checkpoint(root_dir=tmp_path / "never_written", sink=msgs.append)
+    hist = _History(loss=[1.0])
+    ckpt.load_best(state)
+    ckpt.load_best(state, hist)
+    assert torch.equal(state.params, before) and hist == {"loss": [1.0]} and msgs == []
+
+
+@pytest.mark.parametrize("device", DEVICES)
+def test_load_best_restores_the_saved_history(device, tmp_path):
+    state = trained_state(device)
+    msgs = []
+    ckpt = Checkpoint(root_dir=tmp_path, sink=msgs.append)
+    ckpt(state, torch.tensor([1.0, 2.0, 3.0, 4.0]), history=_History(loss=[0.5, 0.25]))
+    live = _History(loss=[9.0], extra=[1])
+    ckpt.load_best(state, live)
+    assert live == {"loss": [0.5, 0.25]}
+    assert msgs[-1] == "Loaded best checkpoint."
 
 
 @pytest.mark.gpu
