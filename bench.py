@@ -851,12 +851,17 @@ def main():
                                     extra_flags=TS_ADAGRAD_F32)
         adagrad_f32 = {"kernel_avg_ms": round(f32_ms, 4),
                        "GBs": round(nbytes / (f32_ms * 1e-3) / 1e9, 1)}
-    policy = {"adam": "AdamPolicy<float, %s, %s>" % (str(kw.get("decoupled_weight_decay")).lower(),
-                                                     str(kw.get("amsgrad")).lower()),
-              "sgd": "SgdPolicy<float, %s, %s>" % ("true" if op_args[2] is not None else "false",
-                                                   str(kw.get("nesterov")).lower()),
-              "adagrad": "AdagradPolicy<float>"}[op_name]
-    kernel = f"stream_kernel<{policy}>"
+    policy = {"adam": "AdamPolicy<float, %s, %s, float>" % (
+                  str(kw.get("decoupled_weight_decay")).lower(), str(kw.get("amsgrad")).lower()),
+              "sgd": "SgdPolicy<float, %s, %s, float>" % (
+                  "true" if op_args[2] is not None else "false", str(kw.get("nesterov")).lower()),
+              "adagrad": "AdagradPolicy<float, float>"}[op_name]
+    # the instantiation the operator launches: ANY = false (State's layout), PRE (per-replica
+    # constants from the workspace: Adam and Adagrad), SMALL (operands that fit the 256 MB MALL)
+    n_rt = sum(t is not None and t.dim() == 2 for t in op_args)
+    small = op_args[0].numel() * 4 * n_rt <= 256 << 20
+    kernel = "stream_kernel<%s, false, %s, %s>" % (policy, str(op_name != "sgd").lower(),
+                                                  str(small).lower())
     profile_key = f"{op_name}_stream_kernel_cfg{args.config}"
     hypers = host_hypers(op_name, op_args)
     del op_args
