@@ -1,1718 +1,19 @@
-// optim_kernels.hip -- gfx950 kernels and the extern "C" launchers of
-// include/churten_optim.h.
-//
-// Structure. Each optimizer is a policy (AdamPolicy, SgdPolicy, AdagradPolicy,
-// AdagradF32Policy): its per-replica prologue (hyperparameters, bias
-// corrections, is_first_step, corrected_lr) and its per-element update, both
-// from optim_math.h, over a parameter type T and an optimizer-state type S
-// (S = T, or bfloat16 state next to float32 parameters). Four drivers move the
-// bytes, identically for every policy:
-//
-//   stream_kernel   unit inner stride (the consolidated layout `State`
-//                   produces, and ragged or misaligned rows): one wavefront
-//                   per tile (1-8 packs per thread by operand types),
-//                   non-temporal 16-byte loads and stores from each row's
-//                   first 256-byte boundary (tiles never share a cache line),
-//                   the few head and tail elements of a row one at a time;
-//                   large launches cap residency per CU. Operands at another
-//                   16-byte phase than the parameters take element-aligned
-//                   packs (the ANY variant).
-//   column_kernel   unit replica stride on every operand (transposed views,
-//                   as an outer vmap over a non-leading dimension gives): each
-//                   thread keeps one replica and walks columns, so the threads
-//                   of a workgroup read consecutive replicas -- contiguous
-//                   memory. Non-temporal where workgroups own their cache
-//                   lines and a wavefront has no frozen replica; the replica
-//                   blocks of a column block share an XCD when there are
-//                   several.
-//   element_kernel  any other inner strides: one element per access.
-//   segment_kernel  the gradient arrives as one tensor per parameter (a segment
-//                   table) instead of the consolidated (R, T) gradient buffer:
-//                   the gradient scatter of the training step is fused into the
-//                   update. Optionally the consolidated gradient is written on
-//                   the way through, so `flat_grads` stays what it would have
-//                   been. Same access pattern as stream_kernel over each
-//                   segment's columns, whatever the segment's offset.
-//
-// Operands are ordered [0] param, [1] grad (both T), [2..] optimizer state (S;
-// Adam: exp_avg, exp_avg_sq, [max_exp_avg_sq]; SGD: [momentum_buffer];
-// Adagrad: state_sum). The dense drivers never write the grad; the segmented
-// driver may store the gradient it read into the consolidated buffer.
-//
-// Work decomposition. Rows are cut into tiles of consecutive elements
-// (segments into tiles of their own); a 1-D grid enumerates (replica, tile)
-// pairs replica-major, so blockIdx.x gives both and no grid dimension caps R.
-// A workgroup first reads its replica's active flag: a frozen replica is a
-// workgroup-uniform early exit, so its rows are never read or written (they stay
-// bit-identical, and a replica frozen at step 0 never evaluates 1 - beta^0 = 0).
-// Active workgroups read the replica's hyperparameters once (uniform address:
-// scalar loads) and derive the per-replica constants, then stream their tile.
-// All drivers inline the same per-element update, so the same element gives
-// the same bits whichever driver processed it.
-//
-// (column_kernel instead enumerates (column block, replica block) pairs, in
-// an XCD-aware order when a column has several replica blocks, and tests the
-// flag per thread.)
-//
-// Everything is enqueued on the caller's stream; nothing is allocated.
+// optim_kernels.hip -- the extern "C" entry points of include/churten_optim.h:
+// the dispatch of each call onto the policy its flags and dtype select (the
+// kernels, their launch shapes and the argument checks are in
+// optim_drivers.h), and the allocation-free form's device scratch.
 
 #include <hip/hip_runtime.h>
 
 #include <stdint.h>
 
-#include <algorithm>
-#include <initializer_list>
 #include <mutex>
-#include <type_traits>
 
 #include "../../include/churten_optim.h"
-#include "optim_math.h"
+#include "optim_drivers.h"
 
 namespace churten {
 namespace {
-
-// Launch shape, measured on the MI355X over the 52 GB north-star state: 2
-// packs of 4 elements per thread with non-temporal vector loads and stores
-// (non-temporal hints on both loads and stores were worth ~10% over plain
-// accesses, either alone nothing). The streaming driver runs one wavefront per
-// workgroup under a residency cap (below; 512-element tiles for float32): of
-// 64/128/256 threads x 1/2/4 packs x 8-24 resident waves per CU, that was
-// fastest, ahead of 128 x 2 with its best cap by 2-6% and uncapped 128 x 2 by
-// 6-10%. The other drivers keep 128 threads (1024-element tiles for float32),
-// where their own sweeps put them; packs per thread follow the policy.
-constexpr int kThreads = 128;
-constexpr int kPack = 4;
-constexpr int kUnroll = 2;
-constexpr int kPer = kPack * kUnroll;  // elements per thread per tile
-constexpr int64_t kTile = int64_t(kThreads) * kPer;
-constexpr int kStreamThreads = 64;
-
-// Tile boundaries sit on 256-byte boundaries of the (R, T) rows. Consecutive
-// tiles run on different XCDs (each with its own L2); a 128-byte line split
-// between two of them is fetched twice and written back as two partial lines.
-// Measured on the MI355X with the same buffers viewed 16 / 64 / 128 / 0 bytes
-// off a 256-byte boundary: the Adam step took 19% / 8% / 1% / 0% longer.
-constexpr uint32_t kAlignBytes = 256;
-template <typename T>
-constexpr uint32_t align_elems() {
-  return kAlignBytes / sizeof(T);
-}
-
-template <typename T>
-struct alignas(sizeof(T) * kPack) Pack {
-  T v[kPack];
-};
-
-// A pack as raw 32-bit words, so it can go through the non-temporal builtins
-// (16 B for fp32, 8 B for 16-bit types, 32 B for fp64).
-template <typename T>
-using PackBits = uint32_t __attribute__((ext_vector_type(sizeof(T) * kPack / 4)));
-
-// Streaming accesses: every byte of the optimizer state is touched exactly
-// once per step, so the loads and stores carry the non-temporal hint (NT).
-// Launches whose operands fit the 256 MB MALL several times over take plain,
-// cache-allocating accesses instead (NT = false): back-to-back steps then hit
-// the MALL (see the streaming driver's launch).
-template <bool NT, typename V>
-__device__ __forceinline__ V load_bits(const V* p) {
-  if constexpr (NT) {
-    return __builtin_nontemporal_load(p);
-  } else {
-    return *p;
-  }
-}
-template <bool NT, typename V>
-__device__ __forceinline__ void store_bits(V* p, V v) {
-  if constexpr (NT) {
-    __builtin_nontemporal_store(v, p);
-  } else {
-    *p = v;
-  }
-}
-
-template <bool NT = true, typename T>
-__device__ __forceinline__ Pack<T> load_stream(const Pack<T>* p) {
-  return __builtin_bit_cast(Pack<T>, load_bits<NT>(reinterpret_cast<const PackBits<T>*>(p)));
-}
-
-template <bool NT = true, typename T>
-__device__ __forceinline__ void store_stream(Pack<T>* p, const Pack<T>& v) {
-  store_bits<NT>(reinterpret_cast<PackBits<T>*>(p), __builtin_bit_cast(PackBits<T>, v));
-}
-
-// Packs at addresses that are only element-aligned: operands whose 16-byte
-// boundaries do not line up with the parameters' (a column view at another
-// offset, a per-parameter gradient's rows). gfx950 code runs in unaligned
-// access mode, and hipcc emits the same single global_load/store_dwordx4
-// (dwordx2 for 16-bit types) for these types as for an aligned pack; on an
-// aligned address the access is the aligned one.
-template <typename T>
-using PackBitsU = uint32_t
-    __attribute__((ext_vector_type(sizeof(T) * kPack / 4), aligned(sizeof(T))));
-
-template <bool NT = true, typename T>
-__device__ __forceinline__ Pack<T> load_stream_any(const T* p) {
-  return __builtin_bit_cast(Pack<T>, load_bits<NT>(reinterpret_cast<const PackBitsU<T>*>(p)));
-}
-
-template <bool NT = true, typename T>
-__device__ __forceinline__ void store_stream_any(T* p, const Pack<T>& v) {
-  store_bits<NT>(reinterpret_cast<PackBitsU<T>*>(p), __builtin_bit_cast(PackBitsU<T>, v));
-}
-
-// The packs of an operand from a given element on: 16-byte aligned wherever
-// the parameters' packs are (ANY = false, the usual case: the compiler knows
-// the alignment) or only element-aligned (ANY = true). Indexed by pack.
-template <bool ANY, typename T, bool NT = true>
-struct Packs;
-
-template <typename T, bool NT>
-struct Packs<false, T, NT> {
-  Pack<T>* p = nullptr;
-  Packs() = default;
-  __device__ explicit Packs(T* e) : p(reinterpret_cast<Pack<T>*>(e)) {}
-  __device__ Pack<T> load(int64_t i) const { return load_stream<NT>(p + i); }
-  __device__ void store(int64_t i, const Pack<T>& v) const { store_stream<NT>(p + i, v); }
-};
-
-template <typename T, bool NT>
-struct Packs<true, T, NT> {
-  T* p = nullptr;
-  Packs() = default;
-  __device__ explicit Packs(T* e) : p(e) {}
-  __device__ Pack<T> load(int64_t i) const { return load_stream_any<NT>(p + i * kPack); }
-  __device__ void store(int64_t i, const Pack<T>& v) const {
-    store_stream_any<NT>(p + i * kPack, v);
-  }
-};
-
-constexpr int kMaxOperands = 5;
-
-// (R, T) operands. `data[i]` is element (0, 0) of operand i.
-template <typename T>
-struct Operands {
-  T* data[kMaxOperands];
-  int64_t stride_r[kMaxOperands];
-  int64_t stride_t[kMaxOperands];
-};
-
-// (R,) inputs: the step counter, up to five hyperparameter vectors and the mask.
-// `pre`: the call's per-replica constants (kPreWords doubles per replica,
-// replica r at pre + kPreStride * r), written by the preparation launch; null
-// when the workgroups derive them themselves.
-template <typename T>
-struct Vectors {
-  const T* steps;
-  const T* h[5];
-  const uint8_t* mask;
-  const double* pre;
-};
-
-// Doubles per replica in a workspace of per-replica constants.
-constexpr int kPreStride = 2;
-
-// Tiles of a driver's tile size per row. For the streaming driver, row r's first
-// 256-byte boundary lies head(r) = (A - (res0 + r * rmod) % A) % A elements in
-// (A: 256 bytes in elements of the parameter type; res0: the parameter base's
-// element offset modulo A, rmod: its row stride modulo A); packs stream from
-// there and the head and the at most three tail elements of each row go one at
-// a time. Every operand shares the parameter's phase modulo 4, so the packs are
-// 16-byte aligned in all of them.
-struct Grid {
-  int64_t T;
-  uint32_t tiles_per_row;
-  uint32_t res0, rmod;
-};
-
-// Integer minimum for tile bounds (a plain compare-and-select; HIP's generic
-// min template goes through double for 64-bit integers).
-__device__ __forceinline__ int64_t imin(int64_t a, int64_t b) { return a < b ? a : b; }
-
-template <int64_t TILE>
-__device__ __forceinline__ void tile_of_block(const Grid& g, uint32_t& r,
-                                              int64_t& t0) {
-  const uint32_t tile = blockIdx.x;
-  r = tile / g.tiles_per_row;
-  t0 = int64_t(tile - r * g.tiles_per_row) * TILE;
-}
-
-template <typename T>
-__device__ __forceinline__ double hyper_at(const T* h, uint32_t r) {
-  return static_cast<double>(widen(h[r]));
-}
-
-// ---------------------------------------------------------------------------
-// Policies
-// ---------------------------------------------------------------------------
-// Residency cap of the streaming driver. A large streaming launch runs faster
-// with fewer one-wave workgroups resident per CU than the register budget
-// allows (24): measured on the MI355X over config-5-sized fp32 state (same
-// buffers, interleaved, several processes), with every workgroup deriving its
-// replica's constants: 14 per CU for Adam, 12 with amsgrad and 16 for
-// Adagrad, +3-10% over no cap; bfloat16 state lost with any cap and fp64
-// gained nothing. With the constants precomputed the caps move (below, next to
-// the policies). The cap is dynamic LDS that the kernel never touches (the
-// smallest 256-byte multiple that fits only n workgroups in the CU's 160 KiB),
-// so it changes residency and nothing else. `kStreamLds` / `kStreamLdsPre` are
-// each policy's reservations; small launches (under kCapMinElems elements of
-// the (R, T) operands, 8192 tiles of 512) launch without them, since there the
-// cap would only serialise the launch (config 1 lost 16% with one). The
-// segmented driver (`kSegmentLds`) runs uncapped when workgroups derive their
-// constants (caps of 6-10 moved it by -3% to +2%); with a workspace, float32
-// Adam there runs at 8 workgroups (16 waves) per CU: 6.46-6.47 against
-// 6.38 TB/s uncapped.
-constexpr uint32_t kLdsPerCU = 160 * 1024;
-constexpr uint32_t lds_for_residency(uint32_t n) {
-  uint32_t x = (kLdsPerCU / n) / 256 * 256;
-  while (kLdsPerCU / x > n) x += 256;
-  return x;
-}
-template <typename T, typename S>
-constexpr bool kFp32State = std::is_same<T, float>::value && std::is_same<S, float>::value;
-template <typename T, typename S>
-constexpr uint32_t residency_lds(uint32_t n) {
-  return kFp32State<T, S> ? lds_for_residency(n) : 0u;
-}
-template <typename T, typename S>
-constexpr bool kBf16State = std::is_same<T, float>::value && std::is_same<S, bf16_t>::value;
-constexpr int64_t kCapMinElems = int64_t(8192) * 512;
-
-// Launches whose (R, T) operands take at most this many bytes run the SMALL
-// streaming shape (plain accesses, the policy's kStreamUnrollSmall, no cap):
-// the MI355X's 256 MB MALL then keeps them between back-to-back steps.
-// Measured on configs 1-4 (prep + update through the C ABI, 200 launches, 5
-// rounds): config 1 (34 MB of Adam operands) 11.7 us plain with 2 packs
-// against 13.0 non-temporal; config 3 (209 MB, SGD) 32.0 us plain with 1 pack
-// (2 / 4 / 8 packs: 33.9 / 32.6 / 32.2) against 35.8; configs 2 and 4 (531 /
-// 419 MB) lose 11-16% with plain accesses, so they stay non-temporal.
-constexpr int64_t kMallBytes = int64_t(256) << 20;
-
-// Packs per thread of the streaming driver, by operand types: float32
-// throughout, float32 params with bfloat16 state, 16-bit params, float64.
-// Measured per policy on config-5-sized state (1/2/4/8 packs, one process per
-// sweep, two sweeps): float32 keeps 2 (under its residency cap); bfloat16
-// state wants 4 for Adam (+13%) but 1 for SGD and Adagrad (+8-15%); 16-bit
-// params 4-8 (+12-22%); float64 is flat. 16-bit Adam and Adagrad moved from
-// 4 to 8 once bfloat16 narrowing became one instruction: Adam +6% (half), +10%
-// (bfloat16); Adagrad +4% (half), +5.5% (bfloat16).
-// kLateStores (per policy): the streaming driver stores a thread's packs
-// after all of its arithmetic instead of each pack right after its own.
-// Measured interleaved on the config-5 buffers: Adam +0.6-0.9% (three boxes),
-// Adam with bfloat16 moments +1.9-2.0%, SGD +0.2-0.3%, Adagrad -1.2%; Adam
-// with amsgrad -2.2% (config 2 scaled to 1200 replicas; -0.8% at config 2)
-// against +2.8% for Adam at config 1; float64 Adam -31% (5.06 -> 3.47 TB/s),
-// float16 Adam -2%, bfloat16-parameter Adam +1.4%. So only float32 parameters
-// (with float32 or bfloat16 state) of Adam without amsgrad and of SGD store
-// late. The segmented driver keeps per-pack stores for every policy: late
-// ones lost 0.6-0.8% there.
-template <typename T, typename S>
-constexpr int stream_unroll(int fp32, int bf16_state, int narrow, int wide) {
-  return std::is_same<T, double>::value ? wide
-         : sizeof(T) == 2              ? narrow
-         : !std::is_same<S, T>::value  ? bf16_state
-                                       : fp32;
-}
-
-// Every policy has a parameter/gradient type T and an optimizer-state type S:
-// S == T is the reference's contract; S = bf16_t with T = float keeps the
-// moments (momentum buffers, sums) in bfloat16 while the element math and the
-// parameters stay in float32 (the state is widened on load and rounded to
-// nearest-even on store).
-//
-// Per-replica constants. `prologue<false>` derives a replica's constants in
-// every workgroup (Adam: two fp64 pow; Adagrad: an fp64 divide);
-// `prologue<true>` reads them from the call's workspace, where the preparation
-// launch (`precompute`, once per replica and call, after the step bump) put
-// them. Both give the same bits: the workspace holds the math-type values
-// widened to double. kPreWords is the number of such doubles (0: nothing worth
-// hoisting, the policy never reads a workspace). `reads_state` is decided from
-// the (R,) vectors alone, so the drivers issue their loads before the prologue.
-//
-// Streaming shape with a workspace (kStreamUnrollPre, kStreamLdsPre). Without
-// the pow in every workgroup, float32 Adam runs fastest with one pack per
-// thread (256-element tiles) under the same cap of 14 workgroups per CU:
-// 6.51 against 6.15 TB/s for the per-workgroup form (two boxes, config-5
-// buffers, interleaved); two packs with precomputed constants reached 6.22
-// at that cap and 6.36 at 8, and a workgroup walking 2-8 consecutive tiles
-// with one prologue 6.10-6.22. The same sweep per policy (config-5 shape,
-// 3 interleaved rounds, two boxes; one pack against the old two):
-//   Adam with amsgrad    1 pack, cap 12: 6.34-6.36 TB/s (2 packs: 5.85)
-//   Adagrad (fp64 math)  1 pack, cap 20: 6.45-6.49 (2 packs, cap 16: 5.70;
-//                        caps 18-24 within 0.7% of each other)
-//   Adagrad, fp32 math   1 pack, cap 20: 6.52 (2 packs, cap 16: 5.84)
-//   Adam, bf16 moments   4 packs, cap 12: 6.15-6.31 (uncapped: 5.90-6.23)
-// SGD has no workspace, but with its loads issued before the prologue its
-// buffered float32 form also runs one pack per thread, cap 20: 6.46-6.60
-// against 6.13 for two packs at cap 14. 16-bit parameters (8 packs,
-// uncapped), bfloat16-state SGD and Adagrad (1 pack, uncapped) and float64
-// (2 packs) kept their shapes: nothing else in the sweep beat them.
-
-// Adam / AdamW: h = {lr, beta1, beta2, eps, weight_decay}.
-template <typename T_, bool ADAMW, bool AMSGRAD, typename S_ = T_>
-struct AdamPolicy {
-  using T = T_;
-  using S = S_;
-  using M = op_t<T>;
-  static constexpr int NS = AMSGRAD ? 3 : 2;
-  static constexpr uint32_t kStreamLds = residency_lds<T, S>(AMSGRAD ? 12 : 14);
-  static constexpr int kStreamUnroll = stream_unroll<T, S>(2, 4, 8, 2);
-  static constexpr uint32_t kStreamLdsPre =
-      kBf16State<T, S> ? lds_for_residency(12) : kStreamLds;
-  static constexpr int kStreamUnrollPre = stream_unroll<T, S>(1, 4, 8, 2);
-  static constexpr int kStreamUnrollSmall = stream_unroll<T, S>(2, 4, 8, 2);
-  static constexpr int64_t kStreamSmallBytes = kMallBytes;
-  static constexpr int kSegmentUnroll = stream_unroll<T, S>(2, 4, 8, 2);
-  static constexpr uint32_t kSegmentLds = residency_lds<T, S>(8);
-  static constexpr bool kLateStores = !AMSGRAD && std::is_same<T_, float>::value;
-  static constexpr int kPreWords = 2;
-  struct Rep {
-    AdamHyper h;
-    M bc1, bc2s;
-  };
-  // bias_correction1 and sqrt(bias_correction2) of the bumped step.
-  __device__ static void precompute(const Vectors<T>& v, uint32_t r, double* out) {
-    M bc1, bc2s;
-    adam_bias_corrections<M>(hyper_at(v.h[1], r), hyper_at(v.h[2], r), hyper_at(v.steps, r),
-                             bc1, bc2s);
-    out[0] = static_cast<double>(bc1);
-    out[1] = static_cast<double>(bc2s);
-  }
-  template <bool PRE>
-  __device__ static void prologue(const Vectors<T>& v, uint32_t r, Rep& rep) {
-    rep.h.lr = hyper_at(v.h[0], r);
-    rep.h.beta1 = hyper_at(v.h[1], r);
-    rep.h.beta2 = hyper_at(v.h[2], r);
-    rep.h.eps = hyper_at(v.h[3], r);
-    rep.h.weight_decay = hyper_at(v.h[4], r);
-    if constexpr (PRE) {
-      rep.bc1 = static_cast<M>(v.pre[kPreStride * r]);
-      rep.bc2s = static_cast<M>(v.pre[kPreStride * r + 1]);
-    } else {
-      adam_bias_corrections<M>(rep.h.beta1, rep.h.beta2, hyper_at(v.steps, r), rep.bc1,
-                               rep.bc2s);
-    }
-  }
-  __device__ static bool reads_state(const Vectors<T>&, uint32_t) { return true; }
-  __device__ static void update(M& p, M g, M (&s)[NS], const Rep& rep, bool maximize) {
-    M mx = M(0);
-    if constexpr (AMSGRAD) mx = s[2];
-    adam_element<M, ADAMW, AMSGRAD>(p, g, s[0], s[1], mx, rep.h, maximize, rep.bc1,
-                                    rep.bc2s);
-    if constexpr (AMSGRAD) s[2] = mx;
-  }
-};
-
-// SGD: h = {lr, momentum, dampening, weight_decay}. The hyperparameters are
-// carried as double inside the element math, as torch's ROCm `_fused_sgd_`
-// takes them (checked on the MI355X: carrying them as float instead changes
-// params and buffers by up to a few ulp). Its prologue is four loads and a
-// compare: nothing to precompute.
-template <typename T_, bool HAS_BUF, bool NESTEROV, typename S_ = T_>
-struct SgdPolicy {
-  using T = T_;
-  using S = S_;
-  using M = op_t<T>;
-  static constexpr int NS = HAS_BUF ? 1 : 0;
-  static constexpr uint32_t kStreamLds = HAS_BUF ? residency_lds<T, S>(20) : 0u;
-  static constexpr int kStreamUnroll = stream_unroll<T, S>(HAS_BUF ? 1 : 2, 1, 8, 2);
-  static constexpr uint32_t kStreamLdsPre = kStreamLds;
-  static constexpr int kStreamUnrollPre = kStreamUnroll;
-  static constexpr int kStreamUnrollSmall = stream_unroll<T, S>(1, 1, 8, 2);
-  static constexpr int64_t kStreamSmallBytes = kMallBytes;
-  static constexpr int kSegmentUnroll = 2;
-  static constexpr uint32_t kSegmentLds = 0;
-  static constexpr bool kLateStores = std::is_same<T_, float>::value;
-  static constexpr int kPreWords = 0;
-  struct Rep {
-    SgdHyper<double> h;
-    bool first;
-  };
-  __device__ static void precompute(const Vectors<T>&, uint32_t, double*) {}
-  template <bool PRE>
-  __device__ static void prologue(const Vectors<T>& v, uint32_t r, Rep& rep) {
-    rep.h.lr = hyper_at(v.h[0], r);
-    rep.h.momentum = hyper_at(v.h[1], r);
-    rep.h.dampening = hyper_at(v.h[2], r);
-    rep.h.weight_decay = hyper_at(v.h[3], r);
-    rep.first = widen(v.steps[r]) == M(1);
-  }
-  // On a replica's first step the buffer is overwritten by the gradient
-  // without being read, so it is not fetched.
-  __device__ static bool reads_state(const Vectors<T>& v, uint32_t r) {
-    return widen(v.steps[r]) != M(1);
-  }
-  __device__ static void update(M& p, M g, M (&s)[NS > 0 ? NS : 1], const Rep& rep,
-                                bool maximize) {
-    M buf = s[0];
-    sgd_element<M, double, HAS_BUF, NESTEROV>(p, g, buf, rep.h, maximize, rep.first);
-    s[0] = buf;
-  }
-};
-
-// Adagrad: h = {lr, lr_decay, weight_decay, eps}.
-template <typename T_, typename S_ = T_>
-struct AdagradPolicy {
-  using T = T_;
-  using S = S_;
-  using M = op_t<T>;
-  static constexpr int NS = 1;
-  static constexpr uint32_t kStreamLds = residency_lds<T, S>(16);
-  static constexpr int kStreamUnroll = stream_unroll<T, S>(2, 1, 8, 2);
-  static constexpr uint32_t kStreamLdsPre = residency_lds<T, S>(20);
-  static constexpr int kStreamUnrollPre = stream_unroll<T, S>(1, 1, 8, 2);
-  static constexpr int kStreamUnrollSmall = stream_unroll<T, S>(2, 1, 8, 2);
-  static constexpr int64_t kStreamSmallBytes = kMallBytes;
-  static constexpr int kSegmentUnroll = 2;
-  static constexpr uint32_t kSegmentLds = 0;
-  static constexpr bool kLateStores = false;
-  static constexpr int kPreWords = 1;
-  struct Rep {
-    AdagradHyper h;
-  };
-  // corrected_lr of the bumped step.
-  __device__ static void precompute(const Vectors<T>& v, uint32_t r, double* out) {
-    out[0] = adagrad_corrected_lr(hyper_at(v.h[0], r), hyper_at(v.h[1], r),
-                                  static_cast<float>(widen(v.steps[r])));
-  }
-  template <bool PRE>
-  __device__ static void prologue(const Vectors<T>& v, uint32_t r, Rep& rep) {
-    rep.h.weight_decay = hyper_at(v.h[2], r);
-    rep.h.eps = hyper_at(v.h[3], r);
-    if constexpr (PRE) {
-      rep.h.corrected_lr = v.pre[kPreStride * r];
-    } else {
-      rep.h.corrected_lr = adagrad_corrected_lr(hyper_at(v.h[0], r), hyper_at(v.h[1], r),
-                                                static_cast<float>(widen(v.steps[r])));
-    }
-  }
-  __device__ static bool reads_state(const Vectors<T>&, uint32_t) { return true; }
-  __device__ static void update(M& p, M g, M (&s)[NS], const Rep& rep, bool maximize) {
-    adagrad_element<M>(p, g, s[0], rep.h, maximize);
-  }
-};
-
-// Float32 Adagrad (TS_ADAGRAD_F32): the reference CPU kernel's float element
-// math instead of ATen's fp64 update; h = {lr, lr_decay, wd, eps}. The math
-// type is float for every storage type (float64 parameters are rejected).
-template <typename T_, typename S_ = T_>
-struct AdagradF32Policy {
-  using T = T_;
-  using S = S_;
-  using M = float;
-  static constexpr int NS = 1;
-  static constexpr uint32_t kStreamLds = residency_lds<T, S>(16);
-  static constexpr int kStreamUnroll = stream_unroll<T, S>(2, 1, 4, 2);
-  static constexpr uint32_t kStreamLdsPre = residency_lds<T, S>(20);
-  static constexpr int kStreamUnrollPre = stream_unroll<T, S>(1, 1, 4, 2);
-  static constexpr int kStreamUnrollSmall = stream_unroll<T, S>(2, 1, 4, 2);
-  static constexpr int64_t kStreamSmallBytes = kMallBytes;
-  static constexpr int kSegmentUnroll = 2;
-  static constexpr uint32_t kSegmentLds = 0;
-  static constexpr bool kLateStores = false;
-  static constexpr int kPreWords = 1;
-  struct Rep {
-    AdagradF32Hyper h;
-  };
-  __device__ static void precompute(const Vectors<T>& v, uint32_t r, double* out) {
-    out[0] = static_cast<double>(
-        adagrad_corrected_lr_f32(hyper_at(v.h[0], r), hyper_at(v.h[1], r), hyper_at(v.steps, r)));
-  }
-  template <bool PRE>
-  __device__ static void prologue(const Vectors<T>& v, uint32_t r, Rep& rep) {
-    const double wd = hyper_at(v.h[2], r);
-    rep.h.weight_decay = static_cast<float>(wd);
-    rep.h.has_weight_decay = wd != 0.0;
-    rep.h.eps = static_cast<float>(hyper_at(v.h[3], r));
-    if constexpr (PRE) {
-      rep.h.corrected_lr = static_cast<float>(v.pre[kPreStride * r]);
-    } else {
-      rep.h.corrected_lr = adagrad_corrected_lr_f32(hyper_at(v.h[0], r), hyper_at(v.h[1], r),
-                                                    hyper_at(v.steps, r));
-    }
-  }
-  __device__ static bool reads_state(const Vectors<T>&, uint32_t) { return true; }
-  __device__ static void update(M& p, M g, M (&s)[NS], const Rep& rep, bool maximize) {
-    adagrad_element_f32(p, g, s[0], rep.h, maximize);
-  }
-};
-
-template <typename P>
-constexpr int state_slots() {
-  return P::NS > 0 ? P::NS : 1;
-}
-
-// Packs per thread and residency reservation of the streaming driver, with
-// the per-replica constants read from a workspace (PRE) or derived in every
-// workgroup, for large launches and for SMALL ones (operands that fit the
-// MALL: plain accesses, no cap).
-template <typename P, bool PRE, bool SMALL>
-constexpr int stream_unroll_of() {
-  return SMALL ? P::kStreamUnrollSmall : PRE ? P::kStreamUnrollPre : P::kStreamUnroll;
-}
-template <typename P, bool PRE, bool SMALL>
-constexpr uint32_t stream_lds_of() {
-  return SMALL ? 0u : PRE ? P::kStreamLdsPre : P::kStreamLds;
-}
-
-// Elements per streaming tile: one wavefront x the policy's packs per thread.
-template <typename P, bool PRE, bool SMALL>
-constexpr int64_t stream_tile() {
-  return int64_t(kStreamThreads) * kPack * stream_unroll_of<P, PRE, SMALL>();
-}
-
-// Bytes of (R, T) operands a launch reads (all rows): params and grads in
-// the parameter type, the state buffers in the state type.
-template <typename P>
-constexpr int64_t operand_bytes_per_elem() {
-  return 2 * int64_t(sizeof(typename P::T)) + P::NS * int64_t(sizeof(typename P::S));
-}
-
-// Elements per segmented-driver tile (128 threads). Measured per policy at the
-// config-5 layout with per-parameter gradients (1/2/4 packs): Adam with
-// bfloat16 moments or 16-bit params wants 4 (+8-17%); SGD and Adagrad were
-// within noise of 2 for every operand type, and float32/float64 Adam too.
-// With one-instruction bfloat16 narrowing, 16-bit Adam gained again from 8:
-// +2.7% (half), +4.2% (bfloat16).
-template <typename P>
-constexpr int64_t segment_tile() {
-  return int64_t(kThreads) * kPack * P::kSegmentUnroll;
-}
-
-template <typename P>
-struct KArgs {
-  Operands<typename P::T> x;
-  Vectors<typename P::T> vec;
-  Grid g;
-  bool maximize;
-};
-
-// One element through the policy: widen, update, narrow. `s_io` holds the
-// state operands' values (unread ones are never used).
-template <typename P>
-__device__ __forceinline__ void apply_element(typename P::T& p_io, typename P::T g_in,
-                                              typename P::S (&s_io)[state_slots<P>()],
-                                              bool load_state, const typename P::Rep& rep,
-                                              bool maximize) {
-  using M = typename P::M;
-  M p = widen(p_io);
-  M s[state_slots<P>()];
-#pragma unroll
-  for (int k = 0; k < state_slots<P>(); ++k) {
-    s[k] = (load_state && k < P::NS) ? M(widen(s_io[k])) : M(0);
-  }
-  P::update(p, widen(g_in), s, rep, maximize);
-  p_io = narrow<typename P::T>(p);
-#pragma unroll
-  for (int k = 0; k < P::NS; ++k) {
-    s_io[k] = narrow<typename P::S>(s[k]);
-  }
-}
-
-// Row r of (R, T) operand b, as the parameter type (b < 2) or the state type.
-template <typename P>
-__device__ __forceinline__ typename P::T* pg_row(const Operands<typename P::T>& x, int b,
-                                                 uint32_t r) {
-  return x.data[b] + int64_t(r) * x.stride_r[b];
-}
-template <typename P>
-__device__ __forceinline__ typename P::S* state_row(const Operands<typename P::T>& x, int b,
-                                                    uint32_t r) {
-  return reinterpret_cast<typename P::S*>(x.data[b]) + int64_t(r) * x.stride_r[b];
-}
-
-// ---------------------------------------------------------------------------
-// Drivers
-// ---------------------------------------------------------------------------
-// PRE: the per-replica constants come from the call's workspace (a.vec.pre).
-// A thread's loads are issued before the replica's prologue, which then runs
-// while they are in flight.
-// SMALL: the launch's operands fit the MALL; plain accesses and the small-launch
-// tile instead of non-temporal ones.
-template <typename P, bool ANY, bool PRE, bool SMALL>
-__global__ __launch_bounds__(kStreamThreads) void stream_kernel(KArgs<P> a) {
-  using T = typename P::T;
-  using S = typename P::S;
-  constexpr int NS = P::NS;
-  constexpr int SS = state_slots<P>();
-  constexpr bool NT = !SMALL;
-  constexpr int U = stream_unroll_of<P, PRE, SMALL>();
-  constexpr int64_t kStreamTile = stream_tile<P, PRE, SMALL>();
-  uint32_t r;
-  int64_t t0;
-  tile_of_block<kStreamTile>(a.g, r, t0);
-  if (!a.vec.mask[r]) {
-    return;
-  }
-  const bool load_state = P::reads_state(a.vec, r);
-
-  constexpr uint32_t A = align_elems<T>();
-  const int64_t width = a.g.T;
-  const int64_t head = imin(width, (A - (a.g.res0 + r * a.g.rmod) % A) % A);
-  const int64_t packs_row = (width - head) / kPack;
-  T* const pbase = pg_row<P>(a.x, 0, r);
-  const T* const gbase = pg_row<P>(a.x, 1, r);
-  S* sbase[SS];
-#pragma unroll
-  for (int b = 0; b < NS; ++b) sbase[b] = state_row<P>(a.x, 2 + b, r);
-
-  // The parameters' packs are 16-byte aligned by construction; with ANY the
-  // other operands sit at another 16-byte phase and use element-aligned packs.
-  Pack<T>* prow = reinterpret_cast<Pack<T>*>(pbase + head) + t0 / kPack;
-  const Packs<ANY, T, NT> grow(const_cast<T*>(gbase) + head + t0);
-  Packs<ANY, S, NT> srow[SS];
-#pragma unroll
-  for (int b = 0; b < NS; ++b) srow[b] = Packs<ANY, S, NT>(sbase[b] + head + t0);
-  const int64_t packs_left = packs_row - t0 / kPack;
-
-  Pack<T> vp[U], vg[U];
-  Pack<S> vs[SS][U];
-#pragma unroll
-  for (int u = 0; u < U; ++u) {
-    const int64_t i = int64_t(u) * kStreamThreads + threadIdx.x;
-    if (i < packs_left) {
-      vp[u] = load_stream<NT>(prow + i);
-      vg[u] = grow.load(i);
-      if (load_state) {
-#pragma unroll
-        for (int b = 0; b < NS; ++b) {
-          vs[b][u] = srow[b].load(i);
-        }
-      }
-    }
-  }
-  typename P::Rep rep;
-  P::template prologue<PRE>(a.vec, r, rep);
-  const auto store_packs = [&](int u, int64_t i) {
-    store_stream<NT>(prow + i, vp[u]);
-#pragma unroll
-    for (int b = 0; b < NS; ++b) {
-      srow[b].store(i, vs[b][u]);
-    }
-  };
-#pragma unroll
-  for (int u = 0; u < U; ++u) {
-    const int64_t i = int64_t(u) * kStreamThreads + threadIdx.x;
-    if (i < packs_left) {
-#pragma unroll
-      for (int k = 0; k < kPack; ++k) {
-        S st[SS];
-#pragma unroll
-        for (int b = 0; b < NS; ++b) st[b] = vs[b][u].v[k];
-        apply_element<P>(vp[u].v[k], vg[u].v[k], st, load_state, rep, a.maximize);
-#pragma unroll
-        for (int b = 0; b < NS; ++b) vs[b][u].v[k] = st[b];
-      }
-      if constexpr (!P::kLateStores) store_packs(u, i);
-    }
-  }
-  if constexpr (P::kLateStores) {
-#pragma unroll
-    for (int u = 0; u < U; ++u) {
-      const int64_t i = int64_t(u) * kStreamThreads + threadIdx.x;
-      if (i < packs_left) store_packs(u, i);
-    }
-  }
-
-  // The row's head before its first 256-byte boundary (tile 0) and its at most
-  // three tail elements (last tile), one element per access.
-  const auto one = [&](int64_t j) {
-    T pe = pbase[j];
-    S st[SS];
-    if (load_state) {
-#pragma unroll
-      for (int b = 0; b < NS; ++b) st[b] = sbase[b][j];
-    }
-    apply_element<P>(pe, gbase[j], st, load_state, rep, a.maximize);
-    pbase[j] = pe;
-#pragma unroll
-    for (int b = 0; b < NS; ++b) sbase[b][j] = st[b];
-  };
-  if (t0 == 0) {
-    for (int64_t j = threadIdx.x; j < head; j += kStreamThreads) one(j);
-  }
-  if (t0 + kStreamTile >= width) {
-    for (int64_t j = head + packs_row * kPack + threadIdx.x; j < width; j += kStreamThreads) one(j);
-  }
-}
-
-template <typename P>
-__global__ __launch_bounds__(kThreads) void element_kernel(KArgs<P> a) {
-  using T = typename P::T;
-  using S = typename P::S;
-  constexpr int NS = P::NS;
-  constexpr int SS = state_slots<P>();
-  uint32_t r;
-  int64_t t0;
-  tile_of_block<kTile>(a.g, r, t0);
-  if (!a.vec.mask[r]) {
-    return;
-  }
-  typename P::Rep rep;
-  P::template prologue<false>(a.vec, r, rep);
-  const bool load_state = P::reads_state(a.vec, r);
-
-  T* const prow = pg_row<P>(a.x, 0, r);
-  const T* const grow = pg_row<P>(a.x, 1, r);
-  S* srow[SS];
-#pragma unroll
-  for (int b = 0; b < NS; ++b) srow[b] = state_row<P>(a.x, 2 + b, r);
-  T vp[kPer], vg[kPer];
-  S vs[SS][kPer];
-#pragma unroll
-  for (int u = 0; u < kPer; ++u) {
-    const int64_t t = t0 + int64_t(u) * kThreads + threadIdx.x;
-    if (t < a.g.T) {
-      vp[u] = prow[t * a.x.stride_t[0]];
-      vg[u] = grow[t * a.x.stride_t[1]];
-      if (load_state) {
-#pragma unroll
-        for (int b = 0; b < NS; ++b) {
-          vs[b][u] = srow[b][t * a.x.stride_t[2 + b]];
-        }
-      }
-    }
-  }
-#pragma unroll
-  for (int u = 0; u < kPer; ++u) {
-    const int64_t t = t0 + int64_t(u) * kThreads + threadIdx.x;
-    if (t < a.g.T) {
-      S st[SS];
-#pragma unroll
-      for (int b = 0; b < NS; ++b) st[b] = vs[b][u];
-      apply_element<P>(vp[u], vg[u], st, load_state, rep, a.maximize);
-      prow[t * a.x.stride_t[0]] = vp[u];
-#pragma unroll
-      for (int b = 0; b < NS; ++b) {
-        srow[b][t * a.x.stride_t[2 + b]] = st[b];
-      }
-    }
-  }
-}
-
-// Replica-minor operands: every (R, T) operand has unit replica stride (the
-// transposed views an outer vmap over a non-leading dimension produces, or
-// (T, R) buffers seen as (R, T)). A row-walking workgroup would touch one
-// element per cache line there, so this driver turns the walk around: a
-// workgroup covers `rb` consecutive replicas times a block of columns, each
-// thread keeps one replica (its hyperparameters and per-replica constants,
-// computed once) and walks columns `cpi` apart, so the threads of one
-// iteration read consecutive replicas of consecutive columns -- contiguous
-// memory when the column stride is R. Above 256 replicas, when 256-thread
-// replica blocks would leave over a quarter of the threads idle, workgroups
-// have 128 threads: R = 257 / 300 ran at 4.3 / 4.7 TB/s instead of 3.3, while
-// R = 600 / 1000 / 2000 keep 256 (4.7 / 4.7 / 4.7; 128 gave 4.8 / 4.4 / 4.8).
-//
-// Non-temporal accesses where no cache line is shared between workgroups (one
-// replica block, or replica blocks, columns and bases on 128-byte boundaries)
-// and the wavefront has no frozen replica: +6-9% there (R = 8..256: 5.3 -> 5.8
-// TB/s; R = 4096: 4.8 -> 5.1). Where replica blocks split lines (R = 257..2000)
-// plain accesses let L2 merge the two halves: non-temporal ones ran at 2.6-3.9
-// TB/s instead of 4.4-4.8. (Threads that keep four replicas and move them as
-// one pack, so that a column of up to 1024 replicas has one workgroup, measured
-// 0.1-0.9 TB/s slower at every R.)
-constexpr int kColThreads = 256;
-constexpr int kColThreadsNarrow = 128;
-constexpr int kColIters = 32;  // columns per thread per workgroup
-constexpr int kColUnroll = 4;
-constexpr uint32_t kLineBytes = 128;
-constexpr uint32_t kXcds = 8;
-
-struct ColGrid {
-  int64_t R, T;
-  uint32_t threads;    // workgroup size, at most kColThreads
-  uint32_t rb;         // replicas per workgroup, min(R, threads)
-  uint32_t cpi;        // columns per iteration, threads / rb
-  uint32_t n_rblocks;  // ceil(R / rb)
-};
-
-template <typename P>
-struct ColArgs {
-  Operands<typename P::T> x;
-  Vectors<typename P::T> vec;
-  ColGrid g;
-  bool maximize;
-};
-
-// One element of any storage type, plain or non-temporal.
-template <typename T>
-using ElemBits = std::conditional_t<sizeof(T) == 2, uint16_t,
-                                    std::conditional_t<sizeof(T) == 4, uint32_t, uint64_t>>;
-template <bool NT, typename T>
-__device__ __forceinline__ T load_one(const T* p) {
-  if constexpr (NT) {
-    return __builtin_bit_cast(
-        T, __builtin_nontemporal_load(reinterpret_cast<const ElemBits<T>*>(p)));
-  } else {
-    return *p;
-  }
-}
-template <bool NT, typename T>
-__device__ __forceinline__ void store_one(T* p, T v) {
-  if constexpr (NT) {
-    __builtin_nontemporal_store(__builtin_bit_cast(ElemBits<T>, v),
-                                reinterpret_cast<ElemBits<T>*>(p));
-  } else {
-    *p = v;
-  }
-}
-
-// One thread's walk over its replica's columns, plain or non-temporal.
-template <typename P, bool NT>
-__device__ __forceinline__ void column_walk(const ColArgs<P>& a, int64_t r, int64_t t_first,
-                                            const typename P::Rep& rep, bool load_state) {
-  using T = typename P::T;
-  using S = typename P::S;
-  constexpr int NS = P::NS;
-  constexpr int SS = state_slots<P>();
-  T* const pcol = a.x.data[0] + r;
-  const T* const gcol = a.x.data[1] + r;
-  S* scol[SS];
-#pragma unroll
-  for (int b = 0; b < NS; ++b) scol[b] = reinterpret_cast<S*>(a.x.data[2 + b]) + r;
-
-  for (int j = 0; j < kColIters; j += kColUnroll) {
-    T vp[kColUnroll], vg[kColUnroll];
-    S vs[SS][kColUnroll];
-#pragma unroll
-    for (int u = 0; u < kColUnroll; ++u) {
-      const int64_t t = t_first + int64_t(j + u) * a.g.cpi;
-      if (t < a.g.T) {
-        vp[u] = load_one<NT>(pcol + t * a.x.stride_t[0]);
-        vg[u] = load_one<NT>(gcol + t * a.x.stride_t[1]);
-        if (load_state) {
-#pragma unroll
-          for (int b = 0; b < NS; ++b) vs[b][u] = load_one<NT>(scol[b] + t * a.x.stride_t[2 + b]);
-        }
-      }
-    }
-#pragma unroll
-    for (int u = 0; u < kColUnroll; ++u) {
-      const int64_t t = t_first + int64_t(j + u) * a.g.cpi;
-      if (t < a.g.T) {
-        S st[SS];
-#pragma unroll
-        for (int b = 0; b < NS; ++b) st[b] = vs[b][u];
-        apply_element<P>(vp[u], vg[u], st, load_state, rep, a.maximize);
-        store_one<NT>(pcol + t * a.x.stride_t[0], vp[u]);
-#pragma unroll
-        for (int b = 0; b < NS; ++b) store_one<NT>(scol[b] + t * a.x.stride_t[2 + b], st[b]);
-      }
-    }
-  }
-}
-
-// NT: the launch's lines are private to workgroups (col_lines_private); a
-// wavefront then goes non-temporal unless it has frozen replicas, whose
-// unwritten elements would leave partial lines (non-temporal partial lines ran
-// at 3.4-3.7 TB/s where plain ones ran at 4.7-4.9 with a tenth of the replicas
-// frozen; non-temporal loads with plain stores were no better, 2.8-3.4).
-// Storing after all four unrolled columns' arithmetic (the streaming driver's
-// late stores) moved the column driver by -3% (non-temporal) to +2% (plain):
-// not adopted.
-template <typename P, bool NT>
-__global__ __launch_bounds__(kColThreads) void column_kernel(ColArgs<P> a) {
-  uint32_t blk = blockIdx.x;
-  if (a.g.n_rblocks > 1) {
-    // The replica blocks of a column block run on one XCD: workgroups are
-    // dealt to the kXcds XCDs round-robin, so XCD x takes the x-th contiguous
-    // range of the remapped order, and consecutive replica blocks meet in its
-    // L2 (lines split between them are fetched once). Against the plain order
-    // on the same buffers: R = 257 / 300 / 1000 / 2000 4.4-4.7 -> 4.8-5.0
-    // TB/s (two boxes); with private lines R = 2048 4.7 -> 5.3, R = 4096 5.0
-    // -> 5.7 on one box and 5.7 -> 5.6 on another, R = 8192 5.8 either way.
-    // With one replica block the plain order is faster (R <= 256: 5.8 against
-    // 5.0-5.5 remapped).
-    const uint32_t n = gridDim.x, x = blockIdx.x % kXcds, per = n / kXcds, rem = n % kXcds;
-    blk = x * per + (x < rem ? x : rem) + blockIdx.x / kXcds;
-  }
-  const uint32_t rblk = blk % a.g.n_rblocks;
-  const uint32_t cblk = blk / a.g.n_rblocks;
-  const uint32_t rr = threadIdx.x % a.g.rb;
-  const uint32_t cc = threadIdx.x / a.g.rb;
-  const int64_t r = int64_t(rblk) * a.g.rb + rr;
-  const bool in_range = cc < a.g.cpi && r < a.g.R;
-  const bool active = in_range && a.vec.mask[r];
-  bool nt = false;
-  if constexpr (NT) {
-    nt = __ballot(in_range) == __ballot(active);
-  }
-  // Threads past the last replica or column lane, and frozen replicas, have
-  // nothing to do (the workgroup has no barrier).
-  if (!active) {
-    return;
-  }
-  typename P::Rep rep;
-  P::template prologue<false>(a.vec, static_cast<uint32_t>(r), rep);
-  const bool load_state = P::reads_state(a.vec, static_cast<uint32_t>(r));
-  const int64_t t_first = int64_t(cblk) * a.g.cpi * kColIters + cc;
-  if (nt) {
-    column_walk<P, true>(a, r, t_first, rep, load_state);
-  } else {
-    column_walk<P, false>(a, r, t_first, rep, load_state);
-  }
-}
-
-// ---------------------------------------------------------------------------
-// Segmented gradients
-// ---------------------------------------------------------------------------
-constexpr int kMaxSegments = 64;
-
-// Up to kMaxSegments per-parameter (R, numel) tensors, each mapped onto the
-// columns [col, col + numel) of the (R, T) layout. tile0 is the prefix sum of
-// the segments' tile counts, so a row has tile0[n] tiles; bit s of `vec_ok`
-// says segment s takes the vector walk (the (R, T) operands are streamable and
-// the segment's data is element-aligned).
-template <typename T>
-struct Segments {
-  const T* data[kMaxSegments];
-  int64_t stride_r[kMaxSegments];
-  int64_t col[kMaxSegments];
-  int64_t numel[kMaxSegments];
-  uint32_t tile0[kMaxSegments + 1];
-  uint64_t vec_ok;
-  int n;
-};
-
-template <typename P>
-struct SegArgs {
-  KArgs<P> k;  // k.x.data[1]: consolidated gradient to write, or null;
-               // k.g.res0 / rmod: the params rows' 256-byte phase
-  Segments<typename P::T> seg;
-};
-
-__device__ __forceinline__ int segment_of_tile(const uint32_t* tile0, int n, uint32_t t) {
-  int lo = 0, hi = n - 1;
-  while (lo < hi) {
-    const int mid = (lo + hi + 1) >> 1;
-    if (tile0[mid] <= t) lo = mid;
-    else hi = mid - 1;
-  }
-  return lo;
-}
-
-// A segment's tile on the vector walk. The walk follows the (R, T) layout: in
-// row r the segment's first 256-byte boundary lies `head` elements in (head <
-// A, as for the streaming driver); packs of 4 elements stream from there, tile
-// k taking packs [k * TILE / 4, (k + 1) * TILE / 4). Tile 0 also takes the
-// head elements and the segment's last tile the at most three tail elements,
-// one element per access. The per-parameter gradient's rows keep their own
-// alignment: they are read with element-aligned pack loads.
-struct SegTile {
-  int64_t head;   // elements before the first pack
-  int64_t first;  // element index of this tile's first pack
-  int64_t packs;  // packs in this tile (may be <= 0)
-  int64_t tail;   // first tail element (== numel: none)
-  bool has_head, has_tail;
-};
-
-template <typename T, int64_t TILE>
-__device__ __forceinline__ SegTile seg_tile(uint32_t res0, uint32_t rmod, uint32_t r,
-                                            int64_t col, int64_t numel, int64_t j0) {
-  constexpr uint32_t A = align_elems<T>();
-  SegTile t;
-  const uint32_t phase = (res0 + r * rmod + static_cast<uint32_t>(col % A)) % A;
-  t.head = imin(numel, (A - phase) % A);
-  const int64_t packs_seg = (numel - t.head) / kPack;
-  t.first = t.head + j0;
-  t.packs = packs_seg - j0 / kPack;
-  t.tail = t.head + packs_seg * kPack;
-  t.has_head = j0 == 0;
-  t.has_tail = j0 + TILE >= numel;
-  return t;
-}
-
-// Runs fn(j) for the tile's single elements, spread over the threads.
-template <typename Fn>
-__device__ __forceinline__ void seg_singles(const SegTile& t, int64_t numel, Fn&& fn) {
-  if (t.has_head) {
-    for (int64_t j = threadIdx.x; j < t.head; j += kThreads) fn(j);
-  }
-  if (t.has_tail) {
-    for (int64_t j = t.tail + threadIdx.x; j < numel; j += kThreads) fn(j);
-  }
-}
-
-// PRE: the per-replica constants come from the call's workspace (a.k.vec.pre).
-template <typename P, bool ANY, bool PRE>
-__global__ __launch_bounds__(kThreads) void segment_kernel(SegArgs<P> a) {
-  using T = typename P::T;
-  using S = typename P::S;
-  constexpr int NS = P::NS;
-  constexpr int SS = state_slots<P>();
-  constexpr int U = P::kSegmentUnroll;
-  constexpr int64_t kSegTile = segment_tile<P>();
-  const uint32_t tiles_per_row = a.seg.tile0[a.seg.n];
-  const uint32_t r = blockIdx.x / tiles_per_row;
-  const uint32_t local = blockIdx.x - r * tiles_per_row;
-  const bool write_grad = a.k.x.data[1] != nullptr;
-  const bool active = a.k.vec.mask[r] != 0;
-  const int s = segment_of_tile(a.seg.tile0, a.seg.n, local);
-  // A segment without data is a gap between gradients: its columns take the
-  // gradient already in the consolidated buffer, or zero when there is none.
-  const bool gap = a.seg.data[s] == nullptr;
-  if (!active && (gap || !write_grad)) {
-    return;
-  }
-  const int64_t numel = a.seg.numel[s];
-  const int64_t col = a.seg.col[s];
-  const int64_t j0 = int64_t(local - a.seg.tile0[s]) * kSegTile;
-  const bool vec = (a.seg.vec_ok >> s) & 1u;
-  // Row r of the segment's columns in the (R, T) operands, and of its gradient
-  // source: the segment's row, or for a gap the consolidated buffer (null:
-  // zero). Only a real segment is stored into the consolidated buffer.
-  T* const g_dst =
-      write_grad ? pg_row<P>(a.k.x, 1, r) + col * a.k.x.stride_t[1] : nullptr;
-  const T* g_src = g_dst;
-  int64_t g_stride = write_grad ? a.k.x.stride_t[1] : 0;
-  if (!gap) {
-    g_src = a.seg.data[s] + int64_t(r) * a.seg.stride_r[s];
-    g_stride = 1;
-  }
-  const bool store_grad = write_grad && !gap;
-
-  if (!active) {
-    // A frozen replica's optimizer state is not touched, but the consolidated
-    // gradient is still filled, as the separate scatter would have filled it.
-    if (vec) {
-      const SegTile t = seg_tile<T, kSegTile>(a.k.g.res0, a.k.g.rmod, r, col, numel, j0);
-#pragma unroll
-      for (int u = 0; u < U; ++u) {
-        const int64_t i = int64_t(u) * kThreads + threadIdx.x;
-        if (i < t.packs) {
-          Packs<ANY, T>(g_dst + t.first).store(i, load_stream_any(g_src + t.first + i * kPack));
-        }
-      }
-      seg_singles(t, numel, [&](int64_t j) { g_dst[j] = g_src[j]; });
-    } else {
-      const int64_t cnt = imin(kSegTile, numel - j0);
-      for (int64_t j = j0 + threadIdx.x; j < j0 + cnt; j += kThreads) {
-        g_dst[j * a.k.x.stride_t[1]] = g_src[j];
-      }
-    }
-    return;
-  }
-
-  typename P::Rep rep;
-  P::template prologue<PRE>(a.k.vec, r, rep);
-  const bool load_state = P::reads_state(a.k.vec, r);
-  const T zero = narrow<T>(op_t<T>(0));
-
-  T* const prow = pg_row<P>(a.k.x, 0, r) + col * a.k.x.stride_t[0];
-  S* srow[SS];
-#pragma unroll
-  for (int b = 0; b < NS; ++b) {
-    srow[b] = state_row<P>(a.k.x, 2 + b, r) + col * a.k.x.stride_t[2 + b];
-  }
-
-  // Element j of the segment, one access per operand.
-  const auto one = [&](int64_t j) {
-    T p = prow[j * a.k.x.stride_t[0]];
-    const T g = g_src != nullptr ? g_src[j * g_stride] : zero;
-    S st[SS];
-    if (load_state) {
-#pragma unroll
-      for (int b = 0; b < NS; ++b) st[b] = srow[b][j * a.k.x.stride_t[2 + b]];
-    }
-    apply_element<P>(p, g, st, load_state, rep, a.k.maximize);
-    prow[j * a.k.x.stride_t[0]] = p;
-    if (store_grad) {
-      g_dst[j * a.k.x.stride_t[1]] = g;
-    }
-#pragma unroll
-    for (int b = 0; b < NS; ++b) srow[b][j * a.k.x.stride_t[2 + b]] = st[b];
-  };
-
-  if (!vec) {
-    const int64_t cnt = imin(kSegTile, numel - j0);
-    for (int64_t j = j0 + threadIdx.x; j < j0 + cnt; j += kThreads) one(j);
-    return;
-  }
-
-  // Vector walk (unit inner strides): the parameters' packs are aligned; with
-  // ANY the other operands sit at another 16-byte phase (element-aligned packs).
-  const SegTile t = seg_tile<T, kSegTile>(a.k.g.res0, a.k.g.rmod, r, col, numel, j0);
-  Pack<T>* const pp = reinterpret_cast<Pack<T>*>(prow + t.first);
-  Packs<ANY, S> sp[SS];
-#pragma unroll
-  for (int b = 0; b < NS; ++b) sp[b] = Packs<ANY, S>(srow[b] + t.first);
-  const Packs<ANY, T> gout(g_dst != nullptr ? g_dst + t.first : nullptr);
-  Pack<T> vp[U], vg[U];
-  Pack<S> vs[SS][U];
-#pragma unroll
-  for (int u = 0; u < U; ++u) {
-    const int64_t i = int64_t(u) * kThreads + threadIdx.x;
-    if (i < t.packs) {
-      vp[u] = load_stream(pp + i);
-      if (gap) {
-        if (g_src != nullptr) {
-          vg[u] = gout.load(i);  // a gap reads the consolidated gradient
-        } else {
-#pragma unroll
-          for (int k = 0; k < kPack; ++k) vg[u].v[k] = zero;
-        }
-      } else {
-        vg[u] = load_stream_any(g_src + t.first + i * kPack);
-      }
-      if (load_state) {
-#pragma unroll
-        for (int b = 0; b < NS; ++b) vs[b][u] = sp[b].load(i);
-      }
-    }
-  }
-#pragma unroll
-  for (int u = 0; u < U; ++u) {
-    const int64_t i = int64_t(u) * kThreads + threadIdx.x;
-    if (i < t.packs) {
-      if (store_grad) {
-        gout.store(i, vg[u]);
-      }
-#pragma unroll
-      for (int k = 0; k < kPack; ++k) {
-        S st[SS];
-#pragma unroll
-        for (int b = 0; b < NS; ++b) st[b] = vs[b][u].v[k];
-        apply_element<P>(vp[u].v[k], vg[u].v[k], st, load_state, rep, a.k.maximize);
-#pragma unroll
-        for (int b = 0; b < NS; ++b) vs[b][u].v[k] = st[b];
-      }
-      store_stream(pp + i, vp[u]);
-#pragma unroll
-      for (int b = 0; b < NS; ++b) sp[b].store(i, vs[b][u]);
-    }
-  }
-  seg_singles(t, numel, one);
-}
-
-// Plain gradient scatter: copies every segment into its columns of the (R, T)
-// destination, every row (frozen replicas included, as a copy would). The
-// vector walk follows the destination's 256-byte boundaries (res0 / rmod as
-// for the update).
-template <typename T>
-struct ScatterArgs {
-  T* dst;
-  int64_t dst_stride_r;
-  uint32_t res0, rmod;
-  Segments<T> seg;
-};
-
-template <typename T>
-__global__ __launch_bounds__(kThreads) void scatter_kernel(ScatterArgs<T> a) {
-  const uint32_t tiles_per_row = a.seg.tile0[a.seg.n];
-  const uint32_t r = blockIdx.x / tiles_per_row;
-  const uint32_t local = blockIdx.x - r * tiles_per_row;
-  const int s = segment_of_tile(a.seg.tile0, a.seg.n, local);
-  const int64_t numel = a.seg.numel[s];
-  const int64_t j0 = int64_t(local - a.seg.tile0[s]) * kTile;
-  const T* src = a.seg.data[s] + int64_t(r) * a.seg.stride_r[s];
-  T* dst = a.dst + int64_t(r) * a.dst_stride_r + a.seg.col[s];
-  if ((a.seg.vec_ok >> s) & 1u) {
-    const SegTile t = seg_tile<T, kTile>(a.res0, a.rmod, r, a.seg.col[s], numel, j0);
-    Pack<T> v[kUnroll];
-#pragma unroll
-    for (int u = 0; u < kUnroll; ++u) {
-      const int64_t i = int64_t(u) * kThreads + threadIdx.x;
-      if (i < t.packs) v[u] = load_stream_any(src + t.first + i * kPack);
-    }
-#pragma unroll
-    for (int u = 0; u < kUnroll; ++u) {
-      const int64_t i = int64_t(u) * kThreads + threadIdx.x;
-      if (i < t.packs) store_stream(reinterpret_cast<Pack<T>*>(dst + t.first) + i, v[u]);
-    }
-    seg_singles(t, numel, [&](int64_t j) { dst[j] = src[j]; });
-    return;
-  }
-  const int64_t cnt = imin(kTile, numel - j0);
-  for (int64_t j = j0 + threadIdx.x; j < j0 + cnt; j += kThreads) {
-    dst[j] = src[j];
-  }
-}
-
-// ---------------------------------------------------------------------------
-// state_steps += active_mask, and the zero return scalar.
-// ---------------------------------------------------------------------------
-template <typename T>
-__global__ __launch_bounds__(kThreads) void bump_steps_kernel(
-    T* __restrict__ steps, const uint8_t* __restrict__ mask, int64_t R,
-    T* __restrict__ out_zero) {
-  const int64_t r = int64_t(blockIdx.x) * kThreads + threadIdx.x;
-  if (r < R) {
-    const op_t<T> one = mask[r] ? op_t<T>(1) : op_t<T>(0);
-    steps[r] = narrow<T>(widen(steps[r]) + one);
-  }
-  if (out_zero != nullptr && r == 0) {
-    *out_zero = narrow<T>(op_t<T>(0));
-  }
-}
-
-// The preparation launch of a call with a workspace: the optional step bump
-// (as bump_steps_kernel), then each active replica's constants from the
-// stored, bumped step into pre + kPreStride * r (frozen replicas' entries are
-// neither written nor read), and the zero result. `v.steps` points at `steps`.
-template <typename P>
-__global__ __launch_bounds__(kThreads) void prep_kernel(Vectors<typename P::T> v,
-                                                        typename P::T* steps, int64_t R,
-                                                        bool bump, double* pre,
-                                                        typename P::T* out_zero) {
-  using T = typename P::T;
-  const int64_t r = int64_t(blockIdx.x) * kThreads + threadIdx.x;
-  if (r < R) {
-    const bool active = v.mask[r] != 0;
-    if (bump) {
-      const op_t<T> one = active ? op_t<T>(1) : op_t<T>(0);
-      steps[r] = narrow<T>(widen(steps[r]) + one);
-    }
-    if (active) {
-      P::precompute(v, static_cast<uint32_t>(r), pre + kPreStride * r);
-    }
-  }
-  if (out_zero != nullptr && r == 0) {
-    *out_zero = narrow<T>(op_t<T>(0));
-  }
-}
-
-// ---------------------------------------------------------------------------
-// Host side
-// ---------------------------------------------------------------------------
-constexpr int kInvalid = static_cast<int>(hipErrorInvalidValue);
-
-template <typename T>
-bool fill_operands(const ts_rt_buf* bufs, int n, Operands<T>& x, bool grad_optional) {
-  for (int b = 0; b < kMaxOperands; ++b) {
-    x.data[b] = nullptr;
-    x.stride_r[b] = 0;
-    x.stride_t[b] = 1;
-  }
-  for (int b = 0; b < n; ++b) {
-    if (bufs[b].data == nullptr) {
-      if (b == 1 && grad_optional) continue;
-      return false;
-    }
-    x.data[b] = static_cast<T*>(bufs[b].data);
-    x.stride_r[b] = bufs[b].stride_r;
-    x.stride_t[b] = bufs[b].stride_t;
-  }
-  return true;
-}
-
-// The streaming drivers take any operands with unit inner stride and
-// element-aligned bases. The walk follows the parameters' 256-byte boundaries
-// (res0 / rmod: their phase modulo 256 bytes, for the grid); operands at
-// another phase use element-aligned packs.
-template <typename P>
-bool rows_streamable(const Operands<typename P::T>& x, int n, uint32_t& res0, uint32_t& rmod) {
-  constexpr uint32_t A = align_elems<typename P::T>();
-  for (int b = 0; b < n; ++b) {
-    if (x.data[b] == nullptr) continue;
-    const size_t elem = b < 2 ? sizeof(typename P::T) : sizeof(typename P::S);
-    const uintptr_t addr = reinterpret_cast<uintptr_t>(x.data[b]);
-    if (x.stride_t[b] != 1 || addr % elem != 0) return false;
-  }
-  const uintptr_t p0 = reinterpret_cast<uintptr_t>(x.data[0]);
-  res0 = static_cast<uint32_t>((p0 / sizeof(typename P::T)) % A);
-  rmod = static_cast<uint32_t>(((x.stride_r[0] % A) + A) % A);
-  return true;
-}
-
-// Whether every present operand's 16-byte boundaries fall on the same element
-// index as the parameters' in every row (common base residue and row stride
-// modulo 4): then all packs are aligned and the drivers' ANY = false variants
-// run.
-template <typename P>
-bool rows_same_phase(const Operands<typename P::T>& x, int n) {
-  const auto residue = [&](int b) {
-    const size_t elem = b < 2 ? sizeof(typename P::T) : sizeof(typename P::S);
-    return static_cast<uint32_t>((reinterpret_cast<uintptr_t>(x.data[b]) / elem) % kPack);
-  };
-  const auto mod = [&](int b) {
-    return static_cast<uint32_t>(((x.stride_r[b] % kPack) + kPack) % kPack);
-  };
-  for (int b = 1; b < n; ++b) {
-    if (x.data[b] == nullptr) continue;
-    if (residue(b) != residue(0) || mod(b) != mod(0)) return false;
-  }
-  return true;
-}
-
-// Every present operand has unit replica stride (and R > 1, where that says
-// anything): the column driver's layout.
-template <typename T>
-bool replica_minor(const Operands<T>& x, int n) {
-  for (int b = 0; b < n; ++b) {
-    if (x.data[b] != nullptr && x.stride_r[b] != 1) return false;
-  }
-  return true;
-}
-
-bool make_col_grid(int64_t R, int64_t T, ColGrid& g, uint32_t& blocks) {
-  if (R <= 1 || R > INT32_MAX || T <= 0) return false;
-  g.R = R;
-  g.T = T;
-  g.threads = kColThreads;
-  if (R > kColThreads) {
-    // 256-thread replica blocks that would leave over a quarter of their
-    // threads idle (R = 257..341, 513..682, ...) give way to 128.
-    const int64_t span = (R + kColThreads - 1) / kColThreads * kColThreads;
-    if (4 * (span - R) > span) g.threads = kColThreadsNarrow;
-  }
-  g.rb = static_cast<uint32_t>(std::min<int64_t>(R, g.threads));
-  g.cpi = g.threads / g.rb;
-  const int64_t n_rblocks = (R + g.rb - 1) / g.rb;
-  const int64_t cols_per_block = int64_t(g.cpi) * kColIters;
-  const int64_t n_cblocks = (T + cols_per_block - 1) / cols_per_block;
-  if (n_rblocks > INT32_MAX / n_cblocks) return false;
-  g.n_rblocks = static_cast<uint32_t>(n_rblocks);
-  blocks = static_cast<uint32_t>(n_rblocks * n_cblocks);
-  return true;
-}
-
-// No cache line of the column driver's operands is shared between two
-// workgroups: one replica block per column, or replica blocks, columns and
-// bases all on 128-byte boundaries.
-template <typename P>
-bool col_lines_private(const Operands<typename P::T>& x, int n, const ColGrid& g) {
-  if (g.n_rblocks == 1) return true;
-  for (int b = 0; b < n; ++b) {
-    if (x.data[b] == nullptr) continue;
-    const size_t es = b < 2 ? sizeof(typename P::T) : sizeof(typename P::S);
-    if (reinterpret_cast<uintptr_t>(x.data[b]) % kLineBytes != 0 ||
-        uint64_t(x.stride_t[b]) * es % kLineBytes != 0 || g.rb * es % kLineBytes != 0) {
-      return false;
-    }
-  }
-  return true;
-}
-
-bool make_grid(int64_t R, int64_t T, int64_t tile, Grid& g, uint32_t& blocks) {
-  const int64_t tiles = (T + tile - 1) / tile;
-  if (R <= 0 || T <= 0 || tiles > INT32_MAX || R > INT32_MAX / tiles) {
-    return false;
-  }
-  g.T = T;
-  g.tiles_per_row = static_cast<uint32_t>(tiles);
-  g.res0 = 0;
-  g.rmod = 0;
-  blocks = static_cast<uint32_t>(R * tiles);
-  return true;
-}
-
-template <typename T>
-int launch_bump(void* steps, const uint8_t* mask, int64_t R, void* out_zero,
-                hipStream_t stream) {
-  const int64_t blocks = R > 0 ? (R + kThreads - 1) / kThreads : 1;
-  if (blocks > INT32_MAX) {
-    return kInvalid;
-  }
-  hipLaunchKernelGGL(bump_steps_kernel<T>, dim3(static_cast<uint32_t>(blocks)),
-                     dim3(kThreads), 0, stream, static_cast<T*>(steps), mask, R,
-                     static_cast<T*>(out_zero));
-  return static_cast<int>(hipGetLastError());
-}
-
-// A caller's segment table: in column order, disjoint, inside [0, cols), with
-// data for every non-empty segment (two tiles writing one column would race).
-// One pass, no allocation.
-bool segments_valid(const ts_segment* segs, int n, int64_t cols) {
-  int64_t end = 0;
-  for (int i = 0; i < n; ++i) {
-    const ts_segment& s = segs[i];
-    if (s.numel < 0 || s.col < 0 || s.col > cols - s.numel) return false;
-    if (s.numel == 0) continue;
-    if (s.data == nullptr || s.col < end) return false;
-    end = s.col + s.numel;
-  }
-  return true;
-}
-
-// Walks a valid table in column order, skipping empty segments. With `gaps`,
-// the column ranges no segment covers (between segments and after the last
-// one, up to `cols`) come out as entries without data.
-struct SegmentWalk {
-  const ts_segment* segs;
-  int n;
-  int64_t cols;
-  bool gaps;
-  int i = 0;
-  int64_t at = 0;
-
-  bool next(ts_segment& out) {
-    while (i < n && segs[i].numel == 0) ++i;
-    const int64_t stop = i < n ? segs[i].col : cols;
-    if (gaps && at < stop) {
-      out = ts_segment{nullptr, 0, at, stop - at};
-      at = stop;
-      return true;
-    }
-    if (i == n) return false;
-    out = segs[i++];
-    at = out.col + out.numel;
-    return true;
-  }
-};
-
-// Fills the next launch's table, up to kMaxSegments entries, from the walk;
-// returns the grid size (0 when the walk is done, -1 when it exceeds the 1-D
-// grid). `vec_rows` says whether the (R, T) operands allow vector access.
-template <typename T>
-int64_t next_chunk(SegmentWalk& w, int64_t R, int64_t tile, bool vec_rows, Segments<T>& out) {
-  out.n = 0;
-  out.vec_ok = 0;
-  uint64_t tiles = 0;
-  ts_segment s;
-  while (out.n < kMaxSegments && w.next(s)) {
-    const int k = out.n++;
-    out.data[k] = static_cast<const T*>(s.data);
-    out.stride_r[k] = s.stride_r;
-    out.col[k] = s.col;
-    out.numel[k] = s.numel;
-    out.tile0[k] = static_cast<uint32_t>(tiles);
-    tiles += static_cast<uint64_t>((s.numel + tile - 1) / tile);
-    if (tiles > UINT32_MAX) return -1;
-    const bool ok = vec_rows && reinterpret_cast<uintptr_t>(s.data) % sizeof(T) == 0;
-    out.vec_ok |= (ok ? uint64_t(1) : uint64_t(0)) << k;
-  }
-  out.tile0[out.n] = static_cast<uint32_t>(tiles);
-  const uint64_t blocks = tiles * static_cast<uint64_t>(R);
-  return blocks > INT32_MAX ? -1 : static_cast<int64_t>(blocks);
-}
-
-// Checks that every launch of a walk fits the grid, without launching.
-template <typename T>
-bool walk_fits(SegmentWalk w, int64_t R, int64_t tile, bool vec_rows, Segments<T>& scratch) {
-  int64_t blocks;
-  while ((blocks = next_chunk<T>(w, R, tile, vec_rows, scratch)) != 0 || scratch.n > 0) {
-    if (blocks < 0) return false;
-  }
-  return true;
-}
-
-// Launches `kernel` once per chunk of the walk.
-template <typename T, typename Args, typename Kernel>
-int launch_walk(SegmentWalk w, int64_t R, int64_t tile, bool vec_rows, Args& a, Segments<T>& seg,
-                Kernel kernel, hipStream_t stream, uint32_t lds = 0) {
-  int64_t blocks;
-  while ((blocks = next_chunk<T>(w, R, tile, vec_rows, seg)) != 0 || seg.n > 0) {
-    if (blocks < 0) return kInvalid;
-    if (blocks == 0) continue;
-    hipLaunchKernelGGL(kernel, dim3(static_cast<uint32_t>(blocks)), dim3(kThreads), lds, stream,
-                       a);
-    const int err = static_cast<int>(hipGetLastError());
-    if (err != 0) return err;
-  }
-  return 0;
-}
-
-// A call: the (R, T) operand table, the (R,) vectors, the flags and the
-// optional workspace for per-replica constants.
-struct Call {
-  const ts_rt_buf* bufs;
-  void* steps;
-  const void* h[5];
-  int nh;
-  const uint8_t* mask;
-  int64_t R, T;
-  uint32_t flags;
-  void* out_zero;
-  void* ws;
-  size_t ws_bytes;
-  hipStream_t stream;
-};
-
-// Whether policy P takes its per-replica constants from the call's workspace.
-template <typename P>
-bool uses_workspace(const Call& c) {
-  return P::kPreWords > 0 && c.ws != nullptr;
-}
-
-template <typename P>
-bool fill_kargs(const Call& c, int nbufs, KArgs<P>& a, bool grad_optional) {
-  using T = typename P::T;
-  if (!fill_operands<T>(c.bufs, nbufs, a.x, grad_optional)) return false;
-  a.vec.steps = static_cast<const T*>(c.steps);
-  for (int i = 0; i < 5; ++i) {
-    a.vec.h[i] = i < c.nh ? static_cast<const T*>(c.h[i]) : nullptr;
-    if (i < c.nh && c.h[i] == nullptr) return false;
-  }
-  a.vec.mask = c.mask;
-  a.vec.pre = uses_workspace<P>(c) ? static_cast<const double*>(c.ws) : nullptr;
-  a.maximize = (c.flags & TS_MAXIMIZE) != 0;
-  return true;
-}
-
-template <typename P>
-int launch_prep(const Call& c, const Vectors<typename P::T>& vec) {
-  using T = typename P::T;
-  const int64_t blocks = (c.R + kThreads - 1) / kThreads;
-  if (blocks > INT32_MAX) {
-    return kInvalid;
-  }
-  hipLaunchKernelGGL(prep_kernel<P>, dim3(static_cast<uint32_t>(blocks)), dim3(kThreads), 0,
-                     c.stream, vec, static_cast<T*>(c.steps), c.R,
-                     (c.flags & TS_BUMP_STEPS) != 0, static_cast<double*>(c.ws),
-                     static_cast<T*>(c.out_zero));
-  return static_cast<int>(hipGetLastError());
-}
-
-// Validation, then the preparation launch (the optional bump and the zero
-// result; with a workspace also the per-replica constants), then `launch`
-// when there is any work. Every check happens before the first enqueue, so an
-// invalid call changes nothing. Empty tensors may carry null data pointers, so
-// operands are only required where they are dereferenced: steps and mask when
-// R > 0, the rest (checked by `prepare`, which also fills the kernel arguments
-// in `vec`) when there is at least one element. A workspace must hold
-// kPreStride doubles per replica and be 8-byte aligned.
-template <typename P, typename Prepare, typename Launch>
-int run_step(const Call& c, const Vectors<typename P::T>& vec, Prepare&& prepare,
-             Launch&& launch) {
-  using T = typename P::T;
-  if (c.bufs == nullptr || c.R < 0 || c.T < 0 ||
-      (c.R > 0 && (c.steps == nullptr || c.mask == nullptr))) {
-    return kInvalid;
-  }
-  if (c.ws != nullptr &&
-      (reinterpret_cast<uintptr_t>(c.ws) % alignof(double) != 0 ||
-       c.ws_bytes / (kPreStride * sizeof(double)) < static_cast<uint64_t>(c.R))) {
-    return kInvalid;
-  }
-  const bool work = c.R > 0 && c.T > 0;
-  if (work && !prepare()) {
-    return kInvalid;
-  }
-  if (work && uses_workspace<P>(c)) {
-    const int err = launch_prep<P>(c, vec);
-    if (err != 0) return err;
-  } else if ((c.flags & TS_BUMP_STEPS) != 0 && c.R > 0) {
-    const int err = launch_bump<T>(c.steps, c.mask, c.R, c.out_zero, c.stream);
-    if (err != 0) return err;
-  } else if (c.out_zero != nullptr) {
-    const int err = launch_bump<T>(c.steps, c.mask, 0, c.out_zero, c.stream);
-    if (err != 0) return err;
-  }
-  if (!work) {
-    return 0;
-  }
-  return launch();
-}
-
-// The streaming driver over `blocks` tiles, capped when the launch is large.
-template <typename P, bool PRE, bool SMALL>
-void launch_stream(const KArgs<P>& a, uint32_t blocks, bool same_phase, hipStream_t stream) {
-  const uint32_t lds = int64_t(blocks) * stream_tile<P, PRE, SMALL>() >= kCapMinElems
-                           ? stream_lds_of<P, PRE, SMALL>()
-                           : 0u;
-  if (same_phase) {
-    hipLaunchKernelGGL((stream_kernel<P, false, PRE, SMALL>), dim3(blocks), dim3(kStreamThreads),
-                       lds, stream, a);
-  } else {
-    hipLaunchKernelGGL((stream_kernel<P, true, PRE, SMALL>), dim3(blocks), dim3(kStreamThreads),
-                       lds, stream, a);
-  }
-}
-
-// Consolidated-gradient update with policy P over `nbufs` operands.
-template <typename P>
-int launch_dense(const Call& c, int nbufs) {
-  KArgs<P> a;
-  uint32_t blocks = 0;
-  bool streamable = false;
-  const bool pre = uses_workspace<P>(c);
-  // Operands that fit the MALL (R, T and the types say so, before any launch).
-  // The small shape is built for the forms the operators run: with a
-  // workspace where the policy has one, and for SGD, which has none.
-  const bool small =
-      (pre || P::kPreWords == 0) &&
-      c.R <= P::kStreamSmallBytes / operand_bytes_per_elem<P>() / std::max<int64_t>(c.T, 1);
-  const auto prepare = [&] {
-    if (!fill_kargs<P>(c, nbufs, a, false)) return false;
-    uint32_t res0 = 0, rmod = 0;
-    streamable = rows_streamable<P>(a.x, nbufs, res0, rmod);
-    const int64_t tile = !streamable ? kTile
-                         : small     ? stream_tile<P, false, true>()
-                         : pre       ? stream_tile<P, true, false>()
-                                     : stream_tile<P, false, false>();
-    if (!make_grid(c.R, c.T, tile, a.g, blocks)) return false;
-    a.g.res0 = res0;
-    a.g.rmod = rmod;
-    return true;
-  };
-  return run_step<P>(c, a.vec, prepare, [&]() -> int {
-    const dim3 grid(blocks), block(kThreads);
-    ColArgs<P> ca;
-    uint32_t col_blocks = 0;
-    if (streamable) {
-      const bool same_phase = rows_same_phase<P>(a.x, nbufs);
-      if constexpr (P::kPreWords > 0) {
-        if (pre) {
-          if (small) {
-            launch_stream<P, true, true>(a, blocks, same_phase, c.stream);
-          } else {
-            launch_stream<P, true, false>(a, blocks, same_phase, c.stream);
-          }
-          return static_cast<int>(hipGetLastError());
-        }
-      }
-      if constexpr (P::kPreWords == 0) {
-        if (small) {
-          launch_stream<P, false, true>(a, blocks, same_phase, c.stream);
-          return static_cast<int>(hipGetLastError());
-        }
-      }
-      launch_stream<P, false, false>(a, blocks, same_phase, c.stream);
-    } else if (replica_minor(a.x, nbufs) && make_col_grid(c.R, c.T, ca.g, col_blocks)) {
-      ca.x = a.x;
-      ca.vec = a.vec;
-      ca.maximize = a.maximize;
-      if (col_lines_private<P>(a.x, nbufs, ca.g)) {
-        hipLaunchKernelGGL((column_kernel<P, true>), dim3(col_blocks), dim3(ca.g.threads), 0,
-                           c.stream, ca);
-      } else {
-        hipLaunchKernelGGL((column_kernel<P, false>), dim3(col_blocks), dim3(ca.g.threads), 0,
-                           c.stream, ca);
-      }
-    } else {
-      hipLaunchKernelGGL(element_kernel<P>, grid, block, 0, c.stream, a);
-    }
-    return static_cast<int>(hipGetLastError());
-  });
-}
-
-// Segmented-gradient update with policy P: one launch per kMaxSegments
-// entries of the walk (their columns are disjoint, so the launches are
-// independent). The gaps make the result that of a scatter followed by the
-// consolidated update in every column.
-template <typename P>
-int launch_segments(const Call& c, int nbufs, const ts_segment* segs, int n_segs) {
-  using T = typename P::T;
-  if (n_segs < 0 || (n_segs > 0 && segs == nullptr)) return kInvalid;
-  SegArgs<P> a;
-  bool vec_rows = false;
-  const SegmentWalk walk{segs, n_segs, c.T, true};
-  const auto prepare = [&] {
-    if (!fill_kargs<P>(c, nbufs, a.k, true) || !segments_valid(segs, n_segs, c.T)) {
-      return false;
-    }
-    a.k.g = Grid{c.T, 0, 0, 0};
-    vec_rows = rows_streamable<P>(a.k.x, nbufs, a.k.g.res0, a.k.g.rmod);
-    return walk_fits<T>(walk, c.R, segment_tile<P>(), vec_rows, a.seg);
-  };
-  return run_step<P>(c, a.k.vec, prepare, [&]() -> int {
-    const bool same_phase = rows_same_phase<P>(a.k.x, nbufs);
-    // with precomputed constants, large launches take the policy's residency
-    // reservation (kSegmentLds)
-    const uint32_t lds = c.R * c.T >= kCapMinElems ? P::kSegmentLds : 0u;
-    if constexpr (P::kPreWords > 0) {
-      if (uses_workspace<P>(c)) {
-        return same_phase ? launch_walk<T>(walk, c.R, segment_tile<P>(), vec_rows, a, a.seg,
-                                           segment_kernel<P, false, true>, c.stream, lds)
-                          : launch_walk<T>(walk, c.R, segment_tile<P>(), vec_rows, a, a.seg,
-                                           segment_kernel<P, true, true>, c.stream, lds);
-      }
-    }
-    return same_phase ? launch_walk<T>(walk, c.R, segment_tile<P>(), vec_rows, a, a.seg,
-                                       segment_kernel<P, false, false>, c.stream)
-                      : launch_walk<T>(walk, c.R, segment_tile<P>(), vec_rows, a, a.seg,
-                                       segment_kernel<P, true, false>, c.stream);
-  });
-}
 
 // Runs `launch` with the policy that matches the call's flags and the number
 // of (R, T) operands that policy reads.
@@ -1856,24 +157,6 @@ struct BumpBody {
   }
 };
 
-Call make_call(const ts_rt_buf* bufs, void* steps, std::initializer_list<const void*> h,
-               const uint8_t* mask, int64_t R, int64_t T, uint32_t flags, void* out_zero,
-               void* stream, void* ws = nullptr, size_t ws_bytes = 0) {
-  Call c;
-  c.ws = ws;
-  c.ws_bytes = ws_bytes;
-  c.bufs = bufs;
-  c.steps = steps;
-  c.nh = 0;
-  for (const void* p : h) c.h[c.nh++] = p;
-  c.mask = mask;
-  c.R = R;
-  c.T = T;
-  c.flags = flags;
-  c.out_zero = out_zero;
-  c.stream = static_cast<hipStream_t>(stream);
-  return c;
-}
 
 // Replicas whose per-replica constants fit ts_adam_step_noalloc's scratch.
 constexpr int64_t kScratchReplicas = 65536;
