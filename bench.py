@@ -482,6 +482,38 @@ def bf16_state_timing(cfg: int, launches: int):
             "step_equivalent_GBs": round(active * T * bytes_per_elem(cfg) / (ms * 1e-3) / 1e9, 1)}
 
 
+def bf16_state_shared_timing(adam_args, launches: int):
+    """`bf16_state_timing` for config 5 on the float32 update's own buffers:
+    params and grads as they are, the bfloat16 moments (the float32 moments
+    narrowed) in the first half of the float32 moments' storage
+    (`half_view`). The same pages as the float32 update, so the comparison
+    with it is not one between two placements of the buffers in HBM.
+    Overwrites the moments."""
+    import torch
+
+    p, gr, m, v = adam_args[:4]
+    mask = adam_args[11]
+    T = p.shape[1]
+    narrowed = (m.to(torch.bfloat16), v.to(torch.bfloat16))
+    mb, vb = half_view(m, torch.bfloat16), half_view(v, torch.bfloat16)
+    mb.copy_(narrowed[0])
+    vb.copy_(narrowed[1])
+    del narrowed
+    args = (p, gr, mb, vb, *adam_args[4:])
+    ms = kernel_only_timing("adam", args, {"amsgrad": False, "maximize": False,
+                                           "decoupled_weight_decay": False},
+                            launches, extra_flags=TS_STATE_BF16)
+    torch.cuda.empty_cache()
+    per_elem = 20
+    nbytes = int(mask.sum().item()) * T * per_elem
+    return {"kernel_avg_ms": round(ms, 4), "bytes_per_elem": per_elem,
+            "achieved_GBs": round(nbytes / (ms * 1e-3) / 1e9, 1),
+            "frac": round(nbytes / (ms * 1e-3) / 1e9 / HBM_PEAK_GBS, 4),
+            "step_equivalent_GBs": round(int(mask.sum().item()) * T * bytes_per_elem(5)
+                                         / (ms * 1e-3) / 1e9, 1),
+            "storage": "first half of the float32 moments' buffers"}
+
+
 def other_ops_timing(adam_args, launches: int):
     """SGD with momentum and Adagrad on the config-5 buffers (kernel-only time,
     20 B per active element each): the Adam state's moments serve as the
@@ -562,31 +594,53 @@ def ceiling_timing(adam_args, launches: int):
     return out
 
 
-def low_precision_timing(launches: int):
+def half_view(t32, dtype):
+    """The first half of a contiguous float32 (N, T) buffer's bytes as an
+    (N, T) tensor of a 2-byte type: the same physical pages as the start of
+    the float32 buffer."""
+    return t32.view(-1).view(dtype)[: t32.numel()].view(t32.shape)
+
+
+def low_precision_timing(adam_args, launches: int):
     """Adam with float16 and with bfloat16 parameters (state in the parameter
     dtype, as torch keeps it) at the config-5 shape and mask: kernel-only time
-    and effective GB/s of 14 B per active element. The buffers are the config's
-    float32 values narrowed, one dtype at a time; for float16 eps is 1e-4 (the
-    config's 1e-8 is 0 in half precision, which turns lanes with a zero
-    exp_avg_sq into NaN)."""
+    and effective GB/s of 14 B per active element. The 16-bit buffers occupy
+    the first half of the float32 update's own buffers (`half_view`), so the
+    comparison with the float32 update is not one between two placements of
+    the buffers in HBM (which alone moves the same kernel by up to +-6%):
+    params and grads are the float32 values narrowed, the moments start at
+    zero. For float16 eps is 1e-4 (the config's 1e-8 is 0 in half precision,
+    which turns lanes with a zero exp_avg_sq into NaN). Overwrites the float32
+    buffers."""
     import torch
 
+    p, gr, m, v = adam_args[:4]
+    vecs = adam_args[5:11]
+    mask = adam_args[11]
+    T = p.shape[1]
+    nb = int(mask.sum().item()) * T * 14
+    dts = (("f16", torch.float16, 2), ("bf16", torch.bfloat16, 3))
+    narrowed = {name: (p.to(dt), gr.to(dt)) for name, dt, _ in dts}  # before any overwrite
     out = {}
-    for name, dt, code in (("f16", torch.float16, 2), ("bf16", torch.bfloat16, 3)):
-        op_name, args, kw, nbytes = make_config(5)
-        args = [t.to(dt) if t is not None and t.is_floating_point() else t for t in args]
+    for name, dt, code in dts:
+        views = [half_view(t, dt) for t in (p, gr, m, v)]
+        views[0].copy_(narrowed[name][0])
+        views[1].copy_(narrowed[name][1])
+        views[2].zero_()
+        views[3].zero_()
+        hyp = [t.to(dt) for t in vecs]
         if dt == torch.float16:
-            args[9].fill_(1e-4)  # eps
-        T = args[0].shape[1]
-        active = int(args[-1].sum().item())
-        nb = active * T * 14
-        ms = kernel_only_timing(op_name, tuple(args), kw, launches, dtype_code=code)
+            hyp[4].fill_(1e-4)  # eps
+        args = (*views, None, *hyp, mask)
+        ms = kernel_only_timing("adam", args, {"amsgrad": False, "maximize": False,
+                                               "decoupled_weight_decay": False},
+                                launches, dtype_code=code)
         gbs = nb / (ms * 1e-3) / 1e9
         out[name] = {"kernel_avg_ms": round(ms, 4), "bytes_per_elem": 14,
                      "achieved_GBs": round(gbs, 1), "frac": round(gbs / HBM_PEAK_GBS, 4),
-                     "eps": float(args[9][0])}
-        del args
-        torch.cuda.empty_cache()
+                     "eps": float(hyp[4][0])}
+    del narrowed
+    torch.cuda.empty_cache()
     return out
 
 
@@ -830,6 +884,15 @@ def main():
                if op_name in ("adam", "adagrad") else None)
     other_ops = (other_ops_timing(op_args, max(10, args.steps // 2))
                  if args.config == 5 and not args.no_other_ops else None)
+    # 16-bit variants on the same buffers (they overwrite them), then the
+    # traffic ceiling, which overwrites them too
+    bf16 = None
+    low_prec = None
+    if args.config == 5:
+        if not args.no_bf16_state:
+            bf16 = bf16_state_shared_timing(op_args, max(10, args.steps // 2))
+        if not args.no_low_precision:
+            low_prec = low_precision_timing(op_args, max(10, args.steps // 2))
     ceiling = (ceiling_timing(op_args, max(10, args.steps // 2))
                if args.config == 5 and not args.no_ceiling else None)
     if ceiling is not None:
@@ -870,14 +933,11 @@ def main():
     snapshot = snapshot_timing(args.config) if args.snapshot else None
     graphed = graph_replay_timing(args.config, args.steps) if args.config != 5 else None
 
-    bf16 = None
-    if not args.no_bf16_state and args.config != 3:
+    if not args.no_bf16_state and args.config not in (3, 5):
         bf16 = bf16_state_timing(args.config, max(10, args.steps // 2))
 
     minor = None if args.no_replica_minor else replica_minor_timing(args.config,
                                                                     max(10, args.steps // 2))
-    low_prec = (low_precision_timing(max(10, args.steps // 2))
-                if args.config == 5 and not args.no_low_precision else None)
 
     scatter = None
     if not args.no_grad_scatter and op_name == "adam":

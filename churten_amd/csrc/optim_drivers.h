@@ -10,10 +10,11 @@
 //
 //   stream_kernel   unit inner stride (the consolidated layout `State`
 //                   produces, and ragged or misaligned rows): one wavefront
-//                   per tile (1-8 packs per thread by operand types),
-//                   non-temporal 16-byte loads and stores from each row's
-//                   first 256-byte boundary (tiles never share a cache line),
-//                   the few head and tail elements of a row one at a time;
+//                   per tile (1-4 packs of 4 or 8 elements per thread by
+//                   operand types), non-temporal 16-byte loads and stores
+//                   from each row's first 256-byte boundary (tiles never
+//                   share a cache line), the few head and tail elements of a
+//                   row one at a time;
 //                   large launches cap residency per CU. Operands at another
 //                   16-byte phase than the parameters take element-aligned
 //                   packs (the ANY variant).
@@ -103,15 +104,18 @@ constexpr uint32_t align_elems() {
   return kAlignBytes / sizeof(T);
 }
 
-template <typename T>
-struct alignas(sizeof(T) * kPack) Pack {
-  T v[kPack];
+// N consecutive elements of one operand: 4 in the drivers' usual pack (16 B
+// for float32, 8 B for 16-bit types, 32 B for float64); the streaming driver
+// takes 8 where a policy has 16-bit operands (kStreamPack), so those move
+// 16 B per access too.
+template <typename T, int N = kPack>
+struct alignas(sizeof(T) * N) Pack {
+  T v[N];
 };
 
-// A pack as raw 32-bit words, so it can go through the non-temporal builtins
-// (16 B for fp32, 8 B for 16-bit types, 32 B for fp64).
-template <typename T>
-using PackBits = uint32_t __attribute__((ext_vector_type(sizeof(T) * kPack / 4)));
+// A pack as raw 32-bit words, so it can go through the non-temporal builtins.
+template <typename T, int N = kPack>
+using PackBits = uint32_t __attribute__((ext_vector_type(sizeof(T) * N / 4)));
 
 // Streaming accesses: every byte of the optimizer state is touched exactly
 // once per step, so the loads and stores carry the non-temporal hint (NT).
@@ -135,14 +139,15 @@ __device__ __forceinline__ void store_bits(V* p, V v) {
   }
 }
 
-template <bool NT = true, typename T>
-__device__ __forceinline__ Pack<T> load_stream(const Pack<T>* p) {
-  return __builtin_bit_cast(Pack<T>, load_bits<NT>(reinterpret_cast<const PackBits<T>*>(p)));
+template <bool NT = true, typename T, int N>
+__device__ __forceinline__ Pack<T, N> load_stream(const Pack<T, N>* p) {
+  return __builtin_bit_cast(Pack<T, N>,
+                            load_bits<NT>(reinterpret_cast<const PackBits<T, N>*>(p)));
 }
 
-template <bool NT = true, typename T>
-__device__ __forceinline__ void store_stream(Pack<T>* p, const Pack<T>& v) {
-  store_bits<NT>(reinterpret_cast<PackBits<T>*>(p), __builtin_bit_cast(PackBits<T>, v));
+template <bool NT = true, typename T, int N>
+__device__ __forceinline__ void store_stream(Pack<T, N>* p, const Pack<T, N>& v) {
+  store_bits<NT>(reinterpret_cast<PackBits<T, N>*>(p), __builtin_bit_cast(PackBits<T, N>, v));
 }
 
 // Packs at addresses that are only element-aligned: operands whose 16-byte
@@ -151,43 +156,45 @@ __device__ __forceinline__ void store_stream(Pack<T>* p, const Pack<T>& v) {
 // access mode, and hipcc emits the same single global_load/store_dwordx4
 // (dwordx2 for 16-bit types) for these types as for an aligned pack; on an
 // aligned address the access is the aligned one.
-template <typename T>
+template <typename T, int N = kPack>
 using PackBitsU = uint32_t
-    __attribute__((ext_vector_type(sizeof(T) * kPack / 4), aligned(sizeof(T))));
+    __attribute__((ext_vector_type(sizeof(T) * N / 4), aligned(sizeof(T))));
 
-template <bool NT = true, typename T>
-__device__ __forceinline__ Pack<T> load_stream_any(const T* p) {
-  return __builtin_bit_cast(Pack<T>, load_bits<NT>(reinterpret_cast<const PackBitsU<T>*>(p)));
+template <bool NT = true, int N = kPack, typename T>
+__device__ __forceinline__ Pack<T, N> load_stream_any(const T* p) {
+  return __builtin_bit_cast(Pack<T, N>,
+                            load_bits<NT>(reinterpret_cast<const PackBitsU<T, N>*>(p)));
 }
 
-template <bool NT = true, typename T>
-__device__ __forceinline__ void store_stream_any(T* p, const Pack<T>& v) {
-  store_bits<NT>(reinterpret_cast<PackBitsU<T>*>(p), __builtin_bit_cast(PackBitsU<T>, v));
+template <bool NT = true, int N = kPack, typename T>
+__device__ __forceinline__ void store_stream_any(T* p, const Pack<T, N>& v) {
+  store_bits<NT>(reinterpret_cast<PackBitsU<T, N>*>(p), __builtin_bit_cast(PackBitsU<T, N>, v));
 }
 
-// The packs of an operand from a given element on: 16-byte aligned wherever
-// the parameters' packs are (ANY = false, the usual case: the compiler knows
-// the alignment) or only element-aligned (ANY = true). Indexed by pack.
-template <bool ANY, typename T, bool NT = true>
+// The N-element packs of an operand from a given element on: aligned to the
+// pack wherever the parameters' packs are (ANY = false, the usual case: the
+// compiler knows the alignment) or only element-aligned (ANY = true). Indexed
+// by pack.
+template <bool ANY, typename T, bool NT = true, int N = kPack>
 struct Packs;
 
-template <typename T, bool NT>
-struct Packs<false, T, NT> {
-  Pack<T>* p = nullptr;
+template <typename T, bool NT, int N>
+struct Packs<false, T, NT, N> {
+  Pack<T, N>* p = nullptr;
   Packs() = default;
-  __device__ explicit Packs(T* e) : p(reinterpret_cast<Pack<T>*>(e)) {}
-  __device__ Pack<T> load(int64_t i) const { return load_stream<NT>(p + i); }
-  __device__ void store(int64_t i, const Pack<T>& v) const { store_stream<NT>(p + i, v); }
+  __device__ explicit Packs(T* e) : p(reinterpret_cast<Pack<T, N>*>(e)) {}
+  __device__ Pack<T, N> load(int64_t i) const { return load_stream<NT>(p + i); }
+  __device__ void store(int64_t i, const Pack<T, N>& v) const { store_stream<NT>(p + i, v); }
 };
 
-template <typename T, bool NT>
-struct Packs<true, T, NT> {
+template <typename T, bool NT, int N>
+struct Packs<true, T, NT, N> {
   T* p = nullptr;
   Packs() = default;
   __device__ explicit Packs(T* e) : p(e) {}
-  __device__ Pack<T> load(int64_t i) const { return load_stream_any<NT>(p + i * kPack); }
-  __device__ void store(int64_t i, const Pack<T>& v) const {
-    store_stream_any<NT>(p + i * kPack, v);
+  __device__ Pack<T, N> load(int64_t i) const { return load_stream_any<NT, N>(p + i * N); }
+  __device__ void store(int64_t i, const Pack<T, N>& v) const {
+    store_stream_any<NT, N>(p + i * N, v);
   }
 };
 
@@ -221,8 +228,8 @@ constexpr int kPreStride = 2;
 // (A: 256 bytes in elements of the parameter type; res0: the parameter base's
 // element offset modulo A, rmod: its row stride modulo A); packs stream from
 // there and the head and the at most three tail elements of each row go one at
-// a time. Every operand shares the parameter's phase modulo 4, so the packs are
-// 16-byte aligned in all of them.
+// a time. Where every operand shares the parameter's phase modulo the pack, the
+// packs are aligned in all of them (else the ANY variants run).
 struct Grid {
   int64_t T;
   uint32_t tiles_per_row;
@@ -295,11 +302,16 @@ constexpr int64_t kMallBytes = int64_t(256) << 20;
 // Packs per thread of the streaming driver, by operand types: float32
 // throughout, float32 params with bfloat16 state, 16-bit params, float64.
 // Measured per policy on config-5-sized state (1/2/4/8 packs, one process per
-// sweep, two sweeps): float32 keeps 2 (under its residency cap); bfloat16
-// state wants 4 for Adam (+13%) but 1 for SGD and Adagrad (+8-15%); 16-bit
-// params 4-8 (+12-22%); float64 is flat. 16-bit Adam and Adagrad moved from
-// 4 to 8 once bfloat16 narrowing became one instruction: Adam +6% (half), +10%
-// (bfloat16); Adagrad +4% (half), +5.5% (bfloat16).
+// sweep, two sweeps): float32 keeps 2 (under its residency cap; 1 with
+// precomputed constants, below); bfloat16 state wants 4 for Adam (+13%) but 1
+// for SGD and Adagrad (+8-15%); float64 is flat. 16-bit params and state take
+// one 8-element (16-byte) pack per thread, uncapped, for large launches.
+// Against the previous 4-element packs x 8 (config-5 buffers, half and
+// bfloat16 timed on the same storage, 5-6 interleaved rounds, three sweeps on
+// different boxes): Adam +4-8% (one box: half -2%), SGD +7-9%, float32-math
+// Adagrad +10-12%, Adagrad -1% to +0.2%; two and four packs per thread and
+// caps of 10-20 were slower on average. Small launches keep 2048-element tiles
+// (four 8-element packs).
 // kLateStores (per policy): the streaming driver stores a thread's packs
 // after all of its arithmetic instead of each pack right after its own.
 // Measured interleaved on the config-5 buffers: Adam +0.6-0.9% (three boxes),
@@ -310,6 +322,16 @@ constexpr int64_t kMallBytes = int64_t(256) << 20;
 // (with float32 or bfloat16 state) of Adam without amsgrad and of SGD store
 // late. The segmented driver keeps per-pack stores for every policy: late
 // ones lost 0.6-0.8% there.
+// Elements per pack of the streaming driver: 8 (16 B) where parameters and
+// state are 16-bit, else 4 (16 B for float32). With float32 parameters next to
+// bfloat16 state a pack stays 4 elements (8 B of state): 8-element packs there
+// make the float32 operands' accesses 32 B apart per lane, measured 5-15%
+// slower on the config-5 buffers.
+template <typename T, typename S>
+constexpr int stream_pack() {
+  return sizeof(T) == 2 && sizeof(S) == 2 ? 8 : kPack;
+}
+
 template <typename T, typename S>
 constexpr int stream_unroll(int fp32, int bf16_state, int narrow, int wide) {
   return std::is_same<T, double>::value ? wide
@@ -332,6 +354,9 @@ constexpr int stream_unroll(int fp32, int bf16_state, int narrow, int wide) {
 // widened to double. kPreWords is the number of such doubles (0: nothing worth
 // hoisting, the policy never reads a workspace). `reads_state` is decided from
 // the (R,) vectors alone, so the drivers issue their loads before the prologue.
+// `decays` / `drop_decay`: whether the replica's weight-decay term is live, and
+// a copy of its constants with the decay set to a literal zero (the element
+// math then skips the term, exactly as it does for a zero decay at run time).
 //
 // Streaming shape with a workspace (kStreamUnrollPre, kStreamLdsPre). Without
 // the pow in every workgroup, float32 Adam runs fastest with one pack per
@@ -348,9 +373,9 @@ constexpr int stream_unroll(int fp32, int bf16_state, int narrow, int wide) {
 //   Adam, bf16 moments   4 packs, cap 12: 6.15-6.31 (uncapped: 5.90-6.23)
 // SGD has no workspace, but with its loads issued before the prologue its
 // buffered float32 form also runs one pack per thread, cap 20: 6.46-6.60
-// against 6.13 for two packs at cap 14. 16-bit parameters (8 packs,
-// uncapped), bfloat16-state SGD and Adagrad (1 pack, uncapped) and float64
-// (2 packs) kept their shapes: nothing else in the sweep beat them.
+// against 6.13 for two packs at cap 14. bfloat16-state SGD and Adagrad (1
+// pack, uncapped) and float64 (2 packs) kept their shapes: nothing else in the
+// sweep beat them. 16-bit parameters: one 8-element pack, uncapped (above).
 
 // Adam / AdamW: h = {lr, beta1, beta2, eps, weight_decay}.
 template <typename T_, bool ADAMW, bool AMSGRAD, typename S_ = T_>
@@ -360,12 +385,13 @@ struct AdamPolicy {
   using M = op_t<T>;
   static constexpr int NS = AMSGRAD ? 3 : 2;
   static constexpr uint32_t kStreamLds = residency_lds<T, S>(AMSGRAD ? 12 : 14);
-  static constexpr int kStreamUnroll = stream_unroll<T, S>(2, 4, 8, 2);
+  static constexpr int kStreamUnroll = stream_unroll<T, S>(2, 4, 1, 2);
   static constexpr uint32_t kStreamLdsPre =
       kBf16State<T, S> ? lds_for_residency(12) : kStreamLds;
-  static constexpr int kStreamUnrollPre = stream_unroll<T, S>(1, 4, 8, 2);
-  static constexpr int kStreamUnrollSmall = stream_unroll<T, S>(2, 4, 8, 2);
+  static constexpr int kStreamUnrollPre = stream_unroll<T, S>(1, 4, 1, 2);
+  static constexpr int kStreamUnrollSmall = stream_unroll<T, S>(2, 4, 4, 2);
   static constexpr int64_t kStreamSmallBytes = kMallBytes;
+  static constexpr int kStreamPack = stream_pack<T, S>();
   static constexpr int kSegmentUnroll = stream_unroll<T, S>(2, 4, 8, 2);
   static constexpr uint32_t kSegmentLds = residency_lds<T, S>(8);
   static constexpr bool kLateStores = !AMSGRAD && std::is_same<T_, float>::value;
@@ -398,6 +424,8 @@ struct AdamPolicy {
     }
   }
   __device__ static bool reads_state(const Vectors<T>&, uint32_t) { return true; }
+  __device__ static bool decays(const Rep& rep) { return rep.h.weight_decay != 0; }
+  __device__ static void drop_decay(Rep& rep) { rep.h.weight_decay = 0.0; }
   __device__ static void update(M& p, M g, M (&s)[NS], const Rep& rep, bool maximize) {
     M mx = M(0);
     if constexpr (AMSGRAD) mx = s[2];
@@ -419,11 +447,12 @@ struct SgdPolicy {
   using M = op_t<T>;
   static constexpr int NS = HAS_BUF ? 1 : 0;
   static constexpr uint32_t kStreamLds = HAS_BUF ? residency_lds<T, S>(20) : 0u;
-  static constexpr int kStreamUnroll = stream_unroll<T, S>(HAS_BUF ? 1 : 2, 1, 8, 2);
+  static constexpr int kStreamUnroll = stream_unroll<T, S>(HAS_BUF ? 1 : 2, 1, 1, 2);
   static constexpr uint32_t kStreamLdsPre = kStreamLds;
   static constexpr int kStreamUnrollPre = kStreamUnroll;
-  static constexpr int kStreamUnrollSmall = stream_unroll<T, S>(1, 1, 8, 2);
+  static constexpr int kStreamUnrollSmall = stream_unroll<T, S>(1, 1, 4, 2);
   static constexpr int64_t kStreamSmallBytes = kMallBytes;
+  static constexpr int kStreamPack = stream_pack<T, S>();
   static constexpr int kSegmentUnroll = 2;
   static constexpr uint32_t kSegmentLds = 0;
   static constexpr bool kLateStores = std::is_same<T_, float>::value;
@@ -446,6 +475,8 @@ struct SgdPolicy {
   __device__ static bool reads_state(const Vectors<T>& v, uint32_t r) {
     return widen(v.steps[r]) != M(1);
   }
+  __device__ static bool decays(const Rep& rep) { return rep.h.weight_decay != 0; }
+  __device__ static void drop_decay(Rep& rep) { rep.h.weight_decay = 0.0; }
   __device__ static void update(M& p, M g, M (&s)[NS > 0 ? NS : 1], const Rep& rep,
                                 bool maximize) {
     M buf = s[0];
@@ -462,11 +493,12 @@ struct AdagradPolicy {
   using M = op_t<T>;
   static constexpr int NS = 1;
   static constexpr uint32_t kStreamLds = residency_lds<T, S>(16);
-  static constexpr int kStreamUnroll = stream_unroll<T, S>(2, 1, 8, 2);
+  static constexpr int kStreamUnroll = stream_unroll<T, S>(2, 1, 1, 2);
   static constexpr uint32_t kStreamLdsPre = residency_lds<T, S>(20);
-  static constexpr int kStreamUnrollPre = stream_unroll<T, S>(1, 1, 8, 2);
-  static constexpr int kStreamUnrollSmall = stream_unroll<T, S>(2, 1, 8, 2);
+  static constexpr int kStreamUnrollPre = stream_unroll<T, S>(1, 1, 1, 2);
+  static constexpr int kStreamUnrollSmall = stream_unroll<T, S>(2, 1, 4, 2);
   static constexpr int64_t kStreamSmallBytes = kMallBytes;
+  static constexpr int kStreamPack = stream_pack<T, S>();
   static constexpr int kSegmentUnroll = 2;
   static constexpr uint32_t kSegmentLds = 0;
   static constexpr bool kLateStores = false;
@@ -491,6 +523,8 @@ struct AdagradPolicy {
     }
   }
   __device__ static bool reads_state(const Vectors<T>&, uint32_t) { return true; }
+  __device__ static bool decays(const Rep& rep) { return rep.h.weight_decay != 0; }
+  __device__ static void drop_decay(Rep& rep) { rep.h.weight_decay = 0.0; }
   __device__ static void update(M& p, M g, M (&s)[NS], const Rep& rep, bool maximize) {
     adagrad_element<M>(p, g, s[0], rep.h, maximize);
   }
@@ -506,11 +540,12 @@ struct AdagradF32Policy {
   using M = float;
   static constexpr int NS = 1;
   static constexpr uint32_t kStreamLds = residency_lds<T, S>(16);
-  static constexpr int kStreamUnroll = stream_unroll<T, S>(2, 1, 4, 2);
+  static constexpr int kStreamUnroll = stream_unroll<T, S>(2, 1, 1, 2);
   static constexpr uint32_t kStreamLdsPre = residency_lds<T, S>(20);
-  static constexpr int kStreamUnrollPre = stream_unroll<T, S>(1, 1, 4, 2);
+  static constexpr int kStreamUnrollPre = stream_unroll<T, S>(1, 1, 1, 2);
   static constexpr int kStreamUnrollSmall = stream_unroll<T, S>(2, 1, 4, 2);
   static constexpr int64_t kStreamSmallBytes = kMallBytes;
+  static constexpr int kStreamPack = stream_pack<T, S>();
   static constexpr int kSegmentUnroll = 2;
   static constexpr uint32_t kSegmentLds = 0;
   static constexpr bool kLateStores = false;
@@ -536,6 +571,11 @@ struct AdagradF32Policy {
     }
   }
   __device__ static bool reads_state(const Vectors<T>&, uint32_t) { return true; }
+  __device__ static bool decays(const Rep& rep) { return rep.h.has_weight_decay; }
+  __device__ static void drop_decay(Rep& rep) {
+    rep.h.weight_decay = 0.0f;
+    rep.h.has_weight_decay = false;
+  }
   __device__ static void update(M& p, M g, M (&s)[NS], const Rep& rep, bool maximize) {
     adagrad_element_f32(p, g, s[0], rep.h, maximize);
   }
@@ -562,7 +602,7 @@ constexpr uint32_t stream_lds_of() {
 // Elements per streaming tile: one wavefront x the policy's packs per thread.
 template <typename P, bool PRE, bool SMALL>
 constexpr int64_t stream_tile() {
-  return int64_t(kStreamThreads) * kPack * stream_unroll_of<P, PRE, SMALL>();
+  return int64_t(kStreamThreads) * P::kStreamPack * stream_unroll_of<P, PRE, SMALL>();
 }
 
 // Bytes of (R, T) operands a launch reads (all rows): params and grads in
@@ -640,6 +680,7 @@ __global__ __launch_bounds__(kStreamThreads) void stream_kernel(KArgs<P> a) {
   constexpr int NS = P::NS;
   constexpr int SS = state_slots<P>();
   constexpr bool NT = !SMALL;
+  constexpr int KP = P::kStreamPack;
   constexpr int U = stream_unroll_of<P, PRE, SMALL>();
   constexpr int64_t kStreamTile = stream_tile<P, PRE, SMALL>();
   uint32_t r;
@@ -653,24 +694,25 @@ __global__ __launch_bounds__(kStreamThreads) void stream_kernel(KArgs<P> a) {
   constexpr uint32_t A = align_elems<T>();
   const int64_t width = a.g.T;
   const int64_t head = imin(width, (A - (a.g.res0 + r * a.g.rmod) % A) % A);
-  const int64_t packs_row = (width - head) / kPack;
+  const int64_t packs_row = (width - head) / KP;
   T* const pbase = pg_row<P>(a.x, 0, r);
   const T* const gbase = pg_row<P>(a.x, 1, r);
   S* sbase[SS];
 #pragma unroll
   for (int b = 0; b < NS; ++b) sbase[b] = state_row<P>(a.x, 2 + b, r);
 
-  // The parameters' packs are 16-byte aligned by construction; with ANY the
-  // other operands sit at another 16-byte phase and use element-aligned packs.
-  Pack<T>* prow = reinterpret_cast<Pack<T>*>(pbase + head) + t0 / kPack;
-  const Packs<ANY, T, NT> grow(const_cast<T*>(gbase) + head + t0);
-  Packs<ANY, S, NT> srow[SS];
+  // The parameters' packs are aligned by construction (a row's packs start at
+  // its first 256-byte boundary); with ANY the other operands sit at another
+  // phase and use element-aligned packs.
+  Pack<T, KP>* prow = reinterpret_cast<Pack<T, KP>*>(pbase + head) + t0 / KP;
+  const Packs<ANY, T, NT, KP> grow(const_cast<T*>(gbase) + head + t0);
+  Packs<ANY, S, NT, KP> srow[SS];
 #pragma unroll
-  for (int b = 0; b < NS; ++b) srow[b] = Packs<ANY, S, NT>(sbase[b] + head + t0);
-  const int64_t packs_left = packs_row - t0 / kPack;
+  for (int b = 0; b < NS; ++b) srow[b] = Packs<ANY, S, NT, KP>(sbase[b] + head + t0);
+  const int64_t packs_left = packs_row - t0 / KP;
 
-  Pack<T> vp[U], vg[U];
-  Pack<S> vs[SS][U];
+  Pack<T, KP> vp[U], vg[U];
+  Pack<S, KP> vs[SS][U];
 #pragma unroll
   for (int u = 0; u < U; ++u) {
     const int64_t i = int64_t(u) * kStreamThreads + threadIdx.x;
@@ -694,21 +736,35 @@ __global__ __launch_bounds__(kStreamThreads) void stream_kernel(KArgs<P> a) {
       srow[b].store(i, vs[b][u]);
     }
   };
+  const auto compute = [&](const typename P::Rep& rp, bool maximize)
+                           __attribute__((always_inline)) {
 #pragma unroll
-  for (int u = 0; u < U; ++u) {
-    const int64_t i = int64_t(u) * kStreamThreads + threadIdx.x;
-    if (i < packs_left) {
+    for (int u = 0; u < U; ++u) {
+      const int64_t i = int64_t(u) * kStreamThreads + threadIdx.x;
+      if (i < packs_left) {
 #pragma unroll
-      for (int k = 0; k < kPack; ++k) {
-        S st[SS];
+        for (int k = 0; k < KP; ++k) {
+          S st[SS];
 #pragma unroll
-        for (int b = 0; b < NS; ++b) st[b] = vs[b][u].v[k];
-        apply_element<P>(vp[u].v[k], vg[u].v[k], st, load_state, rep, a.maximize);
+          for (int b = 0; b < NS; ++b) st[b] = vs[b][u].v[k];
+          apply_element<P>(vp[u].v[k], vg[u].v[k], st, load_state, rp, maximize);
 #pragma unroll
-        for (int b = 0; b < NS; ++b) vs[b][u].v[k] = st[b];
+          for (int b = 0; b < NS; ++b) vs[b][u].v[k] = st[b];
+        }
+        if constexpr (!P::kLateStores) store_packs(u, i);
       }
-      if constexpr (!P::kLateStores) store_packs(u, i);
     }
+  };
+  // The replica's weight decay and `maximize` are uniform over the workgroup:
+  // branch on them once instead of evaluating the decay term per element and
+  // selecting (what the compiler makes of the per-element test). The common
+  // case, neither, runs the math with both as constants.
+  if (!a.maximize && !P::decays(rep)) {
+    typename P::Rep plain = rep;
+    P::drop_decay(plain);
+    compute(plain, false);
+  } else {
+    compute(rep, a.maximize);
   }
   if constexpr (P::kLateStores) {
 #pragma unroll
@@ -718,8 +774,8 @@ __global__ __launch_bounds__(kStreamThreads) void stream_kernel(KArgs<P> a) {
     }
   }
 
-  // The row's head before its first 256-byte boundary (tile 0) and its at most
-  // three tail elements (last tile), one element per access.
+  // The row's head before its first 256-byte boundary (tile 0) and its fewer
+  // than KP tail elements (last tile), one element per access.
   const auto one = [&](int64_t j) {
     T pe = pbase[j];
     S st[SS];
@@ -736,7 +792,7 @@ __global__ __launch_bounds__(kStreamThreads) void stream_kernel(KArgs<P> a) {
     for (int64_t j = threadIdx.x; j < head; j += kStreamThreads) one(j);
   }
   if (t0 + kStreamTile >= width) {
-    for (int64_t j = head + packs_row * kPack + threadIdx.x; j < width; j += kStreamThreads) one(j);
+    for (int64_t j = head + packs_row * KP + threadIdx.x; j < width; j += kStreamThreads) one(j);
   }
 }
 
@@ -1318,18 +1374,18 @@ bool rows_streamable(const Operands<typename P::T>& x, int n, uint32_t& res0, ui
   return true;
 }
 
-// Whether every present operand's 16-byte boundaries fall on the same element
-// index as the parameters' in every row (common base residue and row stride
-// modulo 4): then all packs are aligned and the drivers' ANY = false variants
-// run.
+// Whether every present operand's pack boundaries (packs of `pack` elements)
+// fall on the same element index as the parameters' in every row (common base
+// residue and row stride modulo `pack`): then all packs are aligned and the
+// drivers' ANY = false variants run.
 template <typename P>
-bool rows_same_phase(const Operands<typename P::T>& x, int n) {
+bool rows_same_phase(const Operands<typename P::T>& x, int n, int64_t pack = kPack) {
   const auto residue = [&](int b) {
     const size_t elem = b < 2 ? sizeof(typename P::T) : sizeof(typename P::S);
-    return static_cast<uint32_t>((reinterpret_cast<uintptr_t>(x.data[b]) / elem) % kPack);
+    return static_cast<uint32_t>((reinterpret_cast<uintptr_t>(x.data[b]) / elem) % pack);
   };
   const auto mod = [&](int b) {
-    return static_cast<uint32_t>(((x.stride_r[b] % kPack) + kPack) % kPack);
+    return static_cast<uint32_t>(((x.stride_r[b] % pack) + pack) % pack);
   };
   for (int b = 1; b < n; ++b) {
     if (x.data[b] == nullptr) continue;
@@ -1644,7 +1700,7 @@ int launch_dense(const Call& c, int nbufs) {
     ColArgs<P> ca;
     uint32_t col_blocks = 0;
     if (streamable) {
-      const bool same_phase = rows_same_phase<P>(a.x, nbufs);
+      const bool same_phase = rows_same_phase<P>(a.x, nbufs, P::kStreamPack);
       if constexpr (P::kPreWords > 0) {
         if (pre) {
           if (small) {
