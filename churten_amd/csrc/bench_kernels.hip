@@ -4,7 +4,10 @@
 // same traffic reaches on the same buffers in the same process.
 // cb_narrow_bf16 / cb_narrow_f16: the kernels' float -> bfloat16 / half
 // narrowing over an array, for the tests that check them against torch's
-// conversions on every float bit pattern.
+// conversions on every float bit pattern. cb_div_bc2s: Adam's sqrt(v) /
+// bias_correction2_sqrt as the float update computes it (a multiply by the
+// divisor's double reciprocal), for the tests that check it against a true
+// division.
 //
 // Same decomposition as the streaming driver at float32: one-wave workgroups,
 // 512-element tiles of (replica, tile) pairs, frozen replicas skipped, two
@@ -91,6 +94,16 @@ __global__ __launch_bounds__(256) void narrow_bf16_kernel(const float* in, uint1
   if (i < n) out[i] = churten::narrow<churten::bf16_t>(in[i]).bits;
 }
 
+// b_stride 0: one divisor for every element; 1: one per element.
+__global__ __launch_bounds__(256) void div_bc2s_kernel(const float* x, const float* b,
+                                                       int64_t b_stride, float* out, int64_t n) {
+  const int64_t i = int64_t(blockIdx.x) * 256 + threadIdx.x;
+  if (i < n) {
+    const churten::AdamConsts<float> c = churten::adam_consts<float>(1.0, 1.0f, b[i * b_stride]);
+    out[i] = churten::adam_div_bc2s(x[i], c.bc2s_div);
+  }
+}
+
 __global__ __launch_bounds__(256) void narrow_f16_kernel(const float* in, uint16_t* out,
                                                          int64_t n) {
   const int64_t i = int64_t(blockIdx.x) * 256 + threadIdx.x;
@@ -113,6 +126,18 @@ extern "C" int cb_narrow_bf16(const float* in, uint16_t* out, int64_t n, hipStre
   if (n <= 0 || n > int64_t(UINT32_MAX) * 256) return 1;
   const uint32_t blocks = static_cast<uint32_t>((n + 255) / 256);
   hipLaunchKernelGGL(narrow_bf16_kernel, dim3(blocks), dim3(256), 0, stream, in, out, n);
+  return static_cast<int>(hipGetLastError());
+}
+
+// out[i] = x[i] / b[i * b_stride] as the float Adam update divides sqrt(v) by
+// bias_correction2_sqrt (b_stride 0 or 1). Returns 0, 1 on bad arguments, or
+// the HIP error code.
+extern "C" int cb_div_bc2s(const float* x, const float* b, int64_t b_stride, float* out,
+                           int64_t n, hipStream_t stream) {
+  if (n <= 0 || n > int64_t(UINT32_MAX) * 256 || (b_stride != 0 && b_stride != 1)) return 1;
+  const uint32_t blocks = static_cast<uint32_t>((n + 255) / 256);
+  hipLaunchKernelGGL(div_bc2s_kernel, dim3(blocks), dim3(256), 0, stream, x, b, b_stride, out,
+                     n);
   return static_cast<int>(hipGetLastError());
 }
 

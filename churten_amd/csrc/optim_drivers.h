@@ -347,11 +347,12 @@ constexpr int stream_unroll(int fp32, int bf16_state, int narrow, int wide) {
 // nearest-even on store).
 //
 // Per-replica constants. `prologue<false>` derives a replica's constants in
-// every workgroup (Adam: two fp64 pow; Adagrad: an fp64 divide);
-// `prologue<true>` reads them from the call's workspace, where the preparation
-// launch (`precompute`, once per replica and call, after the step bump) put
-// them. Both give the same bits: the workspace holds the math-type values
-// widened to double. kPreWords is the number of such doubles (0: nothing worth
+// every workgroup (Adam: two fp64 pow and the step size's divide; Adagrad: an
+// fp64 divide); `prologue<true>` reads them from the call's workspace, where
+// the preparation launch (`precompute`, once per replica and call, after the
+// step bump) put them. Both give the same bits: the workspace holds the
+// math-type values widened to double (Adam's divisor of sqrt(v) is a double
+// already). kPreWords is the number of such doubles (0: nothing worth
 // hoisting, the policy never reads a workspace). `reads_state` is decided from
 // the (R,) vectors alone, so the drivers issue their loads before the prologue.
 // `decays` / `drop_decay`: whether the replica's weight-decay term is live, and
@@ -398,15 +399,19 @@ struct AdamPolicy {
   static constexpr int kPreWords = 2;
   struct Rep {
     AdamHyper h;
-    M bc1, bc2s;
+    AdamConsts<M> c;
   };
-  // bias_correction1 and sqrt(bias_correction2) of the bumped step.
-  __device__ static void precompute(const Vectors<T>& v, uint32_t r, double* out) {
+  // The step size and sqrt(v)'s divisor of the bumped step (adam_consts).
+  __device__ static AdamConsts<M> consts(const Vectors<T>& v, uint32_t r) {
     M bc1, bc2s;
     adam_bias_corrections<M>(hyper_at(v.h[1], r), hyper_at(v.h[2], r), hyper_at(v.steps, r),
                              bc1, bc2s);
-    out[0] = static_cast<double>(bc1);
-    out[1] = static_cast<double>(bc2s);
+    return adam_consts<M>(hyper_at(v.h[0], r), bc1, bc2s);
+  }
+  __device__ static void precompute(const Vectors<T>& v, uint32_t r, double* out) {
+    const AdamConsts<M> c = consts(v, r);
+    out[0] = static_cast<double>(c.step_size);
+    out[1] = c.bc2s_div;
   }
   template <bool PRE>
   __device__ static void prologue(const Vectors<T>& v, uint32_t r, Rep& rep) {
@@ -416,11 +421,10 @@ struct AdamPolicy {
     rep.h.eps = hyper_at(v.h[3], r);
     rep.h.weight_decay = hyper_at(v.h[4], r);
     if constexpr (PRE) {
-      rep.bc1 = static_cast<M>(v.pre[kPreStride * r]);
-      rep.bc2s = static_cast<M>(v.pre[kPreStride * r + 1]);
+      rep.c.step_size = static_cast<M>(v.pre[kPreStride * r]);
+      rep.c.bc2s_div = v.pre[kPreStride * r + 1];
     } else {
-      adam_bias_corrections<M>(rep.h.beta1, rep.h.beta2, hyper_at(v.steps, r), rep.bc1,
-                               rep.bc2s);
+      rep.c = consts(v, r);
     }
   }
   __device__ static bool reads_state(const Vectors<T>&, uint32_t) { return true; }
@@ -429,8 +433,7 @@ struct AdamPolicy {
   __device__ static void update(M& p, M g, M (&s)[NS], const Rep& rep, bool maximize) {
     M mx = M(0);
     if constexpr (AMSGRAD) mx = s[2];
-    adam_element<M, ADAMW, AMSGRAD>(p, g, s[0], s[1], mx, rep.h, maximize, rep.bc1,
-                                    rep.bc2s);
+    adam_element<M, ADAMW, AMSGRAD>(p, g, s[0], s[1], mx, rep.h, maximize, rep.c);
     if constexpr (AMSGRAD) s[2] = mx;
   }
 };

@@ -26,6 +26,8 @@
 #include <hip/hip_runtime.h>
 #include <stdint.h>
 
+#include <type_traits>
+
 namespace churten {
 
 // ---------------------------------------------------------------------------
@@ -82,11 +84,55 @@ struct AdamHyper {
   double lr, beta1, beta2, weight_decay, eps;
 };
 
+// A float divided by a per-replica constant b, as a multiply by the double
+// `rcp` = RN64(1 / b): RN32(RN64(x * rcp)) == RN32(x / b) for every float x
+// and b (zeros, infinities and NaNs included; rcp is +-inf for b = +-0 and
+// +-0 for b = +-inf). Why: x and b have 24-bit significands, so x / b is never
+// a midpoint between two floats (a midpoint has a 25-bit odd significand M, and
+// x = b * M would need M to divide x's significand), and its distance to the
+// nearest midpoint is a nonzero multiple of 2^(e_b + e_q - 24) divided by b,
+// i.e. more than 2^-49 of |x / b|, also for subnormal x, b or quotient. The
+// double product errs by at most (1 + 2^-53)^2 - 1 < 2^-52 of it, so both sit
+// on the same side of every rounding boundary. Nine VALU instructions fewer per
+// element than the correctly rounded float divide; tests check the identity on
+// every float x for a set of b, and through the update against torch.
+__device__ __forceinline__ float div_by_rcp(float x, double rcp) {
+  return static_cast<float>(static_cast<double>(x) * rcp);
+}
+
+// Adam's per-replica constants as the element update consumes them: the step
+// size lr / bias_correction1 (a double divide narrowed to the math type, as
+// ATen writes it) and the divisor of sqrt(v): for float math the reciprocal of
+// bias_correction2_sqrt in double (div_by_rcp), for double math the value
+// itself.
+template <typename opmath_t>
+struct AdamConsts {
+  opmath_t step_size;
+  double bc2s_div;
+};
+
+template <typename opmath_t>
+__device__ __forceinline__ AdamConsts<opmath_t> adam_consts(
+    const double lr, const opmath_t bias_correction1, const opmath_t bias_correction2_sqrt) {
+  AdamConsts<opmath_t> c;
+  c.step_size = static_cast<opmath_t>(lr / bias_correction1);
+  if constexpr (std::is_same<opmath_t, float>::value) {
+    c.bc2s_div = 1.0 / static_cast<double>(bias_correction2_sqrt);
+  } else {
+    c.bc2s_div = bias_correction2_sqrt;
+  }
+  return c;
+}
+
+// sqrt(v) / bias_correction2_sqrt in the math type.
+__device__ __forceinline__ float adam_div_bc2s(float s, double d) { return div_by_rcp(s, d); }
+__device__ __forceinline__ double adam_div_bc2s(double s, double d) { return s / d; }
+
 template <typename opmath_t, bool ADAMW, bool AMSGRAD>
 __device__ __forceinline__ void adam_element(
     opmath_t& param, opmath_t grad, opmath_t& exp_avg, opmath_t& exp_avg_sq,
     opmath_t& max_exp_avg_sq, const AdamHyper& h, const bool maximize,
-    const opmath_t bias_correction1, const opmath_t bias_correction2_sqrt) {
+    const AdamConsts<opmath_t>& c) {
   if (maximize) {
     grad = -grad;
   }
@@ -106,15 +152,16 @@ __device__ __forceinline__ void adam_element(
   // exp_avg_sq = beta2 * exp_avg_sq + (1 - beta2) * grad * grad
   exp_avg_sq = static_cast<opmath_t>(
       ::fma(h.beta2, double(exp_avg_sq), ((1 - h.beta2) * double(grad)) * double(grad)));
-  const opmath_t step_size = h.lr / bias_correction1;
+  // ATen: step_size = lr / bias_correction1 (per replica, in c);
+  // denom = (sqrt(v) / bias_correction2_sqrt) + eps.
   opmath_t denom;
   if constexpr (AMSGRAD) {
     max_exp_avg_sq = ::max(max_exp_avg_sq, exp_avg_sq);
-    denom = (std::sqrt(max_exp_avg_sq) / bias_correction2_sqrt) + h.eps;
+    denom = adam_div_bc2s(std::sqrt(max_exp_avg_sq), c.bc2s_div) + h.eps;
   } else {
-    denom = (std::sqrt(exp_avg_sq) / bias_correction2_sqrt) + h.eps;
+    denom = adam_div_bc2s(std::sqrt(exp_avg_sq), c.bc2s_div) + h.eps;
   }
-  param -= step_size * exp_avg / denom;
+  param -= c.step_size * exp_avg / denom;
 }
 
 // Per-replica bias corrections from the (bumped) step count: computed in double

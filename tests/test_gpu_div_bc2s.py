@@ -1,0 +1,94 @@
+"""Adam's float update divides sqrt(v) by the replica's bias_correction2_sqrt
+as a multiply by that divisor's correctly rounded double reciprocal. That is
+exact: the rounded product equals the correctly rounded quotient for every
+float pair. Checked here against torch's true division on the GPU, on every one
+of the 2^32 float bit patterns for a set of divisors (divisors Adam produces,
+odd significands, a subnormal and a huge one) and on random bit-pattern pairs.
+A plausible wrong form (the reciprocal rounded to float) fails the same
+comparison."""
+
+from __future__ import annotations
+
+import ctypes
+import math
+from pathlib import Path
+
+import numpy as np
+import pytest
+import torch
+
+pytestmark = pytest.mark.gpu
+
+LIB = Path(__file__).resolve().parents[1] / "churten_amd" / "lib" / "libchurten_bench.so"
+CHUNK = 1 << 30
+
+
+def _bc2s(beta2: float, step: float) -> float:
+    return float(np.float32(math.sqrt(1.0 - beta2 ** step)))
+
+
+DIVISORS = [
+    _bc2s(0.999, 1),
+    _bc2s(0.999, 7),
+    _bc2s(0.9999, 1),
+    _bc2s(0.999, 10000),
+    1.0,
+    3.0,
+    float(np.float32(0.1)),
+    float(np.float32(1.5 * 2.0 ** -130)),  # subnormal
+    float(np.float32(1.37 * 2.0 ** 100)),
+]
+
+
+def _div(lib, x, b, b_stride):
+    out = torch.empty_like(x)
+    rc = lib.cb_div_bc2s(ctypes.c_void_p(x.data_ptr()), ctypes.c_void_p(b.data_ptr()),
+                         ctypes.c_int64(b_stride), ctypes.c_void_p(out.data_ptr()),
+                         ctypes.c_int64(x.numel()),
+                         ctypes.c_void_p(torch.cuda.current_stream().cuda_stream))
+    assert rc == 0
+    return out
+
+
+def _mismatches(got, want):
+    both_nan = torch.isnan(got) & torch.isnan(want)
+    return ((got.view(torch.int32) != want.view(torch.int32)) & ~both_nan).nonzero()
+
+
+@pytest.mark.parametrize("b", DIVISORS, ids=[f"{d:.6g}" for d in DIVISORS])
+def test_div_bc2s_on_every_float(b):
+    lib = ctypes.CDLL(str(LIB))
+    bt = torch.tensor([b], dtype=torch.float32, device="cuda")
+    for part in range(4):
+        start = part * CHUNK - (1 << 31)
+        x = torch.arange(start, start + CHUNK, dtype=torch.int64, device="cuda").to(
+            torch.int32).view(torch.float32)
+        got = _div(lib, x, bt, 0)
+        # A one-element device tensor, not a Python scalar: torch then divides
+        # elementwise (a CPU scalar divisor would be turned into a multiply).
+        want = x / bt
+        bad = _mismatches(got, want)
+        if bad.numel():
+            i = int(bad[0])
+            pytest.fail(f"b={b!r}: {bad.numel()} x differ; first x bits "
+                        f"0x{int(x[i:i + 1].view(torch.int32)) & 0xFFFFFFFF:08x}: "
+                        f"{float(got[i])!r} vs {float(want[i])!r}")
+        del x, got, want
+
+
+def test_div_bc2s_random_pairs_and_sensitivity():
+    lib = ctypes.CDLL(str(LIB))
+    gen = torch.Generator(device="cuda").manual_seed(2024)
+    n = 1 << 28
+    x = torch.randint(-(1 << 31), 1 << 31, (n,), generator=gen, device="cuda",
+                      dtype=torch.int64).to(torch.int32).view(torch.float32)
+    # divisors over the whole exponent range, and divisors like Adam's
+    b = torch.randint(-(1 << 31), 1 << 31, (n,), generator=gen, device="cuda",
+                      dtype=torch.int64).to(torch.int32).view(torch.float32)
+    b[: n // 2] = torch.rand(n // 2, generator=gen, device="cuda") + 2.0 ** -12
+    got = _div(lib, x, b, 1)
+    want = x / b
+    assert _mismatches(got, want).numel() == 0
+    # The same comparison catches the reciprocal rounded to float first.
+    wrong = x * (1.0 / b)
+    assert _mismatches(wrong, want).numel() > 1000
