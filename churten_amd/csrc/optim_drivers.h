@@ -303,9 +303,10 @@ constexpr int64_t kMallBytes = int64_t(256) << 20;
 // throughout, float32 params with bfloat16 state, 16-bit params, float64.
 // Measured per policy on config-5-sized state (1/2/4/8 packs, one process per
 // sweep, two sweeps): float32 keeps 2 (under its residency cap; 1 with
-// precomputed constants, below); bfloat16 state wants 4 for Adam (+13%) but 1
-// for SGD and Adagrad (+8-15%); float64 is flat. 16-bit params and state take
-// one 8-element (16-byte) pack per thread, uncapped, for large launches.
+// precomputed constants, below); bfloat16 state wants 4 for Adam (+13%; 2 with
+// precomputed constants, below) but 1 for SGD and Adagrad (+8-15%); float64 is
+// flat. 16-bit params and state take one 8-element (16-byte) pack per thread,
+// uncapped, for large launches (Adagrad with precomputed constants: 4, below).
 // Against the previous 4-element packs x 8 (config-5 buffers, half and
 // bfloat16 timed on the same storage, 5-6 interleaved rounds, three sweeps on
 // different boxes): Adam +4-8% (one box: half -2%), SGD +7-9%, float32-math
@@ -371,12 +372,20 @@ constexpr int stream_unroll(int fp32, int bf16_state, int narrow, int wide) {
 //   Adagrad (fp64 math)  1 pack, cap 20: 6.45-6.49 (2 packs, cap 16: 5.70;
 //                        caps 18-24 within 0.7% of each other)
 //   Adagrad, fp32 math   1 pack, cap 20: 6.52 (2 packs, cap 16: 5.84)
-//   Adam, bf16 moments   4 packs, cap 12: 6.15-6.31 (uncapped: 5.90-6.23)
 // SGD has no workspace, but with its loads issued before the prologue its
 // buffered float32 form also runs one pack per thread, cap 20: 6.46-6.60
 // against 6.13 for two packs at cap 14. bfloat16-state SGD and Adagrad (1
 // pack, uncapped) and float64 (2 packs) kept their shapes: nothing else in the
 // sweep beat them. 16-bit parameters: one 8-element pack, uncapped (above).
+// Rechecked after Adam's divide by bias_correction2_sqrt became a multiply
+// (packs 1/2/4 x caps 10-20 and uncapped, 3 interleaved rounds per box, up to
+// three boxes): float32 Adam, Adam with amsgrad, SGD and both Adagrads keep
+// their shapes; two changes:
+//   Adam, bf16 moments   2 packs, cap 12: 6.21-6.26 TB/s (4 packs, cap 12:
+//                        6.00-6.02; 1 pack, cap 20: 6.21-6.22)
+//   Adagrad, 16-bit      4 packs of 8, uncapped: half 6.14-6.18, bfloat16 6.07
+//   parameters           (1 pack: half 5.65-5.88, bfloat16 5.75)
+// Adam and SGD with 16-bit parameters stayed within 2% of one pack, uncapped.
 
 // Adam / AdamW: h = {lr, beta1, beta2, eps, weight_decay}.
 template <typename T_, bool ADAMW, bool AMSGRAD, typename S_ = T_>
@@ -389,7 +398,7 @@ struct AdamPolicy {
   static constexpr int kStreamUnroll = stream_unroll<T, S>(2, 4, 1, 2);
   static constexpr uint32_t kStreamLdsPre =
       kBf16State<T, S> ? lds_for_residency(12) : kStreamLds;
-  static constexpr int kStreamUnrollPre = stream_unroll<T, S>(1, 4, 1, 2);
+  static constexpr int kStreamUnrollPre = stream_unroll<T, S>(1, 2, 1, 2);
   static constexpr int kStreamUnrollSmall = stream_unroll<T, S>(2, 4, 4, 2);
   static constexpr int64_t kStreamSmallBytes = kMallBytes;
   static constexpr int kStreamPack = stream_pack<T, S>();
@@ -498,7 +507,7 @@ struct AdagradPolicy {
   static constexpr uint32_t kStreamLds = residency_lds<T, S>(16);
   static constexpr int kStreamUnroll = stream_unroll<T, S>(2, 1, 1, 2);
   static constexpr uint32_t kStreamLdsPre = residency_lds<T, S>(20);
-  static constexpr int kStreamUnrollPre = stream_unroll<T, S>(1, 1, 1, 2);
+  static constexpr int kStreamUnrollPre = stream_unroll<T, S>(1, 1, 4, 2);
   static constexpr int kStreamUnrollSmall = stream_unroll<T, S>(2, 1, 4, 2);
   static constexpr int64_t kStreamSmallBytes = kMallBytes;
   static constexpr int kStreamPack = stream_pack<T, S>();
