@@ -269,10 +269,7 @@ __device__ __forceinline__ double hyper_at(const T* h, uint32_t r) {
 // each policy's reservations; small launches (under kCapMinElems elements of
 // the (R, T) operands, 8192 tiles of 512) launch without them, since there the
 // cap would only serialise the launch (config 1 lost 16% with one). The
-// segmented driver (`kSegmentLds`) runs uncapped when workgroups derive their
-// constants (caps of 6-10 moved it by -3% to +2%); with a workspace, float32
-// Adam there runs at 8 workgroups (16 waves) per CU: 6.46-6.47 against
-// 6.38 TB/s uncapped.
+// segmented driver runs uncapped (its shapes are next to segment_tile).
 constexpr uint32_t kLdsPerCU = 160 * 1024;
 constexpr uint32_t lds_for_residency(uint32_t n) {
   uint32_t x = (kLdsPerCU / n) / 256 * 256;
@@ -403,7 +400,9 @@ struct AdamPolicy {
   static constexpr int64_t kStreamSmallBytes = kMallBytes;
   static constexpr int kStreamPack = stream_pack<T, S>();
   static constexpr int kSegmentUnroll = stream_unroll<T, S>(2, 4, 8, 2);
-  static constexpr uint32_t kSegmentLds = residency_lds<T, S>(8);
+  static constexpr int kSegmentThreads = kThreads;
+  static constexpr int kSegmentThreadsPre = kFp32State<T, S> ? kStreamThreads : kThreads;
+  static constexpr int kSegmentUnrollPre = kFp32State<T, S> ? 1 : kSegmentUnroll;
   static constexpr bool kLateStores = !AMSGRAD && std::is_same<T_, float>::value;
   static constexpr int kPreWords = 2;
   struct Rep {
@@ -466,7 +465,9 @@ struct SgdPolicy {
   static constexpr int64_t kStreamSmallBytes = kMallBytes;
   static constexpr int kStreamPack = stream_pack<T, S>();
   static constexpr int kSegmentUnroll = 2;
-  static constexpr uint32_t kSegmentLds = 0;
+  static constexpr int kSegmentThreads = kThreads;
+  static constexpr int kSegmentThreadsPre = kThreads;
+  static constexpr int kSegmentUnrollPre = kSegmentUnroll;
   static constexpr bool kLateStores = std::is_same<T_, float>::value;
   static constexpr int kPreWords = 0;
   struct Rep {
@@ -512,7 +513,9 @@ struct AdagradPolicy {
   static constexpr int64_t kStreamSmallBytes = kMallBytes;
   static constexpr int kStreamPack = stream_pack<T, S>();
   static constexpr int kSegmentUnroll = 2;
-  static constexpr uint32_t kSegmentLds = 0;
+  static constexpr int kSegmentThreads = kThreads;
+  static constexpr int kSegmentThreadsPre = kThreads;
+  static constexpr int kSegmentUnrollPre = kSegmentUnroll;
   static constexpr bool kLateStores = false;
   static constexpr int kPreWords = 1;
   struct Rep {
@@ -559,7 +562,9 @@ struct AdagradF32Policy {
   static constexpr int64_t kStreamSmallBytes = kMallBytes;
   static constexpr int kStreamPack = stream_pack<T, S>();
   static constexpr int kSegmentUnroll = 2;
-  static constexpr uint32_t kSegmentLds = 0;
+  static constexpr int kSegmentThreads = kThreads;
+  static constexpr int kSegmentThreadsPre = kThreads;
+  static constexpr int kSegmentUnrollPre = kSegmentUnroll;
   static constexpr bool kLateStores = false;
   static constexpr int kPreWords = 1;
   struct Rep {
@@ -624,15 +629,31 @@ constexpr int64_t operand_bytes_per_elem() {
   return 2 * int64_t(sizeof(typename P::T)) + P::NS * int64_t(sizeof(typename P::S));
 }
 
-// Elements per segmented-driver tile (128 threads). Measured per policy at the
-// config-5 layout with per-parameter gradients (1/2/4 packs): Adam with
-// bfloat16 moments or 16-bit params wants 4 (+8-17%); SGD and Adagrad were
-// within noise of 2 for every operand type, and float32/float64 Adam too.
-// With one-instruction bfloat16 narrowing, 16-bit Adam gained again from 8:
-// +2.7% (half), +4.2% (bfloat16).
-template <typename P>
+// Workgroup size, packs per thread and elements per tile of the segmented
+// driver, with the per-replica constants read from a workspace (PRE) or
+// derived in every workgroup. Measured per policy at the config-5 layout with
+// per-parameter gradients (128 threads, 1/2/4 packs): Adam with bfloat16
+// moments or 16-bit params wants 4 (+8-17%); SGD and Adagrad were within noise
+// of 2 for every operand type, and float32/float64 Adam too. With
+// one-instruction bfloat16 narrowing, 16-bit Adam gained again from 8: +2.7%
+// (half), +4.2% (bfloat16). Float32 Adam with a workspace takes the dense
+// update's one-wave workgroups with one pack, uncapped: on one box 6.33 TB/s
+// against 6.03 for the previous 128 threads x 2 packs under a cap of 8
+// workgroups per CU (64 or 128 threads x 1 or 2 packs x caps 6-20 and none, 3
+// interleaved rounds); on another, 5 rounds, every one of those shapes within
+// 0.2% (6.33-6.35, also when the gradient is stored on the way), 1.6% behind
+// the dense update on the same buffers.
+template <typename P, bool PRE>
+constexpr int segment_threads() {
+  return PRE ? P::kSegmentThreadsPre : P::kSegmentThreads;
+}
+template <typename P, bool PRE>
+constexpr int segment_unroll() {
+  return PRE ? P::kSegmentUnrollPre : P::kSegmentUnroll;
+}
+template <typename P, bool PRE>
 constexpr int64_t segment_tile() {
-  return int64_t(kThreads) * kPack * P::kSegmentUnroll;
+  return int64_t(segment_threads<P, PRE>()) * kPack * segment_unroll<P, PRE>();
 }
 
 template <typename P>
@@ -1094,26 +1115,27 @@ __device__ __forceinline__ SegTile seg_tile(uint32_t res0, uint32_t rmod, uint32
   return t;
 }
 
-// Runs fn(j) for the tile's single elements, spread over the threads.
-template <typename Fn>
+// Runs fn(j) for the tile's single elements, spread over the NTH threads.
+template <int NTH, typename Fn>
 __device__ __forceinline__ void seg_singles(const SegTile& t, int64_t numel, Fn&& fn) {
   if (t.has_head) {
-    for (int64_t j = threadIdx.x; j < t.head; j += kThreads) fn(j);
+    for (int64_t j = threadIdx.x; j < t.head; j += NTH) fn(j);
   }
   if (t.has_tail) {
-    for (int64_t j = t.tail + threadIdx.x; j < numel; j += kThreads) fn(j);
+    for (int64_t j = t.tail + threadIdx.x; j < numel; j += NTH) fn(j);
   }
 }
 
 // PRE: the per-replica constants come from the call's workspace (a.k.vec.pre).
 template <typename P, bool ANY, bool PRE>
-__global__ __launch_bounds__(kThreads) void segment_kernel(SegArgs<P> a) {
+__global__ __launch_bounds__((segment_threads<P, PRE>())) void segment_kernel(SegArgs<P> a) {
   using T = typename P::T;
   using S = typename P::S;
   constexpr int NS = P::NS;
   constexpr int SS = state_slots<P>();
-  constexpr int U = P::kSegmentUnroll;
-  constexpr int64_t kSegTile = segment_tile<P>();
+  constexpr int U = segment_unroll<P, PRE>();
+  constexpr int NTH = segment_threads<P, PRE>();
+  constexpr int64_t kSegTile = segment_tile<P, PRE>();
   const uint32_t tiles_per_row = a.seg.tile0[a.seg.n];
   const uint32_t r = blockIdx.x / tiles_per_row;
   const uint32_t local = blockIdx.x - r * tiles_per_row;
@@ -1150,15 +1172,15 @@ __global__ __launch_bounds__(kThreads) void segment_kernel(SegArgs<P> a) {
       const SegTile t = seg_tile<T, kSegTile>(a.k.g.res0, a.k.g.rmod, r, col, numel, j0);
 #pragma unroll
       for (int u = 0; u < U; ++u) {
-        const int64_t i = int64_t(u) * kThreads + threadIdx.x;
+        const int64_t i = int64_t(u) * NTH + threadIdx.x;
         if (i < t.packs) {
           Packs<ANY, T>(g_dst + t.first).store(i, load_stream_any(g_src + t.first + i * kPack));
         }
       }
-      seg_singles(t, numel, [&](int64_t j) { g_dst[j] = g_src[j]; });
+      seg_singles<NTH>(t, numel, [&](int64_t j) { g_dst[j] = g_src[j]; });
     } else {
       const int64_t cnt = imin(kSegTile, numel - j0);
-      for (int64_t j = j0 + threadIdx.x; j < j0 + cnt; j += kThreads) {
+      for (int64_t j = j0 + threadIdx.x; j < j0 + cnt; j += NTH) {
         g_dst[j * a.k.x.stride_t[1]] = g_src[j];
       }
     }
@@ -1197,7 +1219,7 @@ __global__ __launch_bounds__(kThreads) void segment_kernel(SegArgs<P> a) {
 
   if (!vec) {
     const int64_t cnt = imin(kSegTile, numel - j0);
-    for (int64_t j = j0 + threadIdx.x; j < j0 + cnt; j += kThreads) one(j);
+    for (int64_t j = j0 + threadIdx.x; j < j0 + cnt; j += NTH) one(j);
     return;
   }
 
@@ -1213,7 +1235,7 @@ __global__ __launch_bounds__(kThreads) void segment_kernel(SegArgs<P> a) {
   Pack<S> vs[SS][U];
 #pragma unroll
   for (int u = 0; u < U; ++u) {
-    const int64_t i = int64_t(u) * kThreads + threadIdx.x;
+    const int64_t i = int64_t(u) * NTH + threadIdx.x;
     if (i < t.packs) {
       vp[u] = load_stream(pp + i);
       if (gap) {
@@ -1234,7 +1256,7 @@ __global__ __launch_bounds__(kThreads) void segment_kernel(SegArgs<P> a) {
   }
 #pragma unroll
   for (int u = 0; u < U; ++u) {
-    const int64_t i = int64_t(u) * kThreads + threadIdx.x;
+    const int64_t i = int64_t(u) * NTH + threadIdx.x;
     if (i < t.packs) {
       if (store_grad) {
         gout.store(i, vg[u]);
@@ -1253,7 +1275,7 @@ __global__ __launch_bounds__(kThreads) void segment_kernel(SegArgs<P> a) {
       for (int b = 0; b < NS; ++b) sp[b].store(i, vs[b][u]);
     }
   }
-  seg_singles(t, numel, one);
+  seg_singles<NTH>(t, numel, one);
 }
 
 // Plain gradient scatter: copies every segment into its columns of the (R, T)
@@ -1291,7 +1313,7 @@ __global__ __launch_bounds__(kThreads) void scatter_kernel(ScatterArgs<T> a) {
       const int64_t i = int64_t(u) * kThreads + threadIdx.x;
       if (i < t.packs) store_stream(reinterpret_cast<Pack<T>*>(dst + t.first) + i, v[u]);
     }
-    seg_singles(t, numel, [&](int64_t j) { dst[j] = src[j]; });
+    seg_singles<kThreads>(t, numel, [&](int64_t j) { dst[j] = src[j]; });
     return;
   }
   const int64_t cnt = imin(kTile, numel - j0);
@@ -1561,12 +1583,12 @@ bool walk_fits(SegmentWalk w, int64_t R, int64_t tile, bool vec_rows, Segments<T
 // Launches `kernel` once per chunk of the walk.
 template <typename T, typename Args, typename Kernel>
 int launch_walk(SegmentWalk w, int64_t R, int64_t tile, bool vec_rows, Args& a, Segments<T>& seg,
-                Kernel kernel, hipStream_t stream, uint32_t lds = 0) {
+                Kernel kernel, hipStream_t stream, uint32_t lds = 0, int threads = kThreads) {
   int64_t blocks;
   while ((blocks = next_chunk<T>(w, R, tile, vec_rows, seg)) != 0 || seg.n > 0) {
     if (blocks < 0) return kInvalid;
     if (blocks == 0) continue;
-    hipLaunchKernelGGL(kernel, dim3(static_cast<uint32_t>(blocks)), dim3(kThreads), lds, stream,
+    hipLaunchKernelGGL(kernel, dim3(static_cast<uint32_t>(blocks)), dim3(threads), lds, stream,
                        a);
     const int err = static_cast<int>(hipGetLastError());
     if (err != 0) return err;
@@ -1759,31 +1781,32 @@ int launch_segments(const Call& c, int nbufs, const ts_segment* segs, int n_segs
   SegArgs<P> a;
   bool vec_rows = false;
   const SegmentWalk walk{segs, n_segs, c.T, true};
+  const bool pre = uses_workspace<P>(c);
+  const int64_t tile = pre ? segment_tile<P, true>() : segment_tile<P, false>();
   const auto prepare = [&] {
     if (!fill_kargs<P>(c, nbufs, a.k, true) || !segments_valid(segs, n_segs, c.T)) {
       return false;
     }
     a.k.g = Grid{c.T, 0, 0, 0};
     vec_rows = rows_streamable<P>(a.k.x, nbufs, a.k.g.res0, a.k.g.rmod);
-    return walk_fits<T>(walk, c.R, segment_tile<P>(), vec_rows, a.seg);
+    return walk_fits<T>(walk, c.R, tile, vec_rows, a.seg);
   };
   return run_step<P>(c, a.k.vec, prepare, [&]() -> int {
     const bool same_phase = rows_same_phase<P>(a.k.x, nbufs);
-    // with precomputed constants, large launches take the policy's residency
-    // reservation (kSegmentLds)
-    const uint32_t lds = c.R * c.T >= kCapMinElems ? P::kSegmentLds : 0u;
     if constexpr (P::kPreWords > 0) {
-      if (uses_workspace<P>(c)) {
-        return same_phase ? launch_walk<T>(walk, c.R, segment_tile<P>(), vec_rows, a, a.seg,
-                                           segment_kernel<P, false, true>, c.stream, lds)
-                          : launch_walk<T>(walk, c.R, segment_tile<P>(), vec_rows, a, a.seg,
-                                           segment_kernel<P, true, true>, c.stream, lds);
+      if (pre) {
+        constexpr int nth = segment_threads<P, true>();
+        return same_phase ? launch_walk<T>(walk, c.R, tile, vec_rows, a, a.seg,
+                                           segment_kernel<P, false, true>, c.stream, 0, nth)
+                          : launch_walk<T>(walk, c.R, tile, vec_rows, a, a.seg,
+                                           segment_kernel<P, true, true>, c.stream, 0, nth);
       }
     }
-    return same_phase ? launch_walk<T>(walk, c.R, segment_tile<P>(), vec_rows, a, a.seg,
-                                       segment_kernel<P, false, false>, c.stream)
-                      : launch_walk<T>(walk, c.R, segment_tile<P>(), vec_rows, a, a.seg,
-                                       segment_kernel<P, true, false>, c.stream);
+    constexpr int nth = segment_threads<P, false>();
+    return same_phase ? launch_walk<T>(walk, c.R, tile, vec_rows, a, a.seg,
+                                       segment_kernel<P, false, false>, c.stream, 0, nth)
+                      : launch_walk<T>(walk, c.R, tile, vec_rows, a, a.seg,
+                                       segment_kernel<P, true, false>, c.stream, 0, nth);
   });
 }
 
