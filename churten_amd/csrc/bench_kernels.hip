@@ -4,7 +4,9 @@
 // same traffic reaches on the same buffers in the same process.
 // cb_narrow_bf16 / cb_narrow_f16: the kernels' float -> bfloat16 / half
 // narrowing over an array, for the tests that check them against torch's
-// conversions on every float bit pattern. cb_div_bc2s: Adam's sqrt(v) /
+// conversions on every float bit pattern (cb_narrow2_bf16: the paired form the
+// drivers store packs with). cb_sqrt_rn: the update's float square root over
+// an array, for the test that checks it against torch's. cb_div_bc2s: Adam's sqrt(v) /
 // bias_correction2_sqrt as the float update computes it (a multiply by the
 // divisor's double reciprocal), for the tests that check it against a true
 // division.
@@ -94,6 +96,17 @@ __global__ __launch_bounds__(256) void narrow_bf16_kernel(const float* in, uint1
   if (i < n) out[i] = churten::narrow<churten::bf16_t>(in[i]).bits;
 }
 
+__global__ __launch_bounds__(256) void narrow2_bf16_kernel(const float* in, uint32_t* out,
+                                                           int64_t pairs) {
+  const int64_t i = int64_t(blockIdx.x) * 256 + threadIdx.x;
+  if (i < pairs) out[i] = churten::narrow2_bf16(in[2 * i], in[2 * i + 1]);
+}
+
+__global__ __launch_bounds__(256) void sqrt_rn_kernel(const float* in, float* out, int64_t n) {
+  const int64_t i = int64_t(blockIdx.x) * 256 + threadIdx.x;
+  if (i < n) out[i] = churten::sqrt_rn(in[i]);
+}
+
 // b_stride 0: one divisor for every element; 1: one per element.
 __global__ __launch_bounds__(256) void div_bc2s_kernel(const float* x, const float* b,
                                                        int64_t b_stride, float* out, int64_t n) {
@@ -126,6 +139,24 @@ extern "C" int cb_narrow_bf16(const float* in, uint16_t* out, int64_t n, hipStre
   if (n <= 0 || n > int64_t(UINT32_MAX) * 256) return 1;
   const uint32_t blocks = static_cast<uint32_t>((n + 255) / 256);
   hipLaunchKernelGGL(narrow_bf16_kernel, dim3(blocks), dim3(256), 0, stream, in, out, n);
+  return static_cast<int>(hipGetLastError());
+}
+
+// out[i] = the two bfloat16 (low half first) the drivers store for the floats
+// in[2i], in[2i + 1]. Returns 0, 1 on bad arguments, or the HIP error code.
+extern "C" int cb_narrow2_bf16(const float* in, uint32_t* out, int64_t pairs,
+                               hipStream_t stream) {
+  if (pairs <= 0 || pairs > int64_t(UINT32_MAX) * 256) return 1;
+  const uint32_t blocks = static_cast<uint32_t>((pairs + 255) / 256);
+  hipLaunchKernelGGL(narrow2_bf16_kernel, dim3(blocks), dim3(256), 0, stream, in, out, pairs);
+  return static_cast<int>(hipGetLastError());
+}
+
+// out[i] = the float square root the update kernels take of in[i].
+extern "C" int cb_sqrt_rn(const float* in, float* out, int64_t n, hipStream_t stream) {
+  if (n <= 0 || n > int64_t(UINT32_MAX) * 256) return 1;
+  const uint32_t blocks = static_cast<uint32_t>((n + 255) / 256);
+  hipLaunchKernelGGL(sqrt_rn_kernel, dim3(blocks), dim3(256), 0, stream, in, out, n);
   return static_cast<int>(hipGetLastError());
 }
 

@@ -686,6 +686,62 @@ __device__ __forceinline__ void apply_element(typename P::T& p_io, typename P::T
   }
 }
 
+// N math-type values narrowed into a pack: bfloat16 two at a time
+// (narrow2_bf16, the same bits as narrow<bf16_t> per value), every other type
+// one at a time (hipcc pairs the half conversions itself).
+template <typename T, int N>
+__device__ __forceinline__ Pack<T, N> narrow_pack(const op_t<T> (&x)[N]) {
+  if constexpr (std::is_same<T, bf16_t>::value && N % 2 == 0) {
+    struct Words {
+      uint32_t w[N / 2];
+    } out;
+#pragma unroll
+    for (int k = 0; k < N / 2; ++k) out.w[k] = narrow2_bf16(x[2 * k], x[2 * k + 1]);
+    return __builtin_bit_cast(Pack<T, N>, out);
+  } else {
+    Pack<T, N> out;
+#pragma unroll
+    for (int k = 0; k < N; ++k) out.v[k] = narrow<T>(x[k]);
+    return out;
+  }
+}
+
+// A pack of N elements through the policy, as apply_element does one: widen,
+// update, narrow (the whole pack at once). `vs` holds the state operands'
+// packs (unread ones are never used).
+template <typename P, int N>
+__device__ __forceinline__ void apply_pack(Pack<typename P::T, N>& vp,
+                                           const Pack<typename P::T, N>& vg,
+                                           Pack<typename P::S, N> (&vs)[state_slots<P>()],
+                                           bool load_state, const typename P::Rep& rep,
+                                           bool maximize) {
+  using M = typename P::M;
+  constexpr int SS = state_slots<P>();
+  M pm[N], gm[N];
+  M sm[SS][N];
+#pragma unroll
+  for (int e = 0; e < N; ++e) {
+    pm[e] = widen(vp.v[e]);
+    gm[e] = widen(vg.v[e]);
+#pragma unroll
+    for (int k = 0; k < SS; ++k) {
+      sm[k][e] = (load_state && k < P::NS) ? M(widen(vs[k].v[e])) : M(0);
+    }
+  }
+#pragma unroll
+  for (int e = 0; e < N; ++e) {
+    M s[SS];
+#pragma unroll
+    for (int k = 0; k < SS; ++k) s[k] = sm[k][e];
+    P::update(pm[e], gm[e], s, rep, maximize);
+#pragma unroll
+    for (int k = 0; k < SS; ++k) sm[k][e] = s[k];
+  }
+  vp = narrow_pack<typename P::T, N>(pm);
+#pragma unroll
+  for (int k = 0; k < P::NS; ++k) vs[k] = narrow_pack<typename P::S, N>(sm[k]);
+}
+
 // Row r of (R, T) operand b, as the parameter type (b < 2) or the state type.
 template <typename P>
 __device__ __forceinline__ typename P::T* pg_row(const Operands<typename P::T>& x, int b,
@@ -775,15 +831,12 @@ __global__ __launch_bounds__(kStreamThreads) void stream_kernel(KArgs<P> a) {
     for (int u = 0; u < U; ++u) {
       const int64_t i = int64_t(u) * kStreamThreads + threadIdx.x;
       if (i < packs_left) {
+        Pack<S, KP> st[SS];
 #pragma unroll
-        for (int k = 0; k < KP; ++k) {
-          S st[SS];
+        for (int b = 0; b < NS; ++b) st[b] = vs[b][u];
+        apply_pack<P, KP>(vp[u], vg[u], st, load_state, rp, maximize);
 #pragma unroll
-          for (int b = 0; b < NS; ++b) st[b] = vs[b][u].v[k];
-          apply_element<P>(vp[u].v[k], vg[u].v[k], st, load_state, rp, maximize);
-#pragma unroll
-          for (int b = 0; b < NS; ++b) vs[b][u].v[k] = st[b];
-        }
+        for (int b = 0; b < NS; ++b) vs[b][u] = st[b];
         if constexpr (!P::kLateStores) store_packs(u, i);
       }
     }
@@ -1261,15 +1314,12 @@ __global__ __launch_bounds__((segment_threads<P, PRE>())) void segment_kernel(Se
       if (store_grad) {
         gout.store(i, vg[u]);
       }
+      Pack<S> st[SS];
 #pragma unroll
-      for (int k = 0; k < kPack; ++k) {
-        S st[SS];
+      for (int b = 0; b < NS; ++b) st[b] = vs[b][u];
+      apply_pack<P, kPack>(vp[u], vg[u], st, load_state, rep, a.k.maximize);
 #pragma unroll
-        for (int b = 0; b < NS; ++b) st[b] = vs[b][u].v[k];
-        apply_element<P>(vp[u].v[k], vg[u].v[k], st, load_state, rep, a.k.maximize);
-#pragma unroll
-        for (int b = 0; b < NS; ++b) vs[b][u].v[k] = st[b];
-      }
+      for (int b = 0; b < NS; ++b) vs[b][u] = st[b];
       store_stream(pp + i, vp[u]);
 #pragma unroll
       for (int b = 0; b < NS; ++b) sp[b].store(i, vs[b][u]);

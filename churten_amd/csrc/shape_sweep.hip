@@ -21,7 +21,10 @@
 //   ./shape_sweep adam_bf16state [cfg2|cfg4|cfg5]
 // Families: adam_f32 adam_ams_f32 adam_bf16state adam_f16 adam_bf16 sgd_f32
 // sgd_bf16state sgd_f16 sgd_bf16 adagrad_f32 adagrad_bf16state adagrad_f16
-// adagrad_bf16 seg_adam_f32 (config 5 only). Config 5 needs about 65 GB of
+// adagrad_bf16 seg_adam_f32 (config 5 only); the math families math_adam_f32
+// math_adam_bf16state math_adam_f16 math_adam_bf16 math_adagrad_f32
+// math_adagrad_f16 math_adagrad_bf16 time the shipped shape with the element
+// math's square root as std::sqrt and as the shipped sqrt_rn (bit-identical). Config 5 needs about 65 GB of
 // device memory.
 
 #include <stdio.h>
@@ -63,6 +66,27 @@ template <typename Base, int NTH, int U>
 struct SegmentShape : Base {
   static constexpr int kSegmentThreadsPre = NTH;
   static constexpr int kSegmentUnrollPre = U;
+};
+
+// The same policy with hipcc's std::sqrt in its element math instead of
+// sqrt_rn (bit-identical), for the math family. Adam without AdamW, and
+// Adagrad with fp64 math.
+template <typename Base>
+struct PerElementStdSqrt : Base {
+  using M = typename Base::M;
+  __device__ static void update(M& p, M g, M (&s)[Base::NS], const typename Base::Rep& rep,
+                                bool maximize) {
+    if constexpr (Base::NS >= 2) {  // Adam
+      M mx = M(0);
+      if constexpr (Base::NS == 3) mx = s[2];
+      const M v = adam_moments<M, false, Base::NS == 3>(p, g, s[0], s[1], mx, rep.h, maximize);
+      adam_finish(p, s[0], std::sqrt(v), rep.h, rep.c);
+      if constexpr (Base::NS == 3) s[2] = mx;
+    } else {  // Adagrad (fp64 math)
+      adagrad_sum<M>(p, g, s[0], rep.h, maximize);
+      adagrad_finish<M>(p, g, std::sqrt(s[0]), rep.h);
+    }
+  }
 };
 
 // Deterministic pseudo-random fill: x in (-scale/2, scale/2), or positive.
@@ -227,6 +251,18 @@ void stream_family(int nh, int bytes_per_elem) {
   time_variants(v, double(st.active) * st.T_ * bytes_per_elem, 3);
 }
 
+// Math family: the policy at its shipped shape with std::sqrt and with
+// sqrt_rn, interleaved in one process (so on the same buffers and pages), 5
+// rounds.
+template <typename Base, int NS>
+void math_family(int nh, int bytes_per_elem) {
+  State<typename Base::T, typename Base::S, NS> st;
+  std::vector<Variant> v;
+  v.push_back({"std::sqrt", [&st, nh] { return dense<PerElementStdSqrt<Base>>(st, nh); }, {}});
+  v.push_back({"sqrt_rn (shipped)", [&st, nh] { return dense<Base>(st, nh); }, {}});
+  time_variants(v, double(st.active) * st.T_ * bytes_per_elem, 5);
+}
+
 // The segmented float32 Adam update: the gradient as config 5's twelve
 // per-parameter (R, numel) tensors, the consolidated gradient not written.
 template <typename P, typename St>
@@ -317,6 +353,15 @@ bool run_stream(int nh, int bytes_per_elem) {
     return false;
   }
 }
+template <bool ON, typename P, int NS>
+bool run_math(int nh, int bytes_per_elem) {
+  if constexpr (ON) {
+    math_family<P, NS>(nh, bytes_per_elem);
+    return true;
+  } else {
+    return false;
+  }
+}
 template <bool ON>
 bool run_segment() {
   if constexpr (ON) {
@@ -362,6 +407,16 @@ int main(int argc, char** argv) {
   SWEEP_STREAM(adagrad_bf16state, 1, 4, 16, AdagradPolicy<float, bf16_t>)
   SWEEP_STREAM(adagrad_f16, 1, 4, 10, AdagradPolicy<_Float16>)
   SWEEP_STREAM(adagrad_bf16, 1, 4, 10, AdagradPolicy<bf16_t>)
+#define SWEEP_MATH(NAME, NS, NH, BYTES, ...) \
+  else if (fam == #NAME) ran = run_math<has(#NAME), __VA_ARGS__, NS>(NH, BYTES);
+  SWEEP_MATH(math_adam_f32, 2, 5, 28, AdamPolicy<float, false, false>)
+  SWEEP_MATH(math_adam_bf16state, 2, 5, 20, AdamPolicy<float, false, false, bf16_t>)
+  SWEEP_MATH(math_adam_f16, 2, 5, 14, AdamPolicy<_Float16, false, false>)
+  SWEEP_MATH(math_adam_bf16, 2, 5, 14, AdamPolicy<bf16_t, false, false>)
+  SWEEP_MATH(math_adagrad_f32, 1, 4, 20, AdagradPolicy<float>)
+  SWEEP_MATH(math_adagrad_f16, 1, 4, 10, AdagradPolicy<_Float16>)
+  SWEEP_MATH(math_adagrad_bf16, 1, 4, 10, AdagradPolicy<bf16_t>)
+#undef SWEEP_MATH
   else if (fam == "seg_adam_f32") ran = run_segment<has("seg_adam_f32")>();
   else {
     fprintf(stderr, "unknown family '%s'\n", fam.c_str());
