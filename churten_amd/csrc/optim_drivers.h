@@ -296,6 +296,15 @@ constexpr int64_t kCapMinElems = int64_t(8192) * 512;
 // 419 MB) lose 11-16% with plain accesses, so they stay non-temporal.
 constexpr int64_t kMallBytes = int64_t(256) << 20;
 
+// Launches above the MALL with at most kMidBytes of (R, T) operands reserve
+// each policy's kStreamLdsMid instead of its large-launch cap (with a
+// workspace). Measured with shape_sweep.hip at config 2's size (100 x 265,484,
+// 75% active; three runs on two boxes): float32 Adam at cap 20 5.85-5.94 TB/s
+// against 5.66-5.74 at its cap of 14, and with amsgrad 5.83-5.91 against
+// 5.73-5.79 at its cap of 12. From 2 GB of operands on (R = 128, T = 1M to
+// 8M) the large-launch caps were best or within 0.3%.
+constexpr int64_t kMidBytes = int64_t(1) << 30;
+
 // Packs per thread of the streaming driver, by operand types: float32
 // throughout, float32 params with bfloat16 state, 16-bit params, float64.
 // Measured per policy on config-5-sized state (1/2/4/8 packs, one process per
@@ -395,6 +404,8 @@ struct AdamPolicy {
   static constexpr int kStreamUnroll = stream_unroll<T, S>(2, 4, 1, 2);
   static constexpr uint32_t kStreamLdsPre =
       kBf16State<T, S> ? lds_for_residency(12) : kStreamLds;
+  static constexpr uint32_t kStreamLdsMid =
+      kFp32State<T, S> ? lds_for_residency(20) : kStreamLdsPre;
   static constexpr int kStreamUnrollPre = stream_unroll<T, S>(1, 2, 1, 2);
   static constexpr int kStreamUnrollSmall = stream_unroll<T, S>(2, 4, 4, 2);
   static constexpr int64_t kStreamSmallBytes = kMallBytes;
@@ -460,6 +471,7 @@ struct SgdPolicy {
   static constexpr uint32_t kStreamLds = HAS_BUF ? residency_lds<T, S>(20) : 0u;
   static constexpr int kStreamUnroll = stream_unroll<T, S>(HAS_BUF ? 1 : 2, 1, 1, 2);
   static constexpr uint32_t kStreamLdsPre = kStreamLds;
+  static constexpr uint32_t kStreamLdsMid = kStreamLdsPre;
   static constexpr int kStreamUnrollPre = kStreamUnroll;
   static constexpr int kStreamUnrollSmall = stream_unroll<T, S>(1, 1, 4, 2);
   static constexpr int64_t kStreamSmallBytes = kMallBytes;
@@ -508,6 +520,7 @@ struct AdagradPolicy {
   static constexpr uint32_t kStreamLds = residency_lds<T, S>(16);
   static constexpr int kStreamUnroll = stream_unroll<T, S>(2, 1, 1, 2);
   static constexpr uint32_t kStreamLdsPre = residency_lds<T, S>(20);
+  static constexpr uint32_t kStreamLdsMid = kStreamLdsPre;
   static constexpr int kStreamUnrollPre = stream_unroll<T, S>(1, 1, 4, 2);
   static constexpr int kStreamUnrollSmall = stream_unroll<T, S>(2, 1, 4, 2);
   static constexpr int64_t kStreamSmallBytes = kMallBytes;
@@ -557,6 +570,7 @@ struct AdagradF32Policy {
   static constexpr uint32_t kStreamLds = residency_lds<T, S>(16);
   static constexpr int kStreamUnroll = stream_unroll<T, S>(2, 1, 1, 2);
   static constexpr uint32_t kStreamLdsPre = residency_lds<T, S>(20);
+  static constexpr uint32_t kStreamLdsMid = kStreamLdsPre;
   static constexpr int kStreamUnrollPre = stream_unroll<T, S>(1, 1, 1, 2);
   static constexpr int kStreamUnrollSmall = stream_unroll<T, S>(2, 1, 4, 2);
   static constexpr int64_t kStreamSmallBytes = kMallBytes;
@@ -1738,12 +1752,13 @@ int run_step(const Call& c, const Vectors<typename P::T>& vec, Prepare&& prepare
   return launch();
 }
 
-// The streaming driver over `blocks` tiles, capped when the launch is large.
+// The streaming driver over `blocks` tiles, capped when the launch is large
+// (`mid`: the operands take at most kMidBytes; with a workspace only).
 template <typename P, bool PRE, bool SMALL>
-void launch_stream(const KArgs<P>& a, uint32_t blocks, bool same_phase, hipStream_t stream) {
-  const uint32_t lds = int64_t(blocks) * stream_tile<P, PRE, SMALL>() >= kCapMinElems
-                           ? stream_lds_of<P, PRE, SMALL>()
-                           : 0u;
+void launch_stream(const KArgs<P>& a, uint32_t blocks, bool same_phase, hipStream_t stream,
+                   bool mid = false) {
+  const uint32_t cap = PRE && !SMALL && mid ? P::kStreamLdsMid : stream_lds_of<P, PRE, SMALL>();
+  const uint32_t lds = int64_t(blocks) * stream_tile<P, PRE, SMALL>() >= kCapMinElems ? cap : 0u;
   if (same_phase) {
     hipLaunchKernelGGL((stream_kernel<P, false, PRE, SMALL>), dim3(blocks), dim3(kStreamThreads),
                        lds, stream, a);
@@ -1766,6 +1781,8 @@ int launch_dense(const Call& c, int nbufs) {
   const bool small =
       (pre || P::kPreWords == 0) &&
       c.R <= P::kStreamSmallBytes / operand_bytes_per_elem<P>() / std::max<int64_t>(c.T, 1);
+  const bool mid =
+      c.R <= kMidBytes / operand_bytes_per_elem<P>() / std::max<int64_t>(c.T, 1);
   const auto prepare = [&] {
     if (!fill_kargs<P>(c, nbufs, a, false)) return false;
     uint32_t res0 = 0, rmod = 0;
@@ -1790,7 +1807,7 @@ int launch_dense(const Call& c, int nbufs) {
           if (small) {
             launch_stream<P, true, true>(a, blocks, same_phase, c.stream);
           } else {
-            launch_stream<P, true, false>(a, blocks, same_phase, c.stream);
+            launch_stream<P, true, false>(a, blocks, same_phase, c.stream, mid);
           }
           return static_cast<int>(hipGetLastError());
         }

@@ -18,7 +18,7 @@
 //   hipcc --offload-arch=gfx950 -O3 -std=c++17 \
 //     -Xclang -target-feature -Xclang -packed-fp32-ops \
 //     -DSWEEP_FAMILY=adam_bf16state churten_amd/csrc/shape_sweep.hip -o shape_sweep
-//   ./shape_sweep adam_bf16state [cfg2|cfg4|cfg5]
+//   ./shape_sweep adam_bf16state [cfg2|cfg4|cfg5|RxTxPCT]
 // Families: adam_f32 adam_ams_f32 adam_bf16state adam_f16 adam_bf16 sgd_f32
 // sgd_bf16state sgd_f16 sgd_bf16 adagrad_f32 adagrad_bf16state adagrad_f16
 // adagrad_bf16 seg_adam_f32 (config 5 only); the math families math_adam_f32
@@ -58,6 +58,7 @@ struct StreamShape : Base {
   static constexpr int kStreamUnroll = U;
   static constexpr uint32_t kStreamLdsPre = CAP ? lds_for_residency(CAP) : 0u;
   static constexpr uint32_t kStreamLds = kStreamLdsPre;
+  static constexpr uint32_t kStreamLdsMid = kStreamLdsPre;
 };
 
 // A policy with its segmented shape (with a workspace) replaced; the cap is
@@ -380,8 +381,15 @@ int main(int argc, char** argv) {
   } else if (cfg == "cfg4") {
     g_work = Workload{64, 545100, 100};
   } else if (cfg != "cfg5") {
-    fprintf(stderr, "unknown workload '%s'\n", cfg.c_str());
-    return 2;
+    long r = 0, t = 0;
+    int pct = 0;
+    if (sscanf(cfg.c_str(), "%ldx%ldx%d", &r, &t, &pct) != 3 || r <= 0 || t <= 0 || t % 4 != 0 ||
+        pct <= 0 || pct > 100) {
+      fprintf(stderr, "unknown workload '%s' (cfg2, cfg4, cfg5 or RxTxPCT, T a multiple of 4)\n",
+              cfg.c_str());
+      return 2;
+    }
+    g_work = Workload{r, t, pct};
   }
   if (fam == "seg_adam_f32" && cfg != "cfg5") {
     fprintf(stderr, "the segmented family has config 5's layout only\n");
