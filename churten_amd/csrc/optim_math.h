@@ -135,16 +135,18 @@ struct AdamHyper {
 
 // A float divided by a per-replica constant b, as a multiply by the double
 // `rcp` = RN64(1 / b): RN32(RN64(x * rcp)) == RN32(x / b) for every float x
-// and b (zeros, infinities and NaNs included; rcp is +-inf for b = +-0 and
-// +-0 for b = +-inf). Why: x and b have 24-bit significands, so x / b is never
+// and b, bit for bit (zeros, infinities and NaNs included; rcp is +-inf for
+// b = +-0 and +-0 for b = +-inf), except when x and b are both NaN: then both
+// are NaN, the divide with x's payload, the product with b's (for Adam, b is
+// NaN only for a beta2 that makes 1 - beta2^step negative or NaN). Why: x and b have 24-bit significands, so x / b is never
 // a midpoint between two floats (a midpoint has a 25-bit odd significand M, and
 // x = b * M would need M to divide x's significand), and its distance to the
 // nearest midpoint is a nonzero multiple of 2^(e_b + e_q - 24) divided by b,
 // i.e. more than 2^-49 of |x / b|, also for subnormal x, b or quotient. The
 // double product errs by at most (1 + 2^-53)^2 - 1 < 2^-52 of it, so both sit
 // on the same side of every rounding boundary. Nine VALU instructions fewer per
-// element than the correctly rounded float divide; tests check the identity on
-// every float x for a set of b, and through the update against torch.
+// element than the correctly rounded float divide; tests check the identity bit
+// for bit on every float x for a set of b, and through the update against torch.
 __device__ __forceinline__ float div_by_rcp(float x, double rcp) {
   return static_cast<float>(static_cast<double>(x) * rcp);
 }

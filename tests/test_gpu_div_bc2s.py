@@ -1,11 +1,13 @@
 """Adam's float update divides sqrt(v) by the replica's bias_correction2_sqrt
 as a multiply by that divisor's correctly rounded double reciprocal. That is
 exact: the rounded product equals the correctly rounded quotient for every
-float pair. Checked here against torch's true division on the GPU, on every one
-of the 2^32 float bit patterns for a set of divisors (divisors Adam produces,
-odd significands, a subnormal and a huge one) and on random bit-pattern pairs.
-A plausible wrong form (the reciprocal rounded to float) fails the same
-comparison."""
+float pair, NaN bit patterns included, except where both operands are NaN
+(both results are NaN; the divide keeps x's payload, the product b's).
+Checked here against torch's true division on the GPU, bit for bit, on every
+one of the 2^32 float bit patterns for a set of divisors (divisors Adam
+produces, odd significands, a subnormal and a huge one) and on random
+bit-pattern pairs. A plausible wrong form (the reciprocal rounded to float)
+fails the same comparison."""
 
 from __future__ import annotations
 
@@ -50,9 +52,13 @@ def _div(lib, x, b, b_stride):
     return out
 
 
-def _mismatches(got, want):
-    both_nan = torch.isnan(got) & torch.isnan(want)
-    return ((got.view(torch.int32) != want.view(torch.int32)) & ~both_nan).nonzero()
+def _mismatches(got, want, both_nan=None):
+    # bit for bit, NaN payloads included; `both_nan` marks pairs whose operands
+    # are both NaN, where only NaN-ness has to agree
+    bad = got.view(torch.int32) != want.view(torch.int32)
+    if both_nan is not None:
+        bad &= ~(both_nan & torch.isnan(got) & torch.isnan(want))
+    return bad.nonzero()
 
 
 @pytest.mark.parametrize("b", DIVISORS, ids=[f"{d:.6g}" for d in DIVISORS])
@@ -88,7 +94,8 @@ def test_div_bc2s_random_pairs_and_sensitivity():
     b[: n // 2] = torch.rand(n // 2, generator=gen, device="cuda") + 2.0 ** -12
     got = _div(lib, x, b, 1)
     want = x / b
-    assert _mismatches(got, want).numel() == 0
+    assert _mismatches(got, want, torch.isnan(x) & torch.isnan(b)).numel() == 0
     # The same comparison catches the reciprocal rounded to float first.
     wrong = x * (1.0 / b)
-    assert _mismatches(wrong, want).numel() > 1000
+    finite = torch.isfinite(want)
+    assert _mismatches(wrong[finite], want[finite]).numel() > 1000
