@@ -51,11 +51,13 @@ namespace {
     }                                                                               \
   } while (0)
 
-// A policy with its streaming shape replaced (with and without a workspace).
+// A policy with its streaming shape replaced (with and without a workspace,
+// and for launches that fit the MALL, which run uncapped whatever CAP says).
 template <typename Base, int U, int CAP>
 struct StreamShape : Base {
   static constexpr int kStreamUnrollPre = U;
   static constexpr int kStreamUnroll = U;
+  static constexpr int kStreamUnrollSmall = U;
   static constexpr uint32_t kStreamLdsPre = CAP ? lds_for_residency(CAP) : 0u;
   static constexpr uint32_t kStreamLds = kStreamLdsPre;
   static constexpr uint32_t kStreamLdsMid = kStreamLdsPre;
