@@ -549,12 +549,13 @@ def lds_for_residency(n: int, lds_per_cu: int = 160 * 1024) -> int:
 
 def ceiling_timing(adam_args, launches: int):
     """The Adam step's traffic without its arithmetic on the same config-5
-    buffers (churten_amd/lib/libchurten_bench.so): 4 reads + 3 writes with the
-    update kernel's launch shape and residency cap (14 per CU) and at full
-    residency, the 4 reads alone and the 3 writes alone. `mix_bound` is the
-    rate a 16 B read + 12 B write element reaches if reads and writes each ran
-    at their own measured rate, one after the other. Runs last: the write-only
-    pass overwrites the buffers."""
+    buffers (churten_amd/lib/libchurten_bench.so), each kind at the best of a
+    few launch shapes (one-wave workgroups, 1 or 2 packs per thread, residency
+    caps): 4 reads + 3 writes, also at the update kernel's own shape (1 pack,
+    14 per CU); the 4 reads alone; the 3 writes alone. `mix_bound` is the rate
+    a 16 B read + 12 B write element reaches if reads and writes each ran at
+    their own best rate, one after the other. Runs last: the write-only passes
+    overwrite the buffers."""
     import ctypes
 
     import torch
@@ -570,11 +571,12 @@ def ceiling_timing(adam_args, launches: int):
     sink = torch.zeros(1, device=p.device)
     vp = lambda t: ctypes.c_void_p(t.data_ptr())  # noqa: E731
 
-    def rate(mode, c, lds, per_elem):
+    def rate(mode, c, packs, cap, per_elem):
+        lds = lds_for_residency(cap) if cap else 0
         call = lambda: lib.cb_traffic(  # noqa: E731
             ctypes.c_int(mode), vp(p), vp(gr), vp(m), vp(v), vp(mask), ctypes.c_int64(R),
-            ctypes.c_int64(T), ctypes.c_float(c), ctypes.c_uint32(lds), vp(sink),
-            ctypes.c_void_p(stream.cuda_stream))
+            ctypes.c_int64(T), ctypes.c_float(c), ctypes.c_uint32(lds), ctypes.c_int(packs),
+            vp(sink), ctypes.c_void_p(stream.cuda_stream))
         for _ in range(3):
             assert call() == 0
         e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
@@ -586,11 +588,19 @@ def ceiling_timing(adam_args, launches: int):
         ms = e0.elapsed_time(e1) / launches
         return round(active * T * per_elem / (ms * 1e-3) / 1e9, 1)
 
-    out = {"mix_4r3w_capped_GBs": rate(0, 0.0, lds_for_residency(14), 28),
-           "mix_4r3w_GBs": rate(0, 0.0, 0, 28),
-           "read_4_GBs": rate(1, -3.0e38, 0, 16),
-           "write_3_GBs": rate(2, 0.0, 0, 12)}
-    out["mix_bound_GBs"] = round(28 / (16 / out["read_4_GBs"] + 12 / out["write_3_GBs"]), 1)
+    def best(mode, c, shapes, per_elem):
+        rates = {(k, cap): rate(mode, c, k, cap, per_elem) for k, cap in shapes}
+        (k, cap), r = max(rates.items(), key=lambda kv: kv[1])
+        return r, f"{k} pack{'s' if k > 1 else ''}, " + (f"cap {cap}" if cap else "uncapped"), rates
+
+    mix, mix_shape, mix_rates = best(0, 0.0, [(1, 8), (1, 10), (1, 12), (1, 14), (2, 10)], 28)
+    reads, read_shape, _ = best(1, -3.0e38, [(1, 0), (2, 0), (2, 14)], 16)
+    writes, write_shape, _ = best(2, 0.0, [(1, 8), (1, 10), (1, 12), (2, 8)], 12)
+    out = {"mix_4r3w_GBs": mix, "mix_4r3w_shape": mix_shape,
+           "mix_4r3w_update_shape_GBs": mix_rates[(1, 14)],
+           "read_4_GBs": reads, "read_4_shape": read_shape,
+           "write_3_GBs": writes, "write_3_shape": write_shape}
+    out["mix_bound_GBs"] = round(28 / (16 / reads + 12 / writes), 1)
     return out
 
 
@@ -897,7 +907,7 @@ def main():
                if args.config == 5 and not args.no_ceiling else None)
     if ceiling is not None:
         kern_gbs = nbytes / (kern_ms * 1e-3) / 1e9
-        ceiling["update_kernel_of_capped_mix"] = round(kern_gbs / ceiling["mix_4r3w_capped_GBs"], 4)
+        ceiling["update_kernel_of_mix"] = round(kern_gbs / ceiling["mix_4r3w_GBs"], 4)
         ceiling["update_kernel_of_mix_bound"] = round(kern_gbs / ceiling["mix_bound_GBs"], 4)
     achieved = nbytes / (kern_ms * 1e-3) / 1e9
     fp64_roofline = None

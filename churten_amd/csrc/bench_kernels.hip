@@ -12,8 +12,9 @@
 // division.
 //
 // Same decomposition as the streaming driver at float32: one-wave workgroups,
-// 512-element tiles of (replica, tile) pairs, frozen replicas skipped, two
-// non-temporal 16-byte packs per thread per operand. Modes:
+// tiles of (replica, tile) pairs, frozen replicas skipped, one or two
+// non-temporal 16-byte packs per thread per operand (256- or 512-element
+// tiles). Modes:
 //   0  read params, grads, exp_avg, exp_avg_sq; write params, exp_avg,
 //      exp_avg_sq (28 B per active element, the Adam step's traffic)
 //   1  the four reads only (16 B)
@@ -29,19 +30,18 @@
 namespace {
 
 constexpr int kThreads = 64;
-constexpr int kUnroll = 2;
-constexpr int64_t kTile = int64_t(kThreads) * 4 * kUnroll;
 
 using F4 = float __attribute__((ext_vector_type(4)));
 
 __device__ __forceinline__ F4 ld(const F4* p) { return __builtin_nontemporal_load(p); }
 __device__ __forceinline__ void st(F4* p, F4 v) { __builtin_nontemporal_store(v, p); }
 
-template <int MODE>
+template <int MODE, int kUnroll>
 __global__ __launch_bounds__(kThreads) void traffic_kernel(float* p, const float* g, float* m,
                                                            float* v, const uint8_t* mask,
                                                            int64_t T, uint32_t tiles, float c,
                                                            float* sink) {
+  constexpr int64_t kTile = int64_t(kThreads) * 4 * kUnroll;
   const uint32_t b = blockIdx.x;
   const uint32_t r = b / tiles;
   const int64_t t0 = int64_t(b - r * tiles) * kTile;
@@ -173,30 +173,29 @@ extern "C" int cb_div_bc2s(const float* x, const float* b, int64_t b_stride, flo
 }
 
 // The pattern over the active rows of four row-major (R, T) float32 buffers:
-// T a multiple of 4, every base 16-byte aligned, `mask` R bytes. `lds` is the
-// dynamic LDS per workgroup (a residency cap, as the streaming driver's).
-// Returns 0, 1 on bad arguments, or the HIP error code.
+// T a multiple of 4, every base 16-byte aligned, `mask` R bytes, `packs` 1 or
+// 2 per thread. `lds` is the dynamic LDS per workgroup (a residency cap, as
+// the streaming driver's). Returns 0, 1 on bad arguments, or the HIP error
+// code.
 extern "C" int cb_traffic(int mode, float* p, const float* g, float* m, float* v,
                           const uint8_t* mask, int64_t R, int64_t T, float c, uint32_t lds,
-                          float* sink, hipStream_t stream) {
-  if (R <= 0 || T <= 0 || T % 4 != 0 || mode < 0 || mode > 2) return 1;
+                          int packs, float* sink, hipStream_t stream) {
+  if (R <= 0 || T <= 0 || T % 4 != 0 || mode < 0 || mode > 2 || packs < 1 || packs > 2) return 1;
   for (const void* q : {static_cast<const void*>(p), static_cast<const void*>(g),
                         static_cast<const void*>(m), static_cast<const void*>(v)}) {
     if (reinterpret_cast<uintptr_t>(q) % 16 != 0) return 1;
   }
-  const int64_t tiles = (T + kTile - 1) / kTile;
+  const int64_t tile = int64_t(kThreads) * 4 * packs;
+  const int64_t tiles = (T + tile - 1) / tile;
   if (tiles > INT32_MAX || R > INT32_MAX / tiles) return 1;
   const dim3 grid(static_cast<uint32_t>(R * tiles)), block(kThreads);
   const uint32_t t32 = static_cast<uint32_t>(tiles);
-  if (mode == 0) {
-    hipLaunchKernelGGL(traffic_kernel<0>, grid, block, lds, stream, p, g, m, v, mask, T, t32, c,
-                       sink);
-  } else if (mode == 1) {
-    hipLaunchKernelGGL(traffic_kernel<1>, grid, block, lds, stream, p, g, m, v, mask, T, t32, c,
-                       sink);
-  } else {
-    hipLaunchKernelGGL(traffic_kernel<2>, grid, block, lds, stream, p, g, m, v, mask, T, t32, c,
-                       sink);
-  }
+  using K = void (*)(float*, const float*, float*, float*, const uint8_t*, int64_t, uint32_t,
+                     float, float*);
+  const K kernels[3][2] = {{traffic_kernel<0, 1>, traffic_kernel<0, 2>},
+                           {traffic_kernel<1, 1>, traffic_kernel<1, 2>},
+                           {traffic_kernel<2, 1>, traffic_kernel<2, 2>}};
+  hipLaunchKernelGGL(kernels[mode][packs - 1], grid, block, lds, stream, p, g, m, v, mask, T, t32,
+                     c, sink);
   return static_cast<int>(hipGetLastError());
 }

@@ -15,17 +15,19 @@ pytestmark = pytest.mark.gpu
 LIB = Path(__file__).resolve().parents[1] / "churten_amd" / "lib" / "libchurten_bench.so"
 
 
-def call(lib, mode, ts, mask, c, sink, R=None, T=None):
+def call(lib, mode, ts, mask, c, sink, R=None, T=None, packs=2):
     vp = lambda t: ctypes.c_void_p(t.data_ptr())  # noqa: E731
     R = ts[0].shape[0] if R is None else R
     T = ts[0].shape[1] if T is None else T
     return lib.cb_traffic(ctypes.c_int(mode), *[vp(t) for t in ts], vp(mask), ctypes.c_int64(R),
-                          ctypes.c_int64(T), ctypes.c_float(c), ctypes.c_uint32(0), vp(sink),
+                          ctypes.c_int64(T), ctypes.c_float(c), ctypes.c_uint32(0),
+                          ctypes.c_int(packs), vp(sink),
                           ctypes.c_void_p(torch.cuda.current_stream().cuda_stream))
 
 
+@pytest.mark.parametrize("packs", [1, 2])
 @pytest.mark.parametrize("T", [4, 1000, 1028, 4096])
-def test_traffic_modes(T):
+def test_traffic_modes(T, packs):
     lib = ctypes.CDLL(str(LIB))
     R = 3
     g = torch.Generator(device="cuda").manual_seed(T)
@@ -33,13 +35,13 @@ def test_traffic_modes(T):
     before = [t.clone() for t in ts]
     mask = torch.tensor([True, False, True], device="cuda")
     sink = torch.full((1,), 7.0, device="cuda")
-    assert call(lib, 0, ts, mask, 0.0, sink) == 0      # x + g * 0: unchanged
-    assert call(lib, 1, ts, mask, -3.0e38, sink) == 0  # reads only
+    assert call(lib, 0, ts, mask, 0.0, sink, packs=packs) == 0      # x + g * 0: unchanged
+    assert call(lib, 1, ts, mask, -3.0e38, sink, packs=packs) == 0  # reads only
     torch.cuda.synchronize()
     for a, b in zip(ts, before):
         assert torch.equal(a, b)
     assert sink.item() == 7.0
-    assert call(lib, 2, ts, mask, 1.5, sink) == 0      # writes c to p, m, v of active rows
+    assert call(lib, 2, ts, mask, 1.5, sink, packs=packs) == 0      # writes c to p, m, v of active rows
     torch.cuda.synchronize()
     for i in (0, 2, 3):
         assert torch.equal(ts[i][mask], torch.full_like(ts[i][mask], 1.5))
@@ -53,6 +55,7 @@ def test_traffic_rejects_bad_arguments():
     mask = torch.ones(2, dtype=torch.bool, device="cuda")
     sink = torch.zeros(1, device="cuda")
     assert call(lib, 3, ts, mask, 0.0, sink) == 1                 # no such mode
+    assert call(lib, 0, ts, mask, 0.0, sink, packs=3) == 1        # 1 or 2 packs only
     assert call(lib, 0, ts, mask, 0.0, sink, T=6) == 1            # T not a multiple of 4
     odd = [t.view(-1)[1:9].view(1, 8) for t in ts]               # 4-byte aligned only
     assert call(lib, 0, odd, mask, 0.0, sink, R=1) == 1
