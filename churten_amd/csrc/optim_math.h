@@ -179,6 +179,18 @@ __device__ __forceinline__ AdamConsts<opmath_t> adam_consts(
 __device__ __forceinline__ float adam_div_bc2s(float s, double d) { return div_by_rcp(s, d); }
 __device__ __forceinline__ double adam_div_bc2s(double s, double d) { return s / d; }
 
+// ATen's `x + eps` with eps a double (x the float quotient above), narrowed to
+// the float math type. eps holds a float value here (the hyperparameter
+// tensors are float, or half / bfloat16, widened), and for two floats the sum
+// rounded to double and then to float equals the sum rounded to float once:
+// double rounding is harmless for addition because 53 >= 2 * 24 + 1 bits. So
+// one float add gives ATen's bits (two fp64-unit instructions fewer); tests
+// check the identity on every float x for a set of eps.
+__device__ __forceinline__ float adam_add_eps(float x, double eps) {
+  return x + static_cast<float>(eps);
+}
+__device__ __forceinline__ double adam_add_eps(double x, double eps) { return x + eps; }
+
 // The first part of ATen's adam_math for one element: maximize, weight decay,
 // the two moments (and the running maximum with amsgrad). Returns the value
 // whose square root the denominator takes.
@@ -220,7 +232,7 @@ template <typename opmath_t>
 __device__ __forceinline__ void adam_finish(opmath_t& param, const opmath_t exp_avg,
                                             const opmath_t root, const AdamHyper& h,
                                             const AdamConsts<opmath_t>& c) {
-  const opmath_t denom = adam_div_bc2s(root, c.bc2s_div) + h.eps;
+  const opmath_t denom = adam_add_eps(adam_div_bc2s(root, c.bc2s_div), h.eps);
   param -= c.step_size * exp_avg / denom;
 }
 
