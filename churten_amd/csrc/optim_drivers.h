@@ -212,13 +212,36 @@ struct Operands {
 // `pre`: the call's per-replica constants (kPreWords doubles per replica,
 // replica r at pre + kPreStride * r), written by the preparation launch; null
 // when the workgroups derive them themselves.
+// `ilp_rows`: which rows torch's fused kernels would run on their vector path
+// (see ilp_row).
 template <typename T>
 struct Vectors {
   const T* steps;
   const T* h[5];
   const uint8_t* mask;
   const double* pre;
+  uint32_t ilp_rows;
 };
+
+// Whether row r takes the vector path of torch's fused optimizer kernels (and
+// of the reference's row kernel, adagrad.cu:119-133): the row's length a
+// multiple of 4 and every operand's row pointer aligned to 4 elements, with
+// unit inner stride (ATen MultiTensorApply's kILP = 4; its chunks start at
+// multiples of 4). `rule` is 0 when no row does; else bit 0 is set and
+// operand b < 3 adds its base's element offset modulo 4 (bits 1+4b, 2+4b) and
+// its row stride modulo 4 (bits 3+4b, 4+4b); row r is aligned in operand b
+// when their (offset + r * stride) is 0 modulo 4.
+__device__ __forceinline__ bool ilp_row(uint32_t rule, uint32_t r) {
+  if (rule == 0) return false;
+  bool ok = true;
+#pragma unroll
+  for (int b = 0; b < 3; ++b) {
+    const uint32_t res = (rule >> (1 + 4 * b)) & 3u;
+    const uint32_t mod = (rule >> (3 + 4 * b)) & 3u;
+    ok = ok && ((res + r * mod) & 3u) == 0;
+  }
+  return ok;
+}
 
 // Doubles per replica in a workspace of per-replica constants.
 constexpr int kPreStride = 2;
@@ -533,6 +556,7 @@ struct AdagradPolicy {
   static constexpr int kPreWords = 1;
   struct Rep {
     AdagradHyper h;
+    bool once;  // float16 state sum rounded once (ilp_row)
   };
   // corrected_lr of the bumped step.
   __device__ static void precompute(const Vectors<T>& v, uint32_t r, double* out) {
@@ -543,6 +567,7 @@ struct AdagradPolicy {
   __device__ static void prologue(const Vectors<T>& v, uint32_t r, Rep& rep) {
     rep.h.weight_decay = hyper_at(v.h[2], r);
     rep.h.eps = hyper_at(v.h[3], r);
+    rep.once = kHalf && ilp_row(v.ilp_rows, r);
     if constexpr (PRE) {
       rep.h.corrected_lr = v.pre[kPreStride * r];
     } else {
@@ -553,7 +578,27 @@ struct AdagradPolicy {
   __device__ static bool reads_state(const Vectors<T>&, uint32_t) { return true; }
   __device__ static bool decays(const Rep& rep) { return rep.h.weight_decay != 0; }
   __device__ static void drop_decay(Rep& rep) { rep.h.weight_decay = 0.0; }
+  // float16 parameters and state. torch's fused Adagrad stores the state sum
+  // of a row on its vector path (ilp_row) rounded once from the exact
+  // g * g + s, g the maximized and decayed gradient (its build turns the float
+  // fma and the narrowing into one v_fma_mix); on its element path it stores
+  // the float sum, which the square root takes everywhere, rounded to half.
+  // The two differ where g * g + s lies within a quarter of a float ulp of a
+  // half-way point between two halves without being one (such as a half-way
+  // g * g and a float16 subnormal s). The once-rounded form agrees with torch
+  // on every pair of float16 (g, s) values, maximize either way; bfloat16 and
+  // the other types store the rounded float sum on both paths.
+  static constexpr bool kHalf = std::is_same_v<T, _Float16> && std::is_same_v<S, _Float16>;
   __device__ static void update(M& p, M g, M (&s)[NS], const Rep& rep, bool maximize) {
+    if constexpr (kHalf) {
+      if (rep.once) {
+        const M s_in = s[0];
+        adagrad_sum<M>(p, g, s[0], rep.h, maximize);
+        adagrad_finish<M>(p, g, sqrt_rn(s[0]), rep.h);
+        s[0] = fma_half(g, g, s_in);
+        return;
+      }
+    }
     adagrad_element<M>(p, g, s[0], rep.h, maximize);
   }
 };
@@ -1682,6 +1727,25 @@ bool uses_workspace(const Call& c) {
   return P::kPreWords > 0 && c.ws != nullptr;
 }
 
+// The rule ilp_row decodes, over the first three operands (parameters,
+// gradients, first state; an absent gradient counts as aligned, as the
+// freshly allocated buffer it stands for).
+template <typename P>
+uint32_t ilp_rows_rule(const Operands<typename P::T>& x, int64_t cols) {
+  if (cols % 4 != 0) return 0;
+  uint32_t rule = 1;
+  for (int b = 0; b < 3; ++b) {
+    if (x.data[b] == nullptr) continue;
+    const size_t elem = b < 2 ? sizeof(typename P::T) : sizeof(typename P::S);
+    const uintptr_t addr = reinterpret_cast<uintptr_t>(x.data[b]);
+    if (x.stride_t[b] != 1 || addr % elem != 0) return 0;
+    const uint32_t res = static_cast<uint32_t>((addr / elem) % 4);
+    const uint32_t mod = static_cast<uint32_t>(((x.stride_r[b] % 4) + 4) % 4);
+    rule |= res << (1 + 4 * b) | mod << (3 + 4 * b);
+  }
+  return rule;
+}
+
 template <typename P>
 bool fill_kargs(const Call& c, int nbufs, KArgs<P>& a, bool grad_optional) {
   using T = typename P::T;
@@ -1693,6 +1757,7 @@ bool fill_kargs(const Call& c, int nbufs, KArgs<P>& a, bool grad_optional) {
   }
   a.vec.mask = c.mask;
   a.vec.pre = uses_workspace<P>(c) ? static_cast<const double*>(c.ws) : nullptr;
+  a.vec.ilp_rows = ilp_rows_rule<P>(a.x, c.T);
   a.maximize = (c.flags & TS_MAXIMIZE) != 0;
   return true;
 }

@@ -74,6 +74,17 @@ template <> __device__ __forceinline__ bf16_t narrow<bf16_t>(float x) {
   return out;
 }
 
+// a * b + c rounded once, to half (v_fma_mixlo_f16 on float operands: the
+// exact value, one rounding to nearest even, half subnormals kept), returned
+// as the float holding that half, which narrow<_Float16> passes unchanged.
+// Rounding the float fma to half instead rounds twice, and differs where the
+// float result is a half-way point between two halves and the exact one is not.
+__device__ __forceinline__ float fma_half(float a, float b, float c) {
+  uint32_t d = 0;
+  asm("v_fma_mixlo_f16 %0, %1, %2, %3" : "+v"(d) : "v"(a), "v"(b), "v"(c));
+  return static_cast<float>(__builtin_bit_cast(_Float16, static_cast<uint16_t>(d)));
+}
+
 // Two floats to a packed pair of bfloat16 (first in the low half), each exactly
 // as narrow<bf16_t>: one v_cvt_pk_bf16_f32 for both, with NaN made torch's
 // 0x7FC0 on the float side (the conversion keeps a quiet NaN's top bits, and

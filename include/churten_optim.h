@@ -132,7 +132,12 @@ int ts_sgd_step(const ts_rt_buf* bufs, ts_dtype dtype, void* state_steps,
 /* Fused Adagrad (lr_decay, weight decay, maximize) over (R, T), fp64 element
  * math as ROCm ATen's `adagrad_math` (ATen/native/hip/fused_adagrad_utils.cuh,
  * called by the reference at csrc/cuda/adagrad.cu:141-148).
- * bufs: [0] params (rw), [1] grads (r), [2] state_sums (rw). */
+ * bufs: [0] params (rw), [1] grads (r), [2] state_sums (rw).
+ * float16: a row whose length is a multiple of 4, with unit inner stride and
+ * all three row pointers aligned to 4 elements (the vector path of torch's
+ * fused kernels and of adagrad.cu:119-133) stores its state sum rounded once
+ * from the exact g*g + s, as torch's ROCm build does there; other rows store
+ * the float sum rounded to half. */
 int ts_adagrad_step(const ts_rt_buf* bufs, ts_dtype dtype, void* state_steps,
                     const void* lr, const void* lr_decay,
                     const void* weight_decay, const void* eps,

@@ -42,13 +42,17 @@ def _vecs(R, *rows, dtype=torch.float32):
 # float64 parameters: the products inside the update are inexact there, so these
 # cases also pin which multiply-adds torch's build fuses. 16-bit parameters: the
 # update narrows a double expression to the float math value and that to the
-# storage type, two roundings that must not be folded into one (70001-element
-# rows hit the half-way cases).
+# storage type, two roundings that must not be folded into one (long rows hit
+# the half-way cases). torch runs rows whose length is a multiple of 4 on its
+# vector path and the others element by element, two separately compiled
+# bodies: 262144-element rows (four of its 65536-element chunks) take the first
+# at length, 70001-element rows the second.
 DTYPES = [torch.float32, torch.float64, torch.float16, torch.bfloat16]
+ROWS = [64, 45, 70001, 262144]
 
 
 @pytest.mark.parametrize("dtype", DTYPES, ids=str)
-@pytest.mark.parametrize("T", [64, 45, 70001])
+@pytest.mark.parametrize("T", ROWS)
 @pytest.mark.parametrize("amsgrad,maximize,decoupled,wd",
                          list(itertools.product([False, True], [False, True],
                                                 [False, True], [0.0, 1e-2])))
@@ -88,7 +92,7 @@ def test_adam_rows_bit_identical_to_aten(T, amsgrad, maximize, decoupled, wd, dt
 
 # torch warns that is_first_step means nothing without momentum buffers.
 @pytest.mark.filterwarnings("ignore:`is_first_step` argument has no effect")
-@pytest.mark.parametrize("T", [64, 45, 70001])
+@pytest.mark.parametrize("T", ROWS)
 @pytest.mark.parametrize("momentum,dampening,wd,nesterov,maximize", [
     c for c in itertools.product([0.0, 0.9], [0.0, 0.3], [0.0, 1e-2], [False, True],
                                  [False, True])
@@ -136,7 +140,7 @@ def test_sgd_rows_bit_identical_to_aten(T, momentum, dampening, wd, nesterov,
 # momentum reduce to (its buffer, which ATen does not keep, is checked against
 # the oracle by the golden-case tests).
 @pytest.mark.filterwarnings("ignore:`is_first_step` argument has no effect")
-@pytest.mark.parametrize("T", [45, 70001])
+@pytest.mark.parametrize("T", [45, 70001, 262144])
 @pytest.mark.parametrize("maximize,wd", [(False, 0.0), (True, 1e-2)])
 @pytest.mark.parametrize("dtype", DTYPES, ids=str)
 def test_sgd_config3_flags_bit_identical_to_aten(T, maximize, wd, dtype):
@@ -179,7 +183,7 @@ def test_sgd_config3_flags_bit_identical_to_aten(T, maximize, wd, dtype):
     assert torch.equal(steps, ref_steps)
 
 
-@pytest.mark.parametrize("T", [64, 45, 70001])
+@pytest.mark.parametrize("T", ROWS)
 @pytest.mark.parametrize("lr_decay,wd,eps,maximize", list(itertools.product(
     [0.0, 1e-2], [0.0, 1e-2], [1e-10, 1e-6], [False, True])))
 @pytest.mark.parametrize("dtype", DTYPES, ids=str)

@@ -10,6 +10,11 @@ cases draw the layout at random -- row width, column offset inside a wider
 buffer, row padding, transposed storage, mixed layouts across operands,
 parameter dtype, bfloat16 state, optimizer and flags, frozen replicas -- and
 compare each against the same step on contiguous copies.
+
+One exception follows torch: float16 Adagrad rounds the state sum once on rows
+that torch's fused kernel runs on its vector path and twice elsewhere, so each
+of its rows is compared with contiguous copies whose rows take the same path
+(the plain copies, or copies one element off alignment).
 """
 
 from __future__ import annotations
@@ -47,6 +52,15 @@ def placed(t: torch.Tensor, kind: str, off: int, pad: int) -> torch.Tensor:
         v = buf[:, off:off + 2 * T:2]
     v.copy_(t)
     return v
+
+
+def vector_rows(ops) -> torch.Tensor:
+    """Per row of (R, T) operands, ATen's vector-path condition: the length a
+    multiple of 4, unit inner stride, row pointers aligned to 4 elements."""
+    R = ops[0].shape[0]
+    return torch.tensor([all(t.shape[1] % 4 == 0 and t.stride(1) == 1 and
+                             t[r].data_ptr() % (4 * t.element_size()) == 0 for t in ops)
+                         for r in range(R)], device=DEV)
 
 
 def draw(rng: random.Random):
@@ -112,6 +126,14 @@ def run_case(c):
     for _ in range(2):
         step(view, s_view)
         step(dense, s_dense)
+    if op == "adagrad" and dt == torch.float16:
+        # the same rows of the element path: row stride T + 4, one element in
+        off_path = [placed(t, "rows", 1, 3) for t in bufs]
+        s_off = steps.clone()
+        for _ in range(2):
+            step(off_path, s_off)
+        on = vector_rows(view).view(R, 1)
+        dense = [torch.where(on, b, e) for b, e in zip(dense, off_path)]
     torch.cuda.synchronize()
     assert torch.equal(s_view, s_dense)
     for i, (a, b) in enumerate(zip(view, dense)):

@@ -209,6 +209,14 @@ def run_both(device, op, kw, kind, dtype, with_out, strided_grads, strided_state
             a["G"] = column_view(G0, offset)
     b = dict(p=p.clone(), st=clone_all(st), steps=steps.clone(),
              G=G0.clone() if with_out else torch.zeros_like(G0))
+    if offset and op == "adagrad" and dtype == torch.float16:
+        # float16 Adagrad rounds its state once on the rows torch's fused kernel
+        # runs on its vector path (aligned rows) and twice elsewhere: the
+        # consolidated update runs on the same layout, so its rows agree
+        b["p"] = column_view(p, offset)
+        b["st"] = [column_view(x, offset) if x is not None else None for x in st]
+        if with_out:
+            b["G"] = column_view(G0, offset)
     for _ in range(n_steps):
         grads = make_grads(shapes, R, dtype, device, gen, strided_grads)
         seg_grads = [at_offset(g, offset) for g in grads] if offset else grads
