@@ -388,6 +388,10 @@ constexpr int stream_unroll(int fp32, int bf16_state, int narrow, int wide) {
 // `decays` / `drop_decay`: whether the replica's weight-decay term is live, and
 // a copy of its constants with the decay set to a literal zero (the element
 // math then skips the term, exactly as it does for a zero decay at run time).
+// `kVariant` / `variant` / `set_variant`: a per-replica choice between two
+// forms of the element math (float16 Adagrad's once- or twice-rounded state
+// sum), which the streaming and segmented drivers branch on once per
+// workgroup with the choice set to a literal (with_variant).
 //
 // Streaming shape with a workspace (kStreamUnrollPre, kStreamLdsPre). Without
 // the pow in every workgroup, float32 Adam runs fastest with one pack per
@@ -438,6 +442,7 @@ struct AdamPolicy {
   static constexpr int kSegmentThreadsPre = kFp32State<T, S> ? kStreamThreads : kThreads;
   static constexpr int kSegmentUnrollPre = kFp32State<T, S> ? 1 : kSegmentUnroll;
   static constexpr bool kLateStores = !AMSGRAD && std::is_same<T_, float>::value;
+  static constexpr bool kVariant = false;
   static constexpr int kPreWords = 2;
   struct Rep {
     AdamHyper h;
@@ -504,6 +509,7 @@ struct SgdPolicy {
   static constexpr int kSegmentThreadsPre = kThreads;
   static constexpr int kSegmentUnrollPre = kSegmentUnroll;
   static constexpr bool kLateStores = std::is_same<T_, float>::value;
+  static constexpr bool kVariant = false;
   static constexpr int kPreWords = 0;
   struct Rep {
     SgdHyper<double> h;
@@ -553,6 +559,7 @@ struct AdagradPolicy {
   static constexpr int kSegmentThreadsPre = kThreads;
   static constexpr int kSegmentUnrollPre = kSegmentUnroll;
   static constexpr bool kLateStores = false;
+  static constexpr bool kVariant = std::is_same_v<T, _Float16> && std::is_same_v<S, _Float16>;
   static constexpr int kPreWords = 1;
   struct Rep {
     AdagradHyper h;
@@ -567,7 +574,7 @@ struct AdagradPolicy {
   __device__ static void prologue(const Vectors<T>& v, uint32_t r, Rep& rep) {
     rep.h.weight_decay = hyper_at(v.h[2], r);
     rep.h.eps = hyper_at(v.h[3], r);
-    rep.once = kHalf && ilp_row(v.ilp_rows, r);
+    rep.once = kVariant && ilp_row(v.ilp_rows, r);
     if constexpr (PRE) {
       rep.h.corrected_lr = v.pre[kPreStride * r];
     } else {
@@ -588,9 +595,45 @@ struct AdagradPolicy {
   // g * g and a float16 subnormal s). The once-rounded form agrees with torch
   // on every pair of float16 (g, s) values, maximize either way; bfloat16 and
   // the other types store the rounded float sum on both paths.
-  static constexpr bool kHalf = std::is_same_v<T, _Float16> && std::is_same_v<S, _Float16>;
+  __device__ static bool variant(const Rep& rep) { return rep.once; }
+  __device__ static void set_variant(Rep& rep, bool once) { rep.once = once; }
+  // A pack on a vector-path row (false otherwise, for the generic form): the
+  // update as apply_pack's, then the state pairs straight out of
+  // v_fma_mixlo/hi_f16 on the decayed gradients and the sums as loaded, in
+  // place of narrowing the float sums (one instruction more per pair).
+  template <int N>
+  __device__ static bool update_pack(Pack<T, N>& vp, const Pack<T, N>& vg, Pack<S, N>& vs,
+                                     const Rep& rep, bool maximize) {
+    static_assert(N % 2 == 0, "state pairs");
+    if (!rep.once) return false;
+    struct Words {
+      uint32_t w[N / 2];
+    };
+    const Words s_in = __builtin_bit_cast(Words, vs);
+    M pm[N], gm[N], sm[N];
+#pragma unroll
+    for (int e = 0; e < N; ++e) {
+      pm[e] = widen(vp.v[e]);
+      gm[e] = widen(vg.v[e]);
+      sm[e] = widen(vs.v[e]);
+    }
+#pragma unroll
+    for (int e = 0; e < N; ++e) {
+      adagrad_sum<M>(pm[e], gm[e], sm[e], rep.h, maximize);
+      adagrad_finish<M>(pm[e], gm[e], sqrt_rn(sm[e]), rep.h);
+    }
+    Words out;
+#pragma unroll
+    for (int k = 0; k < N / 2; ++k) {
+      out.w[k] = fma_half2_sq(gm[2 * k], gm[2 * k + 1], s_in.w[k]);
+    }
+    vs = __builtin_bit_cast(Pack<S, N>, out);
+#pragma unroll
+    for (int e = 0; e < N; ++e) vp.v[e] = narrow<T>(pm[e]);
+    return true;
+  }
   __device__ static void update(M& p, M g, M (&s)[NS], const Rep& rep, bool maximize) {
-    if constexpr (kHalf) {
+    if constexpr (kVariant) {
       if (rep.once) {
         const M s_in = s[0];
         adagrad_sum<M>(p, g, s[0], rep.h, maximize);
@@ -625,6 +668,7 @@ struct AdagradF32Policy {
   static constexpr int kSegmentThreadsPre = kThreads;
   static constexpr int kSegmentUnrollPre = kSegmentUnroll;
   static constexpr bool kLateStores = false;
+  static constexpr bool kVariant = false;
   static constexpr int kPreWords = 1;
   struct Rep {
     AdagradF32Hyper h;
@@ -776,6 +820,9 @@ __device__ __forceinline__ void apply_pack(Pack<typename P::T, N>& vp,
                                            bool maximize) {
   using M = typename P::M;
   constexpr int SS = state_slots<P>();
+  if constexpr (P::kVariant) {
+    if (P::template update_pack<N>(vp, vg, vs[0], rep, maximize)) return;
+  }
   M pm[N], gm[N];
   M sm[SS][N];
 #pragma unroll
@@ -811,6 +858,42 @@ template <typename P>
 __device__ __forceinline__ typename P::S* state_row(const Operands<typename P::T>& x, int b,
                                                     uint32_t r) {
   return reinterpret_cast<typename P::S*>(x.data[b]) + int64_t(r) * x.stride_r[b];
+}
+
+// Runs `f` on the replica's constants with the policy's variant choice, if it
+// has one, set to a literal: one branch per workgroup, and element math
+// compiled for each choice.
+template <typename P, typename F>
+__device__ __forceinline__ void with_variant(const typename P::Rep& rep, F&& f) {
+  if constexpr (P::kVariant) {
+    typename P::Rep fixed = rep;
+    if (P::variant(rep)) {
+      P::set_variant(fixed, true);
+      f(fixed);
+    } else {
+      P::set_variant(fixed, false);
+      f(fixed);
+    }
+  } else {
+    f(rep);
+  }
+}
+
+// Runs `f` with `maximize` as a literal for policies with a variant, whose
+// pack form takes the sign-corrected gradient as a value (a run-time flag
+// would cost a negation and a select per element there); others get the
+// run-time flag.
+template <typename P, typename F>
+__device__ __forceinline__ void with_maximize(bool maximize, F&& f) {
+  if constexpr (P::kVariant) {
+    if (maximize) {
+      f(true);
+    } else {
+      f(false);
+    }
+  } else {
+    f(maximize);
+  }
 }
 
 // ---------------------------------------------------------------------------
@@ -907,9 +990,11 @@ __global__ __launch_bounds__(kStreamThreads) void stream_kernel(KArgs<P> a) {
   if (!a.maximize && !P::decays(rep)) {
     typename P::Rep plain = rep;
     P::drop_decay(plain);
-    compute(plain, false);
+    with_variant<P>(plain, [&](const typename P::Rep& rp) { compute(rp, false); });
   } else {
-    compute(rep, a.maximize);
+    with_variant<P>(rep, [&](const typename P::Rep& rp) {
+      with_maximize<P>(a.maximize, [&](bool mx) { compute(rp, mx); });
+    });
   }
   if constexpr (P::kLateStores) {
 #pragma unroll
@@ -1366,24 +1451,28 @@ __global__ __launch_bounds__((segment_threads<P, PRE>())) void segment_kernel(Se
       }
     }
   }
+  with_variant<P>(rep, [&](const typename P::Rep& rp) {
+    with_maximize<P>(a.k.maximize, [&](bool mx) {
 #pragma unroll
-  for (int u = 0; u < U; ++u) {
-    const int64_t i = int64_t(u) * NTH + threadIdx.x;
-    if (i < t.packs) {
-      if (store_grad) {
-        gout.store(i, vg[u]);
+      for (int u = 0; u < U; ++u) {
+        const int64_t i = int64_t(u) * NTH + threadIdx.x;
+        if (i < t.packs) {
+          if (store_grad) {
+            gout.store(i, vg[u]);
+          }
+          Pack<S> st[SS];
+#pragma unroll
+          for (int b = 0; b < NS; ++b) st[b] = vs[b][u];
+          apply_pack<P, kPack>(vp[u], vg[u], st, load_state, rp, mx);
+#pragma unroll
+          for (int b = 0; b < NS; ++b) vs[b][u] = st[b];
+          store_stream(pp + i, vp[u]);
+#pragma unroll
+          for (int b = 0; b < NS; ++b) sp[b].store(i, vs[b][u]);
+        }
       }
-      Pack<S> st[SS];
-#pragma unroll
-      for (int b = 0; b < NS; ++b) st[b] = vs[b][u];
-      apply_pack<P, kPack>(vp[u], vg[u], st, load_state, rep, a.k.maximize);
-#pragma unroll
-      for (int b = 0; b < NS; ++b) vs[b][u] = st[b];
-      store_stream(pp + i, vp[u]);
-#pragma unroll
-      for (int b = 0; b < NS; ++b) sp[b].store(i, vs[b][u]);
-    }
-  }
+    });
+  });
   seg_singles<NTH>(t, numel, one);
 }
 

@@ -85,6 +85,20 @@ __device__ __forceinline__ float fma_half(float a, float b, float c) {
   return static_cast<float>(__builtin_bit_cast(_Float16, static_cast<uint16_t>(d)));
 }
 
+// The pair (a0 * a0 + c.lo, a1 * a1 + c.hi) for float a0, a1 and a packed
+// pair of halves c (as loaded), each rounded once to half as fma_half, packed
+// the same way: v_fma_mixlo_f16 writes the low half, v_fma_mixhi_f16 the high
+// half of the same register, and op_sel picks c's half as an f16 operand (no
+// conversion of c).
+__device__ __forceinline__ uint32_t fma_half2_sq(float a0, float a1, uint32_t c) {
+  uint32_t d;
+  asm("v_fma_mixlo_f16 %0, %1, %1, %3 op_sel_hi:[0,0,1]\n\t"
+      "v_fma_mixhi_f16 %0, %2, %2, %3 op_sel:[0,0,1] op_sel_hi:[0,0,1]"
+      : "=&v"(d)
+      : "v"(a0), "v"(a1), "v"(c));
+  return d;
+}
+
 // Two floats to a packed pair of bfloat16 (first in the low half), each exactly
 // as narrow<bf16_t>: one v_cvt_pk_bf16_f32 for both, with NaN made torch's
 // 0x7FC0 on the float side (the conversion keeps a quiet NaN's top bits, and
