@@ -123,7 +123,14 @@ __device__ __forceinline__ uint32_t narrow2_bf16(float a, float b) {
 // keeps +inf; NaN stays v_sqrt's NaN), so sqrt_rn_short drops them: 9 VALU
 // instructions instead of 16. sqrt_rn takes it when no lane of the wavefront
 // holds a tiny, zero or negative x (a wave-uniform branch per value), and
-// std::sqrt otherwise. Checked against torch's sqrt on every float bit pattern.
+// std::sqrt otherwise. +-0 needs no scaling either: v_sqrt returns it, below
+// is a NaN pattern (0xFFFFFFFF / 0x7FFFFFFF, so the first test fails) and the
+// residual with above is a zero (not > 0), so the short path returns +-0 as
+// std::sqrt does. A wavefront whose only small values are zeros (16-bit
+// moments that underflowed, zero gradients) takes it too: a second ballot,
+// only when the first finds a small value. Checked against torch's sqrt on
+// every float bit pattern and on wavefronts mixing zeros, tiny and ordinary
+// values.
 // Measured against std::sqrt at the config-5 shape (same process, 5 rounds,
 // two boxes): Adam with bfloat16 params +2.9-3.6%, Adagrad with half /
 // bfloat16 params +4.4-5% / +3.8-3.9%, Adam with half params -0.6 to +0.5%,
@@ -141,7 +148,7 @@ __device__ __forceinline__ float sqrt_rn_short(float x) {
   return r;
 }
 __device__ __forceinline__ float sqrt_rn(float x) {
-  if (__ballot(!sqrt_short_ok(x)) != 0) {
+  if (__ballot(!sqrt_short_ok(x)) != 0 && __ballot(!sqrt_short_ok(x) && x != 0.0f) != 0) {
     return std::sqrt(x);
   }
   return sqrt_rn_short(x);

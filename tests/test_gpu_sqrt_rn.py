@@ -1,9 +1,10 @@
 """The update kernels' float square root (a short path when no lane of the
-wavefront holds a value below 2^-96, zero or negative; hipcc's full expansion
-otherwise) against torch's sqrt on the GPU, bit for bit (NaN bits included):
-every one of the 2^32 float bit patterns in order (wavefronts of neighbouring
-patterns: the short path for every value it serves), then shuffled values so
-that wavefronts mix tiny and ordinary ones."""
+wavefront holds a nonzero value below 2^-96 or a negative one; hipcc's full
+expansion otherwise) against torch's sqrt on the GPU, bit for bit (NaN bits
+included): every one of the 2^32 float bit patterns in order (wavefronts of
+neighbouring patterns: the short path for every value it serves), then
+shuffled values so that wavefronts mix tiny and ordinary ones, and wavefronts
+whose only small values are zeros of either sign (the short path for them)."""
 
 from __future__ import annotations
 
@@ -62,3 +63,15 @@ def test_sqrt_rn_mixed_wavefronts():
     y = torch.rand(n, generator=gen, device="cuda") + 0.5
     y[::64] = 2.0 ** -100
     _check(y, _sqrt_rn(lib, y))
+    # zeros alone take the short path: one or many per wavefront, either sign,
+    # and beside a tiny value (the full expansion)
+    z = torch.rand(n, generator=gen, device="cuda") + 0.5
+    z[::64] = 0.0
+    z[1::128] = -0.0
+    z[5::256] = 0.0
+    _check(z, _sqrt_rn(lib, z))
+    z[3::512] = 2.0 ** -120
+    _check(z, _sqrt_rn(lib, z))
+    _check(torch.zeros(4096, device="cuda"), _sqrt_rn(lib, torch.zeros(4096, device="cuda")))
+    neg0 = torch.full((4096,), -0.0, device="cuda")
+    _check(neg0, _sqrt_rn(lib, neg0))
