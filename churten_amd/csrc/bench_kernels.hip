@@ -102,9 +102,10 @@ __global__ __launch_bounds__(256) void narrow2_bf16_kernel(const float* in, uint
   if (i < pairs) out[i] = churten::narrow2_bf16(in[2 * i], in[2 * i + 1]);
 }
 
+template <bool ZEROS>
 __global__ __launch_bounds__(256) void sqrt_rn_kernel(const float* in, float* out, int64_t n) {
   const int64_t i = int64_t(blockIdx.x) * 256 + threadIdx.x;
-  if (i < n) out[i] = churten::sqrt_rn(in[i]);
+  if (i < n) out[i] = churten::sqrt_rn<ZEROS>(in[i]);
 }
 
 // b_stride 0: one divisor for every element; 1: one per element.
@@ -152,11 +153,18 @@ extern "C" int cb_narrow2_bf16(const float* in, uint32_t* out, int64_t pairs,
   return static_cast<int>(hipGetLastError());
 }
 
-// out[i] = the float square root the update kernels take of in[i].
-extern "C" int cb_sqrt_rn(const float* in, float* out, int64_t n, hipStream_t stream) {
+// out[i] = the float square root the update kernels take of in[i]; zeros != 0:
+// the form of the float16-state policies (zero-only wavefronts on the short
+// path).
+extern "C" int cb_sqrt_rn(const float* in, float* out, int64_t n, int zeros,
+                          hipStream_t stream) {
   if (n <= 0 || n > int64_t(UINT32_MAX) * 256) return 1;
   const uint32_t blocks = static_cast<uint32_t>((n + 255) / 256);
-  hipLaunchKernelGGL(sqrt_rn_kernel, dim3(blocks), dim3(256), 0, stream, in, out, n);
+  if (zeros) {
+    hipLaunchKernelGGL(sqrt_rn_kernel<true>, dim3(blocks), dim3(256), 0, stream, in, out, n);
+  } else {
+    hipLaunchKernelGGL(sqrt_rn_kernel<false>, dim3(blocks), dim3(256), 0, stream, in, out, n);
+  }
   return static_cast<int>(hipGetLastError());
 }
 

@@ -486,7 +486,8 @@ struct AdamPolicy {
   __device__ static void update(M& p, M g, M (&s)[NS], const Rep& rep, bool maximize) {
     M mx = M(0);
     if constexpr (AMSGRAD) mx = s[2];
-    adam_element<M, ADAMW, AMSGRAD>(p, g, s[0], s[1], mx, rep.h, maximize, rep.c);
+    adam_element<M, ADAMW, AMSGRAD, std::is_same<S, _Float16>::value>(p, g, s[0], s[1], mx,
+                                                                      rep.h, maximize, rep.c);
     if constexpr (AMSGRAD) s[2] = mx;
   }
 };
@@ -633,7 +634,7 @@ struct AdagradPolicy {
 #pragma unroll
     for (int e = 0; e < N; ++e) {
       adagrad_sum<M>(pm[e], gm[e], sm[e], rep.h, maximize);
-      adagrad_finish<M>(pm[e], gm[e], sqrt_rn(sm[e]), rep.h);
+      adagrad_finish<M>(pm[e], gm[e], sqrt_rn<true>(sm[e]), rep.h);
     }
     Words out;
 #pragma unroll
@@ -650,12 +651,12 @@ struct AdagradPolicy {
       if (rep.once) {
         const M s_in = s[0];
         adagrad_sum<M>(p, g, s[0], rep.h, maximize);
-        adagrad_finish<M>(p, g, sqrt_rn(s[0]), rep.h);
+        adagrad_finish<M>(p, g, sqrt_rn<true>(s[0]), rep.h);
         s[0] = fma_half(g, g, s_in);
         return;
       }
     }
-    adagrad_element<M>(p, g, s[0], rep.h, maximize);
+    adagrad_element<M, std::is_same<S, _Float16>::value>(p, g, s[0], rep.h, maximize);
   }
 };
 

@@ -126,11 +126,13 @@ __device__ __forceinline__ uint32_t narrow2_bf16(float a, float b) {
 // std::sqrt otherwise. +-0 needs no scaling either: v_sqrt returns it, below
 // is a NaN pattern (0xFFFFFFFF / 0x7FFFFFFF, so the first test fails) and the
 // residual with above is a zero (not > 0), so the short path returns +-0 as
-// std::sqrt does. A wavefront whose only small values are zeros (16-bit
-// moments that underflowed, zero gradients) takes it too: a second ballot,
-// only when the first finds a small value. Checked against torch's sqrt on
-// every float bit pattern and on wavefronts mixing zeros, tiny and ordinary
-// values.
+// std::sqrt does. With ZEROS (the float16-state policies, whose moments
+// underflow to zero for small gradients) a wavefront whose only small values
+// are zeros takes it too: a second ballot, only when the first finds a small
+// value. Elsewhere the single ballot: the second one's few scalar
+// instructions per value cost the float32 update about 0.4%. Checked against
+// torch's sqrt on every float bit pattern and on wavefronts mixing zeros,
+// tiny and ordinary values, both forms.
 // Measured against std::sqrt at the config-5 shape (same process, 5 rounds,
 // two boxes): Adam with bfloat16 params +2.9-3.6%, Adagrad with half /
 // bfloat16 params +4.4-5% / +3.8-3.9%, Adam with half params -0.6 to +0.5%,
@@ -147,12 +149,24 @@ __device__ __forceinline__ float sqrt_rn_short(float x) {
   r = r_above > 0.0f ? above : r;
   return r;
 }
+template <bool ZEROS = false>
 __device__ __forceinline__ float sqrt_rn(float x) {
-  if (__ballot(!sqrt_short_ok(x)) != 0 && __ballot(!sqrt_short_ok(x) && x != 0.0f) != 0) {
+  if (__ballot(!sqrt_short_ok(x)) != 0) {
+    if constexpr (ZEROS) {
+      // The zero test stays in this rare branch: computed from an opaque
+      // copy, the compiler cannot hoist it into the common path (where it
+      // cost three instructions per value).
+      float y = x;
+      asm volatile("" : "+v"(y));
+      if (__ballot(!sqrt_short_ok(y) && y != 0.0f) == 0) {
+        return sqrt_rn_short(x);
+      }
+    }
     return std::sqrt(x);
   }
   return sqrt_rn_short(x);
 }
+template <bool ZEROS = false>
 __device__ __forceinline__ double sqrt_rn(double x) { return std::sqrt(x); }
 
 // ---------------------------------------------------------------------------
@@ -269,14 +283,14 @@ __device__ __forceinline__ void adam_finish(opmath_t& param, const opmath_t exp_
 }
 
 // One element of ATen's adam_math.
-template <typename opmath_t, bool ADAMW, bool AMSGRAD>
+template <typename opmath_t, bool ADAMW, bool AMSGRAD, bool ZEROS = false>
 __device__ __forceinline__ void adam_element(
     opmath_t& param, opmath_t grad, opmath_t& exp_avg, opmath_t& exp_avg_sq,
     opmath_t& max_exp_avg_sq, const AdamHyper& h, const bool maximize,
     const AdamConsts<opmath_t>& c) {
   const opmath_t v = adam_moments<opmath_t, ADAMW, AMSGRAD>(param, grad, exp_avg, exp_avg_sq,
                                                             max_exp_avg_sq, h, maximize);
-  adam_finish(param, exp_avg, sqrt_rn(v), h, c);
+  adam_finish(param, exp_avg, sqrt_rn<ZEROS>(v), h, c);
 }
 
 // Per-replica bias corrections from the (bumped) step count: computed in double
@@ -370,12 +384,12 @@ __device__ __forceinline__ void adagrad_finish(opmath_t& param, const opmath_t g
                                 h.corrected_lr * double(grad) / (double(root) + h.eps));
 }
 
-template <typename opmath_t>
+template <typename opmath_t, bool ZEROS = false>
 __device__ __forceinline__ void adagrad_element(
     opmath_t& param, opmath_t grad, opmath_t& state_sum, const AdagradHyper& h,
     const bool maximize) {
   adagrad_sum(param, grad, state_sum, h, maximize);
-  adagrad_finish(param, grad, sqrt_rn(state_sum), h);
+  adagrad_finish(param, grad, sqrt_rn<ZEROS>(state_sum), h);
 }
 
 // Float32 Adagrad (this build's explicitly non-ATen variant): the element loop
