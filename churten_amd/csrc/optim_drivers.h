@@ -431,15 +431,20 @@ struct AdamPolicy {
   static constexpr int NS = AMSGRAD ? 3 : 2;
   static constexpr uint32_t kStreamLds = residency_lds<T, S>(AMSGRAD ? 12 : 14);
   static constexpr int kStreamUnroll = stream_unroll<T, S>(2, 4, 1, 2);
-  // float16 Adam (no amsgrad): four 8-element packs under a cap of 12. Two
-  // boxes, 5 processes, config-5 shape: 6.29-6.40 TB/s against 5.89-6.24 for
-  // one uncapped pack, whose rate swung by up to 6% between processes.
+  // float16 Adam (no amsgrad): one 8-element pack under a cap of 20. Three
+  // boxes, config-5 shape: 6.16-6.38 TB/s on synthetic moments and
+  // 6.37 on moments that start at zero and underflow (the bench's data),
+  // against 5.87-6.35 for the uncapped pack, whose rate swung by up to 6%
+  // between processes; four packs under a cap of 12 matched it on synthetic
+  // moments (6.26-6.40) and lost 1.5% on the zeroed ones.
   static constexpr bool kHalfShape = kHalfAll<T, S> && !AMSGRAD;
   static constexpr uint32_t kStreamLdsPre =
-      kBf16State<T, S> || kHalfShape ? lds_for_residency(12) : kStreamLds;
+      kBf16State<T, S> ? lds_for_residency(12)
+      : kHalfShape     ? lds_for_residency(20)
+                       : kStreamLds;
   static constexpr uint32_t kStreamLdsMid =
       kFp32State<T, S> ? lds_for_residency(20) : kStreamLdsPre;
-  static constexpr int kStreamUnrollPre = kHalfShape ? 4 : stream_unroll<T, S>(1, 2, 1, 2);
+  static constexpr int kStreamUnrollPre = stream_unroll<T, S>(1, 2, 1, 2);
   static constexpr int kStreamUnrollSmall = stream_unroll<T, S>(2, 4, 4, 2);
   static constexpr int64_t kStreamSmallBytes = kMallBytes;
   static constexpr int kStreamPack = stream_pack<T, S>();
