@@ -421,6 +421,10 @@ constexpr int stream_unroll(int fp32, int bf16_state, int narrow, int wide) {
 //   Adagrad, 16-bit      4 packs of 8, uncapped: half 6.14-6.18, bfloat16 6.07
 //   parameters           (1 pack: half 5.65-5.88, bfloat16 5.75)
 // Adam and SGD with 16-bit parameters stayed within 2% of one pack, uncapped.
+// Rechecked once more after the zero-aware square root (up to three boxes,
+// each shape in 2-3 processes): float16 Adam moved to one pack under a cap
+// of 20 and bfloat16 SGD to two packs under a cap of 20 (at the policies);
+// float16 SGD and 16-bit Adagrad kept their shapes.
 
 // Adam / AdamW: h = {lr, beta1, beta2, eps, weight_decay}.
 template <typename T_, bool ADAMW, bool AMSGRAD, typename S_ = T_>
