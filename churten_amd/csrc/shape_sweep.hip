@@ -77,6 +77,8 @@ struct SegmentShape : Base {
 template <typename Base>
 struct PerElementStdSqrt : Base {
   using M = typename Base::M;
+  // every pack through update() below (not float16 Adagrad's pair form)
+  static constexpr bool kVariant = false;
   __device__ static void update(M& p, M g, M (&s)[Base::NS], const typename Base::Rep& rep,
                                 bool maximize) {
     if constexpr (Base::NS >= 2) {  // Adam
