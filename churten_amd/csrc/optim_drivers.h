@@ -742,10 +742,26 @@ constexpr uint32_t stream_lds_of() {
   return SMALL ? 0u : PRE ? P::kStreamLdsPre : P::kStreamLds;
 }
 
-// Elements per streaming tile: one wavefront x the policy's packs per thread.
+// Threads per streaming workgroup: one wavefront, or a policy's kStreamBlock
+// for its launches beyond the MALL.
+template <typename P, typename = void>
+struct stream_block_of {
+  static constexpr int value = kStreamThreads;
+};
+template <typename P>
+struct stream_block_of<P, std::void_t<decltype(P::kStreamBlock)>> {
+  static constexpr int value = P::kStreamBlock;
+};
+template <typename P, bool SMALL>
+constexpr int stream_threads() {
+  return SMALL ? kStreamThreads : stream_block_of<P>::value;
+}
+
+// Elements per streaming tile: the workgroup's threads x the policy's packs
+// per thread.
 template <typename P, bool PRE, bool SMALL>
 constexpr int64_t stream_tile() {
-  return int64_t(kStreamThreads) * P::kStreamPack * stream_unroll_of<P, PRE, SMALL>();
+  return int64_t(stream_threads<P, SMALL>()) * P::kStreamPack * stream_unroll_of<P, PRE, SMALL>();
 }
 
 // Bytes of (R, T) operands a launch reads (all rows): params and grads in
@@ -928,7 +944,8 @@ __device__ __forceinline__ void with_maximize(bool maximize, F&& f) {
 // SMALL: the launch's operands fit the MALL; plain accesses and the small-launch
 // tile instead of non-temporal ones.
 template <typename P, bool ANY, bool PRE, bool SMALL>
-__global__ __launch_bounds__(kStreamThreads) void stream_kernel(KArgs<P> a) {
+__global__ __launch_bounds__((stream_threads<P, SMALL>())) void stream_kernel(KArgs<P> a) {
+  constexpr int NTH = stream_threads<P, SMALL>();  // threads per workgroup
   using T = typename P::T;
   using S = typename P::S;
   constexpr int NS = P::NS;
@@ -969,7 +986,7 @@ __global__ __launch_bounds__(kStreamThreads) void stream_kernel(KArgs<P> a) {
   Pack<S, KP> vs[SS][U];
 #pragma unroll
   for (int u = 0; u < U; ++u) {
-    const int64_t i = int64_t(u) * kStreamThreads + threadIdx.x;
+    const int64_t i = int64_t(u) * NTH + threadIdx.x;
     if (i < packs_left) {
       vp[u] = load_stream<NT>(prow + i);
       vg[u] = grow.load(i);
@@ -994,7 +1011,7 @@ __global__ __launch_bounds__(kStreamThreads) void stream_kernel(KArgs<P> a) {
                            __attribute__((always_inline)) {
 #pragma unroll
     for (int u = 0; u < U; ++u) {
-      const int64_t i = int64_t(u) * kStreamThreads + threadIdx.x;
+      const int64_t i = int64_t(u) * NTH + threadIdx.x;
       if (i < packs_left) {
         Pack<S, KP> st[SS];
 #pragma unroll
@@ -1022,7 +1039,7 @@ __global__ __launch_bounds__(kStreamThreads) void stream_kernel(KArgs<P> a) {
   if constexpr (P::kLateStores) {
 #pragma unroll
     for (int u = 0; u < U; ++u) {
-      const int64_t i = int64_t(u) * kStreamThreads + threadIdx.x;
+      const int64_t i = int64_t(u) * NTH + threadIdx.x;
       if (i < packs_left) store_packs(u, i);
     }
   }
@@ -1042,10 +1059,10 @@ __global__ __launch_bounds__(kStreamThreads) void stream_kernel(KArgs<P> a) {
     for (int b = 0; b < NS; ++b) sbase[b][j] = st[b];
   };
   if (t0 == 0) {
-    for (int64_t j = threadIdx.x; j < head; j += kStreamThreads) one(j);
+    for (int64_t j = threadIdx.x; j < head; j += NTH) one(j);
   }
   if (t0 + kStreamTile >= width) {
-    for (int64_t j = head + packs_row * KP + threadIdx.x; j < width; j += kStreamThreads) one(j);
+    for (int64_t j = head + packs_row * KP + threadIdx.x; j < width; j += NTH) one(j);
   }
 }
 
@@ -1937,11 +1954,11 @@ void launch_stream(const KArgs<P>& a, uint32_t blocks, bool same_phase, hipStrea
   const uint32_t cap = PRE && !SMALL && mid ? P::kStreamLdsMid : stream_lds_of<P, PRE, SMALL>();
   const uint32_t lds = int64_t(blocks) * stream_tile<P, PRE, SMALL>() >= kCapMinElems ? cap : 0u;
   if (same_phase) {
-    hipLaunchKernelGGL((stream_kernel<P, false, PRE, SMALL>), dim3(blocks), dim3(kStreamThreads),
-                       lds, stream, a);
+    hipLaunchKernelGGL((stream_kernel<P, false, PRE, SMALL>), dim3(blocks),
+                       dim3(stream_threads<P, SMALL>()), lds, stream, a);
   } else {
-    hipLaunchKernelGGL((stream_kernel<P, true, PRE, SMALL>), dim3(blocks), dim3(kStreamThreads),
-                       lds, stream, a);
+    hipLaunchKernelGGL((stream_kernel<P, true, PRE, SMALL>), dim3(blocks),
+                       dim3(stream_threads<P, SMALL>()), lds, stream, a);
   }
 }
 

@@ -53,8 +53,9 @@ namespace {
 
 // A policy with its streaming shape replaced (with and without a workspace,
 // and for launches that fit the MALL, which run uncapped whatever CAP says).
-template <typename Base, int U, int CAP>
+template <typename Base, int U, int CAP, int NTH = 64>
 struct StreamShape : Base {
+  static constexpr int kStreamBlock = NTH;
   static constexpr int kStreamUnrollPre = U;
   static constexpr int kStreamUnroll = U;
   static constexpr int kStreamUnrollSmall = U;
