@@ -122,9 +122,12 @@ void check_vec(const at::Tensor& params, const at::Tensor& t, const char* op,
               " must be on ", params.device(), ", got ", t.device());
 }
 
-// The (R,) hyperparameters, in the param dtype and contiguous; a no-op in the
-// normal case.
+// The (R,) hyperparameters, in the param dtype and contiguous. The normal case,
+// already such a vector, returns it without a dispatcher call (reshape, to and
+// contiguous would each return it unchanged; at microsecond steps the host's
+// per-call cost sets the step time).
 at::Tensor hyper(const at::Tensor& t, at::ScalarType dtype) {
+  if (t.dim() == 1 && t.scalar_type() == dtype && t.is_contiguous()) return t;
   return t.reshape({t.numel()}).to(dtype).contiguous();
 }
 
@@ -174,7 +177,9 @@ Prepared prepare(const at::Tensor& params, at::Tensor& state_steps,
   p.flags = flags;
   if (state_steps.scalar_type() == dtype && state_steps.is_contiguous() &&
       active_mask.scalar_type() == at::kBool) {
-    p.mask = active_mask.reshape({active_mask.numel()}).contiguous();
+    p.mask = active_mask.dim() == 1 && active_mask.is_contiguous()
+                 ? active_mask
+                 : active_mask.reshape({active_mask.numel()}).contiguous();
     p.steps = state_steps;
     p.flags |= TS_BUMP_STEPS;
   } else {
