@@ -525,6 +525,10 @@ struct SgdPolicy {
   static constexpr uint32_t kStreamLdsMid = kStreamLdsPre;
   static constexpr int kStreamUnrollPre = kStreamUnroll;
   static constexpr int kStreamUnrollSmall = stream_unroll<T, S>(1, 1, 4, 2);
+  // float32 launches that fit the MALL: two-wavefront workgroups. Config 3's
+  // shape (32 x 545100, 80% active), two calls, 2-3 processes: 6.87-6.91
+  // TB/s against 6.77-6.79 for one wavefront (256 threads: 6.88-6.93).
+  static constexpr int kStreamBlockSmall = kFp32State<T, S> ? 128 : kStreamThreads;
   static constexpr int64_t kStreamSmallBytes = kMallBytes;
   static constexpr int kStreamPack = stream_pack<T, S>();
   static constexpr int kSegmentUnroll = 2;
@@ -743,7 +747,7 @@ constexpr uint32_t stream_lds_of() {
 }
 
 // Threads per streaming workgroup: one wavefront, or a policy's kStreamBlock
-// for its launches beyond the MALL.
+// for its launches beyond the MALL and kStreamBlockSmall for the others.
 template <typename P, typename = void>
 struct stream_block_of {
   static constexpr int value = kStreamThreads;
@@ -752,9 +756,17 @@ template <typename P>
 struct stream_block_of<P, std::void_t<decltype(P::kStreamBlock)>> {
   static constexpr int value = P::kStreamBlock;
 };
+template <typename P, typename = void>
+struct stream_block_small_of {
+  static constexpr int value = kStreamThreads;
+};
+template <typename P>
+struct stream_block_small_of<P, std::void_t<decltype(P::kStreamBlockSmall)>> {
+  static constexpr int value = P::kStreamBlockSmall;
+};
 template <typename P, bool SMALL>
 constexpr int stream_threads() {
-  return SMALL ? kStreamThreads : stream_block_of<P>::value;
+  return SMALL ? stream_block_small_of<P>::value : stream_block_of<P>::value;
 }
 
 // Elements per streaming tile: the workgroup's threads x the policy's packs

@@ -56,6 +56,7 @@ namespace {
 template <typename Base, int U, int CAP, int NTH = 64>
 struct StreamShape : Base {
   static constexpr int kStreamBlock = NTH;
+  static constexpr int kStreamBlockSmall = NTH;
   static constexpr int kStreamUnrollPre = U;
   static constexpr int kStreamUnroll = U;
   static constexpr int kStreamUnrollSmall = U;
