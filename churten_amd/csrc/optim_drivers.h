@@ -576,7 +576,9 @@ struct AdagradPolicy {
   static constexpr uint32_t kStreamLds = residency_lds<T, S>(16);
   static constexpr int kStreamUnroll = stream_unroll<T, S>(2, 1, 1, 2);
   static constexpr uint32_t kStreamLdsPre = residency_lds<T, S>(20);
-  static constexpr uint32_t kStreamLdsMid = kStreamLdsPre;
+  // Mid-size launches (config 4's 419 MB): cap 24, 6.37-6.39 TB/s against
+  // 6.28-6.30 at 20 (four processes, two calls).
+  static constexpr uint32_t kStreamLdsMid = residency_lds<T, S>(24);
   static constexpr int kStreamUnrollPre = stream_unroll<T, S>(1, 1, 4, 2);
   static constexpr int kStreamUnrollSmall = stream_unroll<T, S>(2, 1, 4, 2);
   static constexpr int64_t kStreamSmallBytes = kMallBytes;
