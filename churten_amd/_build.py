@@ -17,6 +17,7 @@ from __future__ import annotations
 
 import os
 import shutil
+from concurrent.futures import ThreadPoolExecutor
 import subprocess
 import sys
 import sysconfig
@@ -43,7 +44,6 @@ HIPCC_FLAGS = [
     "-O3",
     "-std=c++17",
     "-fPIC",
-    "-shared",
     "-Wall",
     "-Xclang",
     "-target-feature",
@@ -76,16 +76,50 @@ def _run(cmd: list[str], verbose: bool) -> None:
         print("\n".join(noisy), flush=True)
 
 
-def build_library(verbose: bool = False) -> Path:
+# The library's translation units: the optimizers' entry points (Adam's
+# dense and segmented ones apart), so that each compiles only its own
+# policies and drivers and they compile in parallel; the shared entry points;
+# the row copies.
+LIB_SOURCES = ("abi_adam.hip", "abi_adam_segments.hip", "abi_sgd.hip", "abi_adagrad.hip",
+               "optim_kernels.hip", "rows.hip")
+OBJ_DIR = PKG / "_objs"
+
+
+def _parallel(jobs: list, workers: int | None = None) -> None:
+    """Runs the zero-argument callables in ``jobs`` concurrently (each one
+    drives a compiler process) and re-raises the first failure."""
+    if not jobs:
+        return
+    n = workers or min(len(jobs), max(1, min(8, os.cpu_count() or 1)))
+    with ThreadPoolExecutor(max_workers=n) as pool:
+        for fut in [pool.submit(j) for j in jobs]:
+            fut.result()
+
+
+def _library_objects(verbose: bool) -> tuple:
+    OBJ_DIR.mkdir(exist_ok=True)
+    objs, jobs = [], []
+    for src in LIB_SOURCES:
+        obj = OBJ_DIR / (Path(src).stem + ".hip.o")
+        objs.append(obj)
+        cmd = [_hipcc(), *HIPCC_FLAGS, "-c", str(CSRC / src), "-o", str(obj)]
+        jobs.append(lambda cmd=cmd: _run(cmd, verbose))
+    return objs, jobs
+
+
+def _link_library(objs: list, verbose: bool) -> Path:
     LIB_DIR.mkdir(parents=True, exist_ok=True)
     tmp = LIB.with_suffix(".so.tmp")
-    _run(
-        [_hipcc(), *HIPCC_FLAGS, str(CSRC / "optim_kernels.hip"), str(CSRC / "rows.hip"),
-         "-o", str(tmp)],
-        verbose,
-    )
+    _run([_hipcc(), f"--offload-arch={ARCH}", "-shared", *map(str, objs), "-o", str(tmp)],
+         verbose)
     os.replace(tmp, LIB)
     return LIB
+
+
+def build_library(verbose: bool = False) -> Path:
+    objs, jobs = _library_objects(verbose)
+    _parallel(jobs)
+    return _link_library(objs, verbose)
 
 
 # The CPU kernels state every fused multiply-add explicitly (std::fma) and
@@ -94,13 +128,10 @@ def build_library(verbose: bool = False) -> Path:
 CPU_KERNEL_FLAGS = ["-O3", "-mavx2", "-mfma", "-ffp-contract=off", "-fno-math-errno"]
 
 
-def build_extension(verbose: bool = False, sanitize: bool = False) -> Path:
-    """``sanitize``: host code with AddressSanitizer and UBSan (load it with
-    their runtimes preloaded; for the CPU tests)."""
+def _extension_objects(verbose: bool, sanitize: bool = False):
     import torch
     from torch.utils import cpp_extension
 
-    torch_lib = Path(torch.__file__).resolve().parent / "lib"
     incs = [*cpp_extension.include_paths(), sysconfig.get_paths()["include"], "/opt/rocm/include"]
     abi = int(torch._C._GLIBCXX_USE_CXX11_ABI)
     common = [
@@ -115,22 +146,32 @@ def build_extension(verbose: bool = False, sanitize: bool = False) -> Path:
         "-DTORCH_EXTENSION_NAME=_C",
         *[f"-isystem{p}" for p in incs],
     ]
-    san = ["-fsanitize=address,undefined", "-fno-omit-frame-pointer", "-g"] if sanitize else []
-    common[1:1] = san
-    build_dir = PKG / "_objs"
-    build_dir.mkdir(exist_ok=True)
-    objs = []
+    common[1:1] = _sanitize_flags(sanitize)
+    OBJ_DIR.mkdir(exist_ok=True)
+    objs, jobs = [], []
     for src, flags in (("torch_ops.cpp", ["-O2"]), ("cpu_kernels.cpp", CPU_KERNEL_FLAGS)):
-        obj = build_dir / (Path(src).stem + ".o")
-        _run([*common, *flags, "-c", str(CSRC / src), "-o", str(obj)], verbose)
-        objs.append(str(obj))
+        obj = OBJ_DIR / (Path(src).stem + ".o")
+        objs.append(obj)
+        cmd = [*common, *flags, "-c", str(CSRC / src), "-o", str(obj)]
+        jobs.append(lambda cmd=cmd: _run(cmd, verbose))
+    return objs, jobs
+
+
+def _sanitize_flags(sanitize: bool) -> list:
+    return ["-fsanitize=address,undefined", "-fno-omit-frame-pointer", "-g"] if sanitize else []
+
+
+def _link_extension(objs: list, verbose: bool, sanitize: bool = False) -> Path:
+    import torch
+
+    torch_lib = Path(torch.__file__).resolve().parent / "lib"
     tmp = EXT.with_suffix(".so.tmp")
     _run(
         [
             "g++",
-            *san,
+            *_sanitize_flags(sanitize),
             "-shared",
-            *objs,
+            *map(str, objs),
             "-o",
             str(tmp),
             f"-L{LIB_DIR}",
@@ -149,19 +190,33 @@ def build_extension(verbose: bool = False, sanitize: bool = False) -> Path:
     return EXT
 
 
+def build_extension(verbose: bool = False, sanitize: bool = False) -> Path:
+    """``sanitize``: host code with AddressSanitizer and UBSan (load it with
+    their runtimes preloaded; for the CPU tests). Links against the library
+    already built."""
+    objs, jobs = _extension_objects(verbose, sanitize)
+    _parallel(jobs)
+    return _link_extension(objs, verbose, sanitize)
+
+
 def build_bench_library(verbose: bool = False) -> Path:
     """The measurement aid bench.py loads (bench_kernels.hip); not the product ABI."""
     LIB_DIR.mkdir(parents=True, exist_ok=True)
     tmp = BENCH_LIB.with_suffix(".so.tmp")
-    _run([_hipcc(), *HIPCC_FLAGS, str(CSRC / "bench_kernels.hip"), "-o", str(tmp)], verbose)
+    _run([_hipcc(), *HIPCC_FLAGS, "-shared", str(CSRC / "bench_kernels.hip"), "-o", str(tmp)],
+         verbose)
     os.replace(tmp, BENCH_LIB)
     return BENCH_LIB
 
 
 def build(verbose: bool = False) -> None:
-    build_library(verbose)
-    build_bench_library(verbose)
-    build_extension(verbose)
+    """Every compile runs concurrently; the library is linked once its objects
+    are there, the operator extension after it (it links against it)."""
+    lib_objs, lib_jobs = _library_objects(verbose)
+    ext_objs, ext_jobs = _extension_objects(verbose)
+    _parallel([*lib_jobs, lambda: build_bench_library(verbose), *ext_jobs])
+    _link_library(lib_objs, verbose)
+    _link_extension(ext_objs, verbose)
 
 
 if __name__ == "__main__":

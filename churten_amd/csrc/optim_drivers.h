@@ -58,7 +58,7 @@
 // Everything is enqueued on the caller's stream; nothing is allocated.
 
 // This header holds the policies, the drivers and their host-side launchers;
-// optim_kernels.hip dispatches the C ABI of include/churten_optim.h onto them.
+// optim_dispatch.h dispatches the C ABI of include/churten_optim.h onto them.
 // Everything is in an anonymous namespace: a translation unit that includes it
 // gets its own kernels.
 #pragma once
@@ -1729,7 +1729,7 @@ bool col_lines_private(const Operands<typename P::T>& x, int n, const ColGrid& g
   return true;
 }
 
-bool make_grid(int64_t R, int64_t T, int64_t tile, Grid& g, uint32_t& blocks) {
+inline bool make_grid(int64_t R, int64_t T, int64_t tile, Grid& g, uint32_t& blocks) {
   const int64_t tiles = (T + tile - 1) / tile;
   if (R <= 0 || T <= 0 || tiles > INT32_MAX || R > INT32_MAX / tiles) {
     return false;
@@ -1758,7 +1758,7 @@ int launch_bump(void* steps, const uint8_t* mask, int64_t R, void* out_zero,
 // A caller's segment table: in column order, disjoint, inside [0, cols), with
 // data for every non-empty segment (two tiles writing one column would race).
 // One pass, no allocation.
-bool segments_valid(const ts_segment* segs, int n, int64_t cols) {
+inline bool segments_valid(const ts_segment* segs, int n, int64_t cols) {
   int64_t end = 0;
   for (int i = 0; i < n; ++i) {
     const ts_segment& s = segs[i];
@@ -2085,9 +2085,9 @@ int launch_segments(const Call& c, int nbufs, const ts_segment* segs, int n_segs
   });
 }
 
-Call make_call(const ts_rt_buf* bufs, void* steps, std::initializer_list<const void*> h,
-               const uint8_t* mask, int64_t R, int64_t T, uint32_t flags, void* out_zero,
-               void* stream, void* ws = nullptr, size_t ws_bytes = 0) {
+inline Call make_call(const ts_rt_buf* bufs, void* steps, std::initializer_list<const void*> h,
+                      const uint8_t* mask, int64_t R, int64_t T, uint32_t flags,
+                      void* out_zero, void* stream, void* ws = nullptr, size_t ws_bytes = 0) {
   Call c;
   c.ws = ws;
   c.ws_bytes = ws_bytes;
