@@ -593,9 +593,11 @@ def ceiling_timing(adam_args, launches: int):
         (k, cap), r = max(rates.items(), key=lambda kv: kv[1])
         return r, f"{k} pack{'s' if k > 1 else ''}, " + (f"cap {cap}" if cap else "uncapped"), rates
 
-    mix, mix_shape, mix_rates = best(0, 0.0, [(1, 8), (1, 10), (1, 12), (1, 14), (2, 10)], 28)
-    reads, read_shape, _ = best(1, -3.0e38, [(1, 0), (2, 0), (2, 14)], 16)
-    writes, write_shape, _ = best(2, 0.0, [(1, 8), (1, 10), (1, 12), (2, 8)], 12)
+    mix, mix_shape, mix_rates = best(
+        0, 0.0, [(1, 4), (1, 6), (1, 8), (1, 10), (1, 12), (1, 14), (2, 3), (2, 4), (2, 10)], 28)
+    reads, read_shape, _ = best(1, -3.0e38, [(1, 0), (1, 6), (1, 10), (2, 0), (2, 14)], 16)
+    writes, write_shape, _ = best(
+        2, 0.0, [(1, 4), (1, 6), (1, 8), (1, 10), (1, 12), (2, 4), (2, 8)], 12)
     out = {"mix_4r3w_GBs": mix, "mix_4r3w_shape": mix_shape,
            "mix_4r3w_update_shape_GBs": mix_rates[(1, 14)],
            "read_4_GBs": reads, "read_4_shape": read_shape,

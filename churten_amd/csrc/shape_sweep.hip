@@ -7,7 +7,7 @@
 // constants of the policies in optim_drivers.h were chosen from.
 //
 // Streaming families vary packs per thread (1, 2, 4) and the residency cap
-// (none, 10-20 one-wave workgroups per CU); the segmented family varies
+// (none, 3-20 one-wave workgroups per CU); the segmented family varies
 // threads per workgroup (64, 128), packs (1, 2) and the cap, next to the dense
 // update on the same state. Every variant is timed in each of several
 // interleaved rounds (2 untimed launches, then 15 timed between two events);
@@ -251,7 +251,7 @@ template <typename Base, int NS>
 void stream_family(int nh, int bytes_per_elem) {
   State<typename Base::T, typename Base::S, NS> st;
   std::vector<Variant> v;
-  using caps = std::integer_sequence<int, 0, 10, 12, 14, 16, 20>;
+  using caps = std::integer_sequence<int, 0, 3, 4, 6, 8, 10, 12, 14, 16, 20>;
   add_stream<Base, decltype(st), 1>(v, st, nh, caps{});
   add_stream<Base, decltype(st), 2>(v, st, nh, caps{});
   add_stream<Base, decltype(st), 4>(v, st, nh, caps{});
