@@ -1,6 +1,7 @@
-// abi_adagrad.hip -- the Adagrad entry points of include/churten_optim.h:
-// the dispatch of each call onto AdagradPolicy (ATen's double math) or, under
-// TS_ADAGRAD_F32, AdagradF32Policy.
+// abi_adagrad.hip -- the Adagrad entry points of include/churten_optim.h,
+// dense and segmented, with and without a workspace (adagrad_run in
+// optim_dispatch.h picks AdagradPolicy, ATen's double math, or under
+// TS_ADAGRAD_F32 AdagradF32Policy).
 
 #include <hip/hip_runtime.h>
 

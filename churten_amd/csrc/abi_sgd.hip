@@ -1,6 +1,6 @@
-// abi_sgd.hip -- the SGD entry points of include/churten_optim.h: the
-// dispatch of each call onto the SgdPolicy its flags, dtype and momentum
-// buffers select.
+// abi_sgd.hip -- the SGD entry points of include/churten_optim.h, dense and
+// segmented (sgd_run in optim_dispatch.h picks the SgdPolicy from the call's
+// dtype, flags and momentum buffers).
 
 #include <hip/hip_runtime.h>
 
