@@ -1254,7 +1254,9 @@ __device__ __forceinline__ void column_walk(const ColArgs<P>& a, int64_t r, int6
 // Storing after all four unrolled columns' arithmetic (the streaming driver's
 // late stores) moved the column driver by -3% (non-temporal) to +2% (plain):
 // not adopted.
-template <typename P, bool NT>
+// PRE: every thread reads its replica's constants from the call's workspace
+// (filled by the preparation launch) instead of deriving them.
+template <typename P, bool NT, bool PRE>
 __global__ __launch_bounds__(kColThreads) void column_kernel(ColArgs<P> a) {
   uint32_t blk = blockIdx.x;
   if (a.g.n_rblocks > 1) {
@@ -1287,7 +1289,7 @@ __global__ __launch_bounds__(kColThreads) void column_kernel(ColArgs<P> a) {
     return;
   }
   typename P::Rep rep;
-  P::template prologue<false>(a.vec, static_cast<uint32_t>(r), rep);
+  P::template prologue<PRE>(a.vec, static_cast<uint32_t>(r), rep);
   const bool load_state = P::reads_state(a.vec, static_cast<uint32_t>(r));
   const int64_t t_first = int64_t(cblk) * a.g.cpi * kColIters + cc;
   if (nt) {
@@ -1960,6 +1962,20 @@ int run_step(const Call& c, const Vectors<typename P::T>& vec, Prepare&& prepare
   return launch();
 }
 
+// The column driver over `blocks` workgroups: non-temporal when no cache line
+// is shared between workgroups; PRE with the call's workspace.
+template <typename P, bool PRE>
+void launch_column(const ColArgs<P>& ca, uint32_t blocks, bool private_lines,
+                   hipStream_t stream) {
+  if (private_lines) {
+    hipLaunchKernelGGL((column_kernel<P, true, PRE>), dim3(blocks), dim3(ca.g.threads), 0, stream,
+                       ca);
+  } else {
+    hipLaunchKernelGGL((column_kernel<P, false, PRE>), dim3(blocks), dim3(ca.g.threads), 0,
+                       stream, ca);
+  }
+}
+
 // The streaming driver over `blocks` tiles, capped when the launch is large
 // (`mid`: the operands take at most kMidBytes; with a workspace only).
 template <typename P, bool PRE, bool SMALL>
@@ -2031,13 +2047,14 @@ int launch_dense(const Call& c, int nbufs) {
       ca.x = a.x;
       ca.vec = a.vec;
       ca.maximize = a.maximize;
-      if (col_lines_private<P>(a.x, nbufs, ca.g)) {
-        hipLaunchKernelGGL((column_kernel<P, true>), dim3(col_blocks), dim3(ca.g.threads), 0,
-                           c.stream, ca);
-      } else {
-        hipLaunchKernelGGL((column_kernel<P, false>), dim3(col_blocks), dim3(ca.g.threads), 0,
-                           c.stream, ca);
+      const bool private_lines = col_lines_private<P>(a.x, nbufs, ca.g);
+      if constexpr (P::kPreWords > 0) {
+        if (pre) {
+          launch_column<P, true>(ca, col_blocks, private_lines, c.stream);
+          return static_cast<int>(hipGetLastError());
+        }
       }
+      launch_column<P, false>(ca, col_blocks, private_lines, c.stream);
     } else {
       hipLaunchKernelGGL(element_kernel<P>, grid, block, 0, c.stream, a);
     }
