@@ -452,6 +452,39 @@ def test_replica_minor_access_paths(R, pad, frozen):
         assert torch.equal(x[~mask], before[i][~mask]), i
 
 
+@pytest.mark.parametrize("amsgrad", [False, True])
+def test_replica_minor_step0_freeze_with_workspace(amsgrad):
+    """Replicas frozen before their first step keep step 0, so the per-replica
+    constants the operator's preparation launch writes for them divide by
+    1 - beta^0 = 0. The column driver's threads for a frozen replica exit
+    before reading those constants or any operand: with NaN in the frozen
+    replicas' state, their columns stay bit-identical and the active replicas
+    get the bits of contiguous buffers."""
+    R, T = 70, 45
+    a = adam_args(R, T, amsgrad, seed=11, steps=0.0)
+    mask = torch.ones(R, dtype=torch.bool, device=DEV)
+    mask[[0, 33, 69]] = False
+    for t in a[2:5]:
+        if t is not None:
+            t[~mask] = float("nan")
+    ops = [t for t in a[:5] if t is not None]
+    view = [_replica_minor(t, 0) for t in ops]
+    dense = [t.clone() for t in ops]
+    before = [t.clone() for t in ops]
+    s_view, s_dense = a[5].clone(), a[5].clone()
+    kw = dict(amsgrad=amsgrad, maximize=False, decoupled_weight_decay=False)
+    mx = lambda b: b[4] if amsgrad else None  # noqa: E731
+    for _ in range(2):
+        K.adam_step_(*view[:4], mx(view), s_view, *a[6:], mask, **kw)
+        K.adam_step_(*dense[:4], mx(dense), s_dense, *a[6:], mask, **kw)
+    torch.cuda.synchronize()
+    assert torch.equal(s_view, s_dense)
+    assert s_view[~mask].eq(0).all() and s_view[mask].eq(2).all()
+    for i, (x, y) in enumerate(zip(view, dense)):
+        assert torch.equal(x.view(torch.int32), y.view(torch.int32)), i
+        assert torch.equal(x[~mask].view(torch.int32), before[i][~mask].view(torch.int32)), i
+
+
 def test_noncontiguous_and_foreign_dtype_side_inputs():
     """(R,) inputs may be strided or float64 and steps float64, mask float:
     normalised like the reference (to the param dtype / bool)."""
