@@ -1080,7 +1080,9 @@ __global__ __launch_bounds__((stream_threads<P, SMALL>())) void stream_kernel(KA
   }
 }
 
-template <typename P>
+// Any strides: kPer elements per thread, one element per access. PRE: the
+// replica's constants come from the call's workspace.
+template <typename P, bool PRE>
 __global__ __launch_bounds__(kThreads) void element_kernel(KArgs<P> a) {
   using T = typename P::T;
   using S = typename P::S;
@@ -1093,7 +1095,7 @@ __global__ __launch_bounds__(kThreads) void element_kernel(KArgs<P> a) {
     return;
   }
   typename P::Rep rep;
-  P::template prologue<false>(a.vec, r, rep);
+  P::template prologue<PRE>(a.vec, r, rep);
   const bool load_state = P::reads_state(a.vec, r);
 
   T* const prow = pg_row<P>(a.x, 0, r);
@@ -2056,7 +2058,13 @@ int launch_dense(const Call& c, int nbufs) {
       }
       launch_column<P, false>(ca, col_blocks, private_lines, c.stream);
     } else {
-      hipLaunchKernelGGL(element_kernel<P>, grid, block, 0, c.stream, a);
+      if constexpr (P::kPreWords > 0) {
+        if (pre) {
+          hipLaunchKernelGGL((element_kernel<P, true>), grid, block, 0, c.stream, a);
+          return static_cast<int>(hipGetLastError());
+        }
+      }
+      hipLaunchKernelGGL((element_kernel<P, false>), grid, block, 0, c.stream, a);
     }
     return static_cast<int>(hipGetLastError());
   });
