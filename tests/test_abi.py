@@ -289,3 +289,27 @@ def test_ops_trace_under_torch_compile(device):
         assert torch.equal(a, b)
     for x, y in zip(eager, comp):
         assert torch.equal(x, y)
+
+
+def test_build_compiles_every_library_source_and_reports_a_failed_job():
+    """build() compiles each translation unit of the library as its own job
+    (they run concurrently) and links them once all have finished; a job that
+    fails raises from the pool instead of being lost in a worker thread."""
+    from churten_amd import _build
+
+    csrc = Path(_build.CSRC)
+    assert {p.name for p in csrc.glob("abi_*.hip")} <= set(_build.LIB_SOURCES)
+    assert {"optim_kernels.hip", "rows.hip"} <= set(_build.LIB_SOURCES)
+    objs, jobs = _build._library_objects(verbose=False)
+    assert len(objs) == len(jobs) == len(_build.LIB_SOURCES)
+    ran = []
+
+    def ok():
+        ran.append(1)
+
+    def fail():
+        raise RuntimeError("build step failed (1): hipcc")
+
+    with pytest.raises(RuntimeError, match="build step failed"):
+        _build._parallel([ok, fail, ok])
+    assert len(ran) == 2
