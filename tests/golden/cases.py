@@ -97,6 +97,27 @@ def all_cases():
     return adam_cases() + sgd_cases() + adagrad_cases()
 
 
+def dtype_cases():
+    """Cases replayed in float64, float16 and bfloat16: each optimizer's whole
+    flag matrix at T = 45 (ragged) and T = 1000, plus every special case (the
+    16397-element rows that cross the CPU chunk, late steps, per-replica
+    momentum with a momentum-0 replica inside a buffered call, first steps)."""
+    return [c for c in all_cases() if c["T"] not in (52, 64)]
+
+
+def digest_bytes(a) -> str:
+    """SHA-256 of an array's raw bytes in its own dtype (numpy array, or a torch
+    tensor of any dtype, bfloat16 included), tagged with the dtype name."""
+    if hasattr(a, "numpy"):
+        import torch
+
+        tag = str(a.dtype).replace("torch.", "")
+        raw = a.detach().contiguous().reshape(-1).view(torch.uint8).numpy().tobytes()
+    else:
+        tag, raw = str(a.dtype), np.ascontiguousarray(a).tobytes()
+    return tag + ":" + hashlib.sha256(raw).hexdigest()
+
+
 def case_id(c) -> str:
     keys = [k for k in c if k not in ("op",)]
     return c["op"] + "-" + "-".join(f"{k}={c[k]}" for k in keys)

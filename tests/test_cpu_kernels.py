@@ -44,6 +44,35 @@ def test_cpu_key_is_registered_and_gpu_key_is_separate():
         assert torch._C._dispatch_has_kernel_for_dispatch_key(name, "CUDA")
 
 
+DTYPE_RECORDS = json.loads((GOLDEN.parent / "cpu_ref_dtypes.json").read_text())["records"]
+
+
+@pytest.mark.parametrize(
+    "rec", DTYPE_RECORDS,
+    ids=lambda r: r["dtype"] + "-" + C.case_id(r["case"]) + ("-strided" if r["strided"] else ""))
+def test_cpu_key_other_dtypes_bit_exact_to_reference_cpu_kernel(rec):
+    """float64 (the reference's vector body when contiguous, its scalar loop when
+    strided), float16 and bfloat16 (its float-accumulating scalar loop): every
+    output, steps included, equals the reference CPU build's bit for bit."""
+    dt = {"float64": torch.float64, "float16": torch.float16,
+          "bfloat16": torch.bfloat16}[rec["dtype"]]
+    out = run_ref(rec["case"], strided=rec["strided"], dtype=dt)
+    bad = [k for k, want in rec["digest"].items() if C.digest_bytes(out[k]) != want]
+    assert not bad, f"{bad} differ from the reference CPU kernel in {rec['dtype']}"
+
+
+def test_dtype_records_cover_the_matrix():
+    """The dtype fixtures hold every optimizer's flag matrix, the frozen row,
+    a momentum-0 replica inside a buffered SGD call, and both layouts."""
+    seen = {(r["dtype"], r["case"]["op"], r["strided"]) for r in DTYPE_RECORDS}
+    assert len(seen) == 3 * 3 * 2
+    sgd = [r["case"] for r in DTYPE_RECORDS if r["case"]["op"] == "sgd"]
+    assert any(c["momentum"] == "mixed" and c["nesterov"] and c["dampening"] == 0.1
+               for c in sgd)
+    assert {c["T"] for c in (r["case"] for r in DTYPE_RECORDS)} >= {45, 1000, 16397}
+    assert all(r["case"]["mask"] == "one_frozen" for r in DTYPE_RECORDS)
+
+
 @pytest.mark.parametrize("dtype", [torch.float64, torch.float16, torch.bfloat16])
 def test_cpu_other_dtypes_close_to_fp32(dtype):
     R, T = 3, 37
