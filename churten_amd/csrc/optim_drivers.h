@@ -323,7 +323,7 @@ constexpr int64_t kMallBytes = int64_t(256) << 20;
 
 // Launches above the MALL with at most kMidBytes of (R, T) operands reserve
 // each policy's kStreamLdsMid instead of its large-launch cap (with a
-// workspace). Measured with shape_sweep.hip at config 2's size (100 x 265,484,
+// workspace). Measured with a launch-shape sweep at config 2's size (100 x 265,484,
 // 75% active; three runs on two boxes): float32 Adam at cap 20 5.85-5.94 TB/s
 // against 5.66-5.74 at its cap of 14, and with amsgrad 5.83-5.91 against
 // 5.73-5.79 at its cap of 12. From 2 GB of operands on (R = 128, T = 1M to

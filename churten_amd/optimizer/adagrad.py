@@ -1,6 +1,6 @@
 """``Adagrad`` -- a GradientTransformation over the consolidated state.
 
-Restates src/torchstrap/optimizer/adagrad.py:274-346: ``init`` registers the
+Restates src/torchstrap/optimizer/adagrad.py:18-90: ``init`` registers the
 ``(N,)`` hyperparameters, the step counter and the ``(N, T)`` accumulator,
 filled with ``initial_accumulator_value`` (pad lanes included: they never see
 a gradient, so they never move the pad parameters); ``update`` issues one

@@ -1,6 +1,6 @@
 """``Adam`` -- a GradientTransformation over the consolidated state.
 
-Restates src/torchstrap/optimizer/adam.py:49-143: ``init`` registers the
+Restates src/torchstrap/optimizer/adam.py:18-112: ``init`` registers the
 per-replica ``(N,)`` hyperparameters (floats or tensors, stored in the param
 dtype), a zero ``state_steps`` counter, ``(N, T)`` moments (plus
 ``max_exp_avg_sqs`` under amsgrad) and the static variant flags; ``update``

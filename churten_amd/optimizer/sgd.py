@@ -1,6 +1,6 @@
 """``SGD`` -- a GradientTransformation over the consolidated state.
 
-Restates src/torchstrap/optimizer/sgd.py:168-256: ``init`` applies
+Restates src/torchstrap/optimizer/sgd.py:17-113: ``init`` applies
 torch.optim.SGD's Nesterov validation across the ensemble (non-zero momentum
 somewhere and no dampening anywhere), registers the ``(N,)``
 hyperparameters and the step counter, and allocates the ``(N, T)`` momentum

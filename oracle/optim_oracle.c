@@ -40,7 +40,7 @@
  *
  * Layout: contiguous row-major (R, T) float32 arrays; `steps` is (R,) float32
  * and is bumped in place (steps[r] += mask[r]) before the update, as every
- * reference operator does (cuda/adam.cu:277, cpu/adam.cpp:394).
+ * reference operator does (cuda/adam.cu:277, cpu/adam.cpp:341).
  *
  * bfloat16 optimizer state (this build's extension; the reference operators
  * reject mixed dtypes): the state is held here as float32 arrays of
