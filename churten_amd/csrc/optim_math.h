@@ -180,19 +180,27 @@ struct AdamHyper {
 };
 
 // A float divided by a per-replica constant b, as a multiply by the double
-// `rcp` = RN64(1 / b): RN32(RN64(x * rcp)) == RN32(x / b) for every float x
-// and b, bit for bit (zeros, infinities and NaNs included; rcp is +-inf for
-// b = +-0 and +-0 for b = +-inf), except when x and b are both NaN: then both
-// are NaN, the divide with x's payload, the product with b's (for Adam, b is
-// NaN only for a beta2 that makes 1 - beta2^step negative or NaN). Why: x and b have 24-bit significands, so x / b is never
-// a midpoint between two floats (a midpoint has a 25-bit odd significand M, and
-// x = b * M would need M to divide x's significand), and its distance to the
-// nearest midpoint is a nonzero multiple of 2^(e_b + e_q - 24) divided by b,
-// i.e. more than 2^-49 of |x / b|, also for subnormal x, b or quotient. The
-// double product errs by at most (1 + 2^-53)^2 - 1 < 2^-52 of it, so both sit
-// on the same side of every rounding boundary. Nine VALU instructions fewer per
-// element than the correctly rounded float divide; tests check the identity bit
-// for bit on every float x for a set of b, and through the update against torch.
+// `rcp` = RN64(1 / b): RN32(RN64(x * rcp)) == RN32(x / b) bit for bit for
+// every float x and b whose quotient is not a subnormal float (zeros,
+// infinities and NaNs included; rcp is +-inf for b = +-0 and +-0 for
+// b = +-inf), except when x and b are both NaN: then both are NaN, the divide
+// with x's payload, the product with b's (for Adam, b is NaN only for a beta2
+// that makes 1 - beta2^step negative or NaN). Why: x and b have 24-bit
+// significands, so a normal quotient is never a midpoint between two floats (a
+// midpoint there has a 25-bit odd significand M, and x = b * M would need M to
+// divide x's significand), and its distance to the nearest midpoint is more
+// than 2^-49 of |x / b|; the double product errs by at most
+// (1 + 2^-53)^2 - 1 < 2^-52 of it, so both sit on the same side of every
+// rounding boundary. A subnormal quotient has fewer significant bits, can be an
+// exact midpoint, and then the product may round the tie the other way
+// (x = 0x00012600, b = 50176: the divide gives 2 * 2^-149, the product
+// 2^-149). For Adam x = sqrt(v) of a float v is 0, at least 2^-75, inf or NaN,
+// so a subnormal quotient needs b > 2^51, i.e. 1 - beta2^step > 2^102, which
+// needs |beta2| > 1 (torch.optim rejects beta2 outside [0, 1)). Nine VALU
+// instructions fewer per element than the correctly rounded float divide;
+// tests check the identity bit for bit on every float x for a set of b, show
+// that the only exceptions are subnormal ties, and check the update against
+// torch.
 __device__ __forceinline__ float div_by_rcp(float x, double rcp) {
   return static_cast<float>(static_cast<double>(x) * rcp);
 }

@@ -163,13 +163,15 @@ def _split_segments(g, T):
     return [(g[:, a:b].contiguous(), a) for a, b in zip(cuts[:-1], cuts[1:]) if b > a]
 
 
+# SGD has no workspace entry points (nothing to precompute)
+_CASE_WS = [pytest.param(c, ws, id=C.case_id(c) + ("-ws" if ws else "-no_ws"))
+            for c in CASES for ws in (False, True) if not (ws and c["op"] == "sgd")]
+
+
 @pytest.mark.parametrize("form", ["dense", "segments", "segments_no_grad_out"])
-@pytest.mark.parametrize("workspace", [False, True], ids=["no_ws", "ws"])
 @pytest.mark.parametrize("bump", [True, False], ids=["bump", "caller_bumps"])
-@pytest.mark.parametrize("c", CASES, ids=C.case_id)
+@pytest.mark.parametrize("c,workspace", _CASE_WS)
 def test_entry_points_bit_exact_to_oracle(c, form, workspace, bump):
-    if workspace and c["op"] == "sgd":
-        pytest.skip("SGD has no workspace entry points (nothing to precompute)")
     x = C.make_inputs(c)
     names = _operand_names(c, x)
     dev = {k: torch.from_numpy(x[k].copy()).to(DEV) for k in names if k != "g"}
@@ -239,15 +241,18 @@ def test_segments_with_gap_take_zero_gradient(op, workspace):
                                   want[k].view(np.uint32)), k
 
 
-@pytest.mark.parametrize("workspace", [False, True], ids=["no_ws", "ws"])
-@pytest.mark.parametrize("op", ["adam", "sgd", "adagrad"])
+def _op_ws(ops):
+    """(op, workspace) pairs; SGD has no workspace entry points."""
+    return [pytest.param(op, ws, id=op + ("-ws" if ws else "-no_ws"))
+            for op in ops for ws in (False, True) if not (ws and op == "sgd")]
+
+
+@pytest.mark.parametrize("op,workspace", _op_ws(["adam", "sgd", "adagrad"]))
 @pytest.mark.parametrize("R,T", [(0, 5), (3, 0), (0, 0), (1, 1), (1, 3), (2, 1)])
 def test_empty_and_unit_shapes(op, R, T, workspace):
     """R or T of 0: the steps of active replicas still tick (when the library
     bumps), out_zero is written, nothing else is touched. R or T of 1: the
     update itself, against the oracle."""
-    if workspace and op == "sgd":
-        pytest.skip("SGD has no workspace entry points")
     g = torch.Generator(device=DEV).manual_seed(R * 10 + T)
     rnd = lambda: torch.randn(R, T, device=DEV, generator=g)  # noqa: E731
     p, gr = rnd(), rnd()
@@ -297,6 +302,101 @@ def test_null_out_zero_and_no_bump_leave_steps_alone():
         s = steps.clone()
         assert abi_step("adam", [p, gr, m, v], s, hyp, mask, 0, workspace=ws) == 0
         assert torch.equal(s, steps)
+
+
+LIB.ts_bump_steps.argtypes = [_I, _P, ctypes.POINTER(ctypes.c_uint8), _I64, _P, _P]
+
+
+@pytest.mark.parametrize("with_zero", [True, False], ids=["out_zero", "null_out_zero"])
+@pytest.mark.parametrize("R", [0, 1, 1000])
+@pytest.mark.parametrize("dtype", list(DTYPE_CODE), ids=str)
+def test_bump_steps_on_device(dtype, R, with_zero):
+    """ts_bump_steps, the reference's `state_steps.add_(active_mask.to(dtype))`
+    (cuda/adam.cu:277), on device buffers: two calls with complementary masks;
+    after each, the steps equal torch's own add of the mask in the steps' dtype
+    bit for bit (including its rounding: 256 + 1 rounds back to 256 in
+    bfloat16), the frozen replicas keep their bits, and out_zero reads +0 (a
+    NULL out_zero is accepted and writes nothing)."""
+    g = torch.Generator().manual_seed(R)
+    steps = torch.randint(0, 3000, (R,), generator=g).to(dtype)
+    if R:
+        steps[0] = 256.0
+    mask = torch.rand(R, generator=g) < 0.7
+    if R > 1:
+        mask[:2] = torch.tensor([True, False])
+    d_steps = steps.to(DEV)
+    stream = ctypes.c_void_p(torch.cuda.current_stream().cuda_stream)
+    for m in (mask, ~mask):
+        before = d_steps.clone()
+        want = before.clone().add_(m.to(DEV).to(dtype))
+        d_mask = m.to(torch.uint8).to(DEV)
+        mask_p = (ctypes.cast(d_mask.data_ptr(), ctypes.POINTER(ctypes.c_uint8)) if R
+                  else None)
+        zero = torch.full((), 7.0, dtype=dtype, device=DEV) if with_zero else None
+        rc = LIB.ts_bump_steps(DTYPE_CODE[dtype], _ptr(d_steps) if R else None, mask_p, R,
+                               _ptr(zero), stream)
+        torch.cuda.synchronize()
+        assert rc == 0
+        _same("steps", d_steps, want)
+        frozen = ~m.to(DEV)
+        _same("frozen steps", d_steps[frozen], before[frozen])
+        if with_zero:
+            _same("out_zero", zero, torch.zeros((), dtype=dtype, device=DEV))
+
+
+@pytest.mark.parametrize("layout", ["rows", "replica_minor"])
+@pytest.mark.parametrize("amsgrad", [False, True])
+def test_workspace_entries_of_frozen_replicas_are_never_written(amsgrad, layout):
+    """ts_adam_step_ws writes workspace constants for active replicas only:
+    with the workspace filled with NaN bit patterns before the call and the
+    frozen replicas at step 0 (whose bias corrections would divide by
+    1 - beta^0 = 0) holding NaN state, the frozen replicas' 16-byte entries
+    keep the NaN bytes, their rows or columns stay bit-identical, and every
+    operand equals the oracle's device form."""
+    R, T = 70, 45
+    rng = np.random.default_rng(21)
+    flags = TS_BUMP_STEPS | TS_ADAMW | (TS_AMSGRAD if amsgrad else 0)
+    host = [rng.standard_normal((R, T)).astype(np.float32) for _ in range(5)]
+    for a in host[2:]:
+        np.abs(a, out=a)
+    mask = np.ones(R, dtype=bool)
+    frozen = [0, 33, 69]
+    mask[frozen] = False
+    for a in host[2:]:
+        a[frozen] = np.nan
+    steps = np.where(mask, 3.0, 0.0).astype(np.float32)
+    hyp = [np.linspace(lo, hi, R, dtype=np.float32) for lo, hi in
+           ((1e-3, 5e-2), (0.8, 0.95), (0.99, 0.9999), (1e-9, 1e-7), (1e-2, 1e-2))]
+
+    def dev(a):
+        if layout == "rows":
+            return torch.from_numpy(a).to(DEV)
+        return torch.from_numpy(np.ascontiguousarray(a.T)).to(DEV).t()
+
+    ops = [dev(a) for a in host[:5 if amsgrad else 4]]
+    d_steps = torch.from_numpy(steps).to(DEV)
+    d_hyp = [torch.from_numpy(h).to(DEV) for h in hyp]
+    d_mask = torch.from_numpy(mask.astype(np.uint8)).to(DEV)
+    table = (RtBuf * 5)(*[RtBuf(t.data_ptr(), t.stride(0), t.stride(1)) for t in ops]
+                        + [RtBuf(0, 0, 1)] * (5 - len(ops)))
+    ws = torch.full((LIB.ts_workspace_bytes(R),), 0xFF, dtype=torch.uint8, device=DEV)
+    rc = LIB.ts_adam_step_ws(table, 0, _ptr(d_steps), *[_ptr(h) for h in d_hyp],
+                             ctypes.cast(d_mask.data_ptr(), ctypes.POINTER(ctypes.c_uint8)),
+                             R, T, flags, None, _ptr(ws), ws.numel(),
+                             ctypes.c_void_p(torch.cuda.current_stream().cuda_stream))
+    torch.cuda.synchronize()
+    assert rc == 0
+    entries = ws.view(R, 16).cpu()
+    assert (entries[frozen] == 0xFF).all()
+    assert not (entries[torch.from_numpy(mask)] == 0xFF).all(dim=1).any()
+    want = [a.copy() for a in host]
+    O.adam_step(O.DEVICE, want[0], want[1], want[2], want[3], want[4] if amsgrad else None,
+                steps, *hyp, mask, amsgrad=amsgrad, maximize=False, decoupled_weight_decay=True)
+    for i, t in enumerate(ops):
+        got = t.cpu().numpy()
+        assert np.array_equal(got.view(np.uint32), want[i].view(np.uint32)), i
+        assert np.array_equal(got[frozen].view(np.uint32), host[i][frozen].view(np.uint32)), i
+    assert np.array_equal(d_steps.cpu().numpy(), steps)
 
 
 # ---------------------------------------------------------------------------
@@ -416,15 +516,12 @@ def test_large_adagrad_rows_bit_identical_to_aten(dtype, workspace):
         _same(f"state_sums[{r}]", s[r], want_s[r])
 
 
-@pytest.mark.parametrize("workspace", [False, True], ids=["no_ws", "ws"])
-@pytest.mark.parametrize("op", ["adam", "sgd", "adagrad", "adagrad_f32"])
+@pytest.mark.parametrize("op,workspace", _op_ws(["adam", "sgd", "adagrad", "adagrad_f32"]))
 def test_large_float32_and_bf16_state_match_oracle(op, workspace):
     """float32 params with float32 and with bfloat16 optimizer state, large
     launches, against the oracle (bfloat16 state: the float32 step, then
     nearest-even rounding); the float32 Adagrad variant against the oracle's
     CPU form, which it reproduces."""
-    if workspace and op == "sgd":
-        pytest.skip("SGD has no workspace entry points")
     kind = "adagrad" if op == "adagrad_f32" else op
     nstate = {"adam": 2, "sgd": 1, "adagrad": 1}[kind]
     for state_bf16 in (False, True):

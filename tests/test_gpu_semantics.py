@@ -110,6 +110,48 @@ def test_sgd_momentum0_replica_is_plain_sgd():
     assert torch.equal(p[0], p0[0] - 0.25 * grad[0])  # lr a power of 2: exact
 
 
+@pytest.mark.parametrize("nesterov", [True, False], ids=["nesterov", "plain"])
+def test_sgd_momentum0_replica_with_dampening(nesterov):
+    """BASELINE config 3's combination (dampening 0.1, nesterov) on momentum-0
+    replicas inside a buffered call; ATen's fused SGD cannot express a
+    per-replica momentum of 0 next to buffered ones, so the values come from
+    the mathematics (reference cuda/sgd.cu:117-130 with momentum 0, in double):
+    - after its first step the buffer is fma(0, buf, (1-d)*g) = (1-d)*g, exact
+      in double ((1-d) has at most 28 significant bits, g 24), so the stored
+      buffer is RN32((1-d)*g);
+    - on its first step the buffer is g;
+    - the parameter moves by lr times g (nesterov: g + 0*buf) or times the
+      buffer narrowed to float (no nesterov: ATen assigns it to the float
+      gradient); with lr a power of 2 that product is exact and p - lr*x is
+      rounded to double and then to float, as computed here.
+    Beside them: a momentum-0.9 replica and a frozen momentum-0 replica."""
+    R, T = 4, 1000
+    d = 0.1
+    g = torch.Generator(device=DEV).manual_seed(14)
+    p = torch.randn(R, T, device=DEV, generator=g)
+    mb = torch.randn(R, T, device=DEV, generator=g)
+    grad = torch.randn(R, T, device=DEV, generator=g)
+    steps = torch.tensor([5.0, 0.0, 3.0, 2.0], device=DEV)  # replica 1 takes its first step
+    mask = torch.tensor([True, True, True, False], device=DEV)
+    p0, mb0 = p.clone(), mb.clone()
+    K.sgd_step_(p, grad, mb, steps, full(R, 0.25), torch.tensor([0.0, 0.0, 0.9, 0.0], device=DEV),
+                full(R, d), full(R, 0.0), mask, nesterov=nesterov, maximize=False)
+    torch.cuda.synchronize()
+    one_minus_d = 1.0 - torch.tensor(d, dtype=torch.float32).double()  # exact in double
+    buf64 = one_minus_d * grad[0].double()  # exact in double
+    assert torch.equal(mb[0], buf64.float())
+    assert torch.equal(mb[1], grad[1])
+    step0 = grad[0].double() if nesterov else buf64.float().double()
+    assert torch.equal(p[0], (p0[0].double() - 0.25 * step0).float())
+    assert torch.equal(p[1], (p0[1].double() - 0.25 * grad[1].double()).float())
+    assert torch.equal(p[3], p0[3]) and torch.equal(mb[3], mb0[3])
+    assert steps.tolist() == [6.0, 1.0, 4.0, 2.0]
+    # the forms a kernel could plausibly compute instead are distinguishable here
+    assert not torch.equal(mb[0], grad[0])  # dampening ignored on momentum-0 rows
+    d32 = torch.tensor(1.0 - d, dtype=torch.float32, device=DEV)
+    assert not torch.equal(mb[0], d32 * grad[0])  # (1 - d) rounded to float first
+
+
 @pytest.mark.parametrize("lr_decay", [0.0, 0.5])
 def test_adagrad_thawed_step_matches_never_frozen(lr_decay):
     """Reference test_inplace_adagrad_masking.py:91-131: a frozen replica's clock
@@ -454,12 +496,14 @@ def test_replica_minor_access_paths(R, pad, frozen):
 
 @pytest.mark.parametrize("amsgrad", [False, True])
 def test_replica_minor_step0_freeze_with_workspace(amsgrad):
-    """Replicas frozen before their first step keep step 0, so the per-replica
-    constants the operator's preparation launch writes for them divide by
-    1 - beta^0 = 0. The column driver's threads for a frozen replica exit
-    before reading those constants or any operand: with NaN in the frozen
-    replicas' state, their columns stay bit-identical and the active replicas
-    get the bits of contiguous buffers."""
+    """Replicas frozen before their first step keep step 0, where the bias
+    corrections would divide by 1 - beta^0 = 0. The operator's preparation
+    launch writes workspace constants for active replicas only, and the column
+    driver's threads for a frozen replica exit before reading constants or any
+    operand: with NaN in the frozen replicas' state, their columns stay
+    bit-identical and the active replicas get the bits of contiguous buffers.
+    (That the frozen replicas' workspace entries are never written is checked
+    through the C ABI with a NaN-filled workspace, in test_gpu_abi.py.)"""
     R, T = 70, 45
     a = adam_args(R, T, amsgrad, seed=11, steps=0.0)
     mask = torch.ones(R, dtype=torch.bool, device=DEV)

@@ -4,7 +4,10 @@ ts_adam_step_noalloc keeps the per-replica constants in the library's own
 device scratch array instead of a caller's workspace. On every call it must
 give what ts_adam_step_ws gives, bit for bit; calls run back to back, the
 later ones with smaller inputs (the scratch keeps the previous call's
-contents, which no call may depend on).
+contents, which no call may depend on). The first call in the process is made
+under HIP graph capture (the first call on a device looks up the scratch's
+address), and eager calls change neither torch's allocated bytes nor the
+device's free memory.
 """
 
 from __future__ import annotations
@@ -54,7 +57,7 @@ def _inputs(R, T, dtype, seed, amsgrad):
     return bufs, steps, hyp, mask
 
 
-def _call(noalloc, bufs, steps, hyp, mask, flags, dtype, out_zero):
+def _call(noalloc, bufs, steps, hyp, mask, flags, dtype, out_zero, sync=True):
     R, T = bufs[0].shape
     table = (RtBuf * 5)(*[RtBuf(t.data_ptr(), t.stride(0), t.stride(1)) for t in bufs]
                         + [RtBuf(0, 0, 1)] * (5 - len(bufs)))
@@ -67,8 +70,60 @@ def _call(noalloc, bufs, steps, hyp, mask, flags, dtype, out_zero):
     else:
         ws = torch.empty(LIB.ts_workspace_bytes(R), dtype=torch.uint8, device=DEV)
         rc = LIB.ts_adam_step_ws(*args, ws.data_ptr(), ws.numel(), stream)
-    torch.cuda.synchronize()
+    if sync:
+        torch.cuda.synchronize()
     return rc
+
+
+INTS = {torch.float32: torch.int32, torch.float64: torch.int64, torch.float16: torch.int16}
+
+
+def test_a_first_call_under_graph_capture_replays_match_workspace_entry_point():
+    """The process's first noalloc call is captured in a torch.cuda graph (the
+    scratch address lookup runs during capture). Three replays, each after a
+    new gradient is copied into the captured one and with eager calls of
+    ts_adam_step_ws on a twin state between them, equal the eager results bit
+    for bit; the captured steps bump and zero result replay too."""
+    R, T, dtype, flags = 12, 4 * 1000 + 12, torch.float32, TS_ADAMW | TS_BUMP_STEPS
+    bufs, steps, hyp, mask = _inputs(R, T, dtype, 7, False)
+    twin, twin_steps = [t.clone() for t in bufs], steps.clone()
+    z, tz = torch.full((1,), 5.0, device=DEV), torch.full((1,), 5.0, device=DEV)
+    g = torch.Generator(device=DEV).manual_seed(8)
+    grads = [torch.randn(R, T, device=DEV, generator=g) for _ in range(3)]
+    # warm up the library (its kernels load) on the workspace entry point only
+    warm = [t.clone() for t in bufs]
+    assert _call(False, warm, steps.clone(), hyp, mask, flags, dtype, z.clone()) == 0
+    graph = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(graph):
+        rc = _call(True, bufs, steps, hyp, mask, flags, dtype, z, sync=False)
+    assert rc == 0
+    for gr in grads:
+        bufs[1].copy_(gr)
+        twin[1].copy_(gr)
+        z.fill_(5.0)
+        graph.replay()
+        torch.cuda.synchronize()
+        assert _call(False, twin, twin_steps, hyp, mask, flags, dtype, tz) == 0
+        for k, (a, b) in enumerate(zip(bufs, twin)):
+            assert torch.equal(a.view(torch.int32), b.view(torch.int32)), k
+        assert torch.equal(steps, twin_steps)
+        assert z.item() == 0.0 and tz.item() == 0.0
+
+
+def test_eager_calls_allocate_nothing():
+    """After the first call on the device, noalloc calls (including a new
+    shape and dtype) leave torch's allocated bytes and hipMemGetInfo's free
+    bytes exactly as they were."""
+    inputs = [_inputs(R, T, dt, 50 + i, bool(f & TS_AMSGRAD)) + (dt, f)
+              for i, (R, T, dt, f) in enumerate(SEQUENCE[1:])]
+    z = [torch.zeros(1, device=DEV, dtype=x[4]) for x in inputs]
+    bufs, steps, hyp, mask, dt, f = inputs[0]
+    assert _call(True, bufs, steps, hyp, mask, f | TS_BUMP_STEPS, dt, z[0]) == 0
+    torch.cuda.synchronize()
+    before = (torch.cuda.memory_allocated(), torch.cuda.mem_get_info()[0])
+    for (bufs, steps, hyp, mask, dt, f), zi in zip(inputs, z):
+        assert _call(True, bufs, steps, hyp, mask, f | TS_BUMP_STEPS, dt, zi) == 0
+        assert (torch.cuda.memory_allocated(), torch.cuda.mem_get_info()[0]) == before
 
 
 # Calls in this order, one after the other: each later input is smaller.
@@ -91,9 +146,8 @@ def test_noalloc_equals_workspace_entry_point_on_successive_calls():
         for _ in range(2):  # two steps of each input
             assert _call(False, a_bufs, a_steps, hyp, mask, flags | TS_BUMP_STEPS, dtype, za) == 0
             assert _call(True, b_bufs, b_steps, hyp, mask, flags | TS_BUMP_STEPS, dtype, zb) == 0
-        ints = {torch.float32: torch.int32, torch.float64: torch.int64, torch.float16: torch.int16}
         for k, (a, b) in enumerate(zip(a_bufs, b_bufs)):
-            assert torch.equal(a.view(ints[dtype]), b.view(ints[dtype])), (i, R, T, k)
+            assert torch.equal(a.view(INTS[dtype]), b.view(INTS[dtype])), (i, R, T, k)
         assert torch.equal(a_steps, b_steps), (i, "steps")
         assert za.item() == 0 and zb.item() == 0
 
