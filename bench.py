@@ -135,11 +135,23 @@ def make_config(cfg: int, device="cuda", seed=None, N=None):
         args = (p, gr, m, v, None, steps, *hyp, mask)
         kw = dict(amsgrad=False, maximize=False, decoupled_weight_decay=False)
     active = int(mask.sum().item())
+    # Config 3: a replica's first step does not read its momentum buffer, but
+    # only the first call has first-step replicas (steps 0, bumped to 1);
+    # every later call, the timed ones included, reads every active buffer,
+    # so the bytes of a step are the steady state's (first_step_bytes below).
     nbytes = active * T * bytes_per_elem(cfg)
-    if cfg == 3:  # a replica's first step does not read its momentum buffer
-        first_active = int((mask & (steps == 0)).sum().item())
-        nbytes -= first_active * T * 4
     return c["op"], args, kw, nbytes
+
+
+def first_step_bytes(cfg: int, device="cuda") -> int | None:
+    """Config 3's first call: the steady-state bytes minus the momentum
+    buffers its first-step replicas do not read (4 B per element). The same
+    seeded draw as the timed state (the device's generator)."""
+    if cfg != 3:
+        return None
+    op_name, args, kw, nbytes = make_config(cfg, device=device)
+    mask, steps = args[-1], args[3]
+    return nbytes - int((mask & (steps == 0)).sum().item()) * args[0].shape[1] * 4
 
 
 # ---------------------------------------------------------------------------
@@ -226,14 +238,13 @@ def cpu_baseline_finish(proc):
 # ---------------------------------------------------------------------------
 # GPU measurements
 # ---------------------------------------------------------------------------
-def kernel_only_timing(op_name, args, kw, launches: int, extra_flags: int = 0,
-                       dtype_code: int = 0, workspace: bool = True) -> float:
-    """Average duration (ms) of the update: the C ABI is called without the
-    step bump, bracketed by HIP events on the launch stream. Adam and Adagrad
-    go through the workspace entry points, as the operator does; their
-    preparation launch (the per-replica constants, one tiny kernel) is inside
-    the bracket, a few microseconds against the update's milliseconds at
-    config 5. workspace=False times the entry points without one."""
+def abi_update_call(op_name, args, kw, extra_flags: int = 0, dtype_code: int = 0,
+                    workspace: bool = True):
+    """A no-argument function that enqueues one update through the C ABI on
+    torch's current stream, without the step bump, and returns its status.
+    Adam and Adagrad go through the workspace entry points, as the operator
+    does (their preparation launch then precedes the update); workspace=False
+    calls the entry points without one."""
     import ctypes
 
     import torch
@@ -283,6 +294,23 @@ def kernel_only_timing(op_name, args, kw, launches: int, extra_flags: int = 0,
             call = lambda: lib.ts_adagrad_step(*head, ctypes.c_void_p(stream.cuda_stream))  # noqa: E731
     else:
         raise ValueError(op_name)
+    def run():
+        return call()
+
+    run.keep_alive = (ws, bufs)  # the workspace and the operand table outlive the call
+    return run
+
+
+def kernel_only_timing(op_name, args, kw, launches: int, extra_flags: int = 0,
+                       dtype_code: int = 0, workspace: bool = True) -> float:
+    """Average duration (ms) of the update: `abi_update_call` bracketed by HIP
+    events on the launch stream. With a workspace the preparation launch (the
+    per-replica constants, one tiny kernel) is inside the bracket, a few
+    microseconds against the update's milliseconds at config 5."""
+    import torch
+
+    call = abi_update_call(op_name, args, kw, extra_flags, dtype_code, workspace)
+    stream = torch.cuda.current_stream()
     for _ in range(3):
         assert call() == 0
     e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
@@ -292,6 +320,147 @@ def kernel_only_timing(op_name, args, kw, launches: int, extra_flags: int = 0,
     e1.record(stream)
     torch.cuda.synchronize()
     return e0.elapsed_time(e1) / launches
+
+
+EVICT_BYTES = 1 << 30
+
+
+def mall_residency_timing(op_name, args, kw, nbytes: int, launches: int):
+    """Where an update's operands are served from when its launches run back
+    to back: each launch (preparation + update, through the C ABI) timed
+    alone between two HIP events, once with the previous launch right before
+    it (operands warm in the 256 MB MALL if they fit) and once with a 1 GiB
+    read of another buffer between launches, outside the timed interval,
+    which evicts them to HBM. Medians over the launches. rocprofv3's
+    FETCH_SIZE counts the bytes that leave the L2 whichever of the two serves
+    them, so this timing is what tells them apart."""
+    import torch
+
+    call = abi_update_call(op_name, args, kw)
+    stream = torch.cuda.current_stream()
+    evict = torch.ones(EVICT_BYTES // 4, device=args[0].device)
+    sink = torch.empty((), device=args[0].device)
+    for _ in range(3):
+        assert call() == 0
+    out = {}
+    for mode in ("warm", "evicted"):
+        ev = [(torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True))
+              for _ in range(launches)]
+        for e0, e1 in ev:
+            if mode == "evicted":
+                torch.amax(evict, dim=0, out=sink)
+            else:
+                call()  # the previous launch on the same operands
+            e0.record(stream)
+            call()
+            e1.record(stream)
+        torch.cuda.synchronize()
+        us = sorted(e0.elapsed_time(e1) * 1e3 for e0, e1 in ev)[launches // 2]
+        out[f"{mode}_us"] = round(us, 2)
+        out[f"{mode}_GBs"] = round(nbytes / (us * 1e-6) / 1e9, 1)
+    del evict
+    torch.cuda.empty_cache()
+    out["evicted_over_warm"] = round(out["evicted_us"] / out["warm_us"], 3)
+    out["operand_bytes"] = int(sum(t.numel() * t.element_size() for t in args
+                                   if t is not None and t.dim() == 2))
+    return out
+
+
+def geometry_timing(rows: int, launches: int, rounds: int = 3):
+    """Config 2's update (AdamW with amsgrad, its hyperparameter draws) at
+    `rows` replicas in four geometries, interleaved over `rounds` rounds in
+    one process: config 2's T (265,484: rows end off a 256-byte boundary)
+    and a T of 265,472 (rows of 4148 x 256 bytes), each with config 2's
+    Bernoulli(0.75) mask and with every replica active. GB/s of the active
+    rows' algorithmic bytes (36 B per element), best and mean."""
+    import torch
+
+    t_cfg = padded_width(CONFIGS[2]["layout"])
+    t_aligned = t_cfg - t_cfg % 64
+    out = {}
+    cases = {}
+    for name, T in (("ragged", t_cfg), ("aligned", t_aligned)):
+        g = torch.Generator(device="cuda").manual_seed(77)
+        f = dict(device="cuda", dtype=torch.float32)
+        p = torch.randn(rows, T, generator=g, **f).mul_(0.02)
+        gr = torch.randn(rows, T, generator=g, **f).mul_(1e-2)
+        m = torch.randn(rows, T, generator=g, **f).mul_(1e-3)
+        v = torch.randn(rows, T, generator=g, **f).mul_(1e-4).abs_()
+        mx = v.clone()
+        steps = torch.randint(1, 1001, (rows,), generator=g, device="cuda").float()
+        lr = torch.pow(10.0, torch.rand(rows, generator=g, **f) * 2 - 4)
+        hyp = [lr] + [torch.full((rows,), x, **f) for x in (0.9, 0.999, 1e-8, 1e-2)]
+        drawn = torch.rand(rows, generator=g, device="cuda") < 0.75
+        kw = dict(amsgrad=True, maximize=False, decoupled_weight_decay=True)
+        for mname, mask in (("mask_0.75", drawn), ("all_active", torch.ones_like(drawn))):
+            args = (p, gr, m, v, mx, steps, *hyp, mask)
+            nb = int(mask.sum().item()) * T * 36
+            cases[f"{name}_T{T}_{mname}"] = (abi_update_call("adam", args, kw), nb, args)
+    res = {k: [] for k in cases}
+    stream = torch.cuda.current_stream()
+    for rnd in range(rounds):
+        for k in (list(cases) if rnd % 2 == 0 else list(cases)[::-1]):
+            call, nb, _ = cases[k]
+            for _ in range(3):
+                assert call() == 0
+            e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+            e0.record(stream)
+            for _ in range(launches):
+                call()
+            e1.record(stream)
+            torch.cuda.synchronize()
+            res[k].append(nb / (e0.elapsed_time(e1) / launches * 1e-3) / 1e9)
+    for k, v in res.items():
+        out[k] = {"active": int(cases[k][2][-1].sum().item()), "best_GBs": round(max(v), 1),
+                  "mean_GBs": round(sum(v) / len(v), 1)}
+    del cases
+    torch.cuda.empty_cache()
+    return out
+
+
+def size_sweep_timing(cfg: int, ns, launches: int):
+    """The config's update on the first n rows of one allocation of max(ns)
+    rows (same buffers, same per-replica hyperparameters and mask, so only
+    the size changes), kernel-only time per launch, and per launch-size class
+    (operands up to 256 MB: small, up to 1 GiB: mid, above: large; each class
+    has its own launch shape) a least-squares fit t = t0 + bytes / rate: t0 is
+    what a launch costs beyond streaming its bytes (the preparation launch,
+    the grid's ramp-up, the drain of its last workgroups), `rate` the
+    streaming rate of that shape."""
+    import torch
+
+    op_name, full, kw, _ = make_config(cfg, N=max(ns))
+    T = full[0].shape[1]
+    n_rt = sum(t is not None and t.dim() == 2 for t in full)
+    pts = []
+    for n in sorted(ns):
+        args = tuple(t[:n] if t is not None else None for t in full)
+        mask = args[-1]
+        active = int(mask.sum().item())
+        nbytes = active * T * bytes_per_elem(cfg)
+        ms = kernel_only_timing(op_name, args, kw, launches)
+        opb = n * T * 4 * n_rt
+        pts.append({"N": n, "active": active, "bytes": nbytes, "operand_bytes": opb,
+                    "class": "small" if opb <= 256 << 20 else "mid" if opb <= 1 << 30 else "large",
+                    "kernel_avg_us": round(ms * 1e3, 2),
+                    "GBs": round(nbytes / (ms * 1e-3) / 1e9, 1)})
+    del full, args
+    torch.cuda.empty_cache()
+    fits = {}
+    for cls in ("small", "mid", "large"):
+        sel = [p for p in pts if p["class"] == cls]
+        if len(sel) < 3:
+            continue
+        xs = [p["bytes"] for p in sel]
+        ys = [p["kernel_avg_us"] for p in sel]
+        mx, my = sum(xs) / len(xs), sum(ys) / len(ys)
+        slope = (sum((x - mx) * (y - my) for x, y in zip(xs, ys))
+                 / sum((x - mx) ** 2 for x in xs))  # us per byte
+        t0 = my - slope * mx
+        fits[cls] = {"t0_us": round(t0, 2), "rate_GBs": round(1e-3 / slope, 1),
+                     "max_residual_us": round(max(abs(y - t0 - slope * x)
+                                                  for x, y in zip(xs, ys)), 2)}
+    return {"points": pts, "fits": fits}
 
 
 def loop_baseline(cfg: int, steps: int, fused: bool, hyper):
@@ -482,7 +651,7 @@ def bf16_state_timing(cfg: int, launches: int):
             "step_equivalent_GBs": round(active * T * bytes_per_elem(cfg) / (ms * 1e-3) / 1e9, 1)}
 
 
-def bf16_state_shared_timing(adam_args, launches: int):
+def bf16_state_shared_timing(adam_args, launches: int, ceiling: bool = True):
     """`bf16_state_timing` for config 5 on the float32 update's own buffers:
     params and grads as they are, the bfloat16 moments (the float32 moments
     narrowed) in the first half of the float32 moments' storage
@@ -503,15 +672,26 @@ def bf16_state_shared_timing(adam_args, launches: int):
     ms = kernel_only_timing("adam", args, {"amsgrad": False, "maximize": False,
                                            "decoupled_weight_decay": False},
                             launches, extra_flags=TS_STATE_BF16)
-    torch.cuda.empty_cache()
     per_elem = 20
     nbytes = int(mask.sum().item()) * T * per_elem
-    return {"kernel_avg_ms": round(ms, 4), "bytes_per_elem": per_elem,
-            "achieved_GBs": round(nbytes / (ms * 1e-3) / 1e9, 1),
-            "frac": round(nbytes / (ms * 1e-3) / 1e9 / HBM_PEAK_GBS, 4),
-            "step_equivalent_GBs": round(int(mask.sum().item()) * T * bytes_per_elem(5)
-                                         / (ms * 1e-3) / 1e9, 1),
-            "storage": "first half of the float32 moments' buffers"}
+    gbs = nbytes / (ms * 1e-3) / 1e9
+    out = {"kernel_avg_ms": round(ms, 4), "bytes_per_elem": per_elem,
+           "achieved_GBs": round(gbs, 1), "frac": round(gbs / HBM_PEAK_GBS, 4),
+           "step_equivalent_GBs": round(int(mask.sum().item()) * T * bytes_per_elem(5)
+                                        / (ms * 1e-3) / 1e9, 1),
+           "storage": "first half of the float32 moments' buffers"}
+    if ceiling:
+        # the same reads and writes without the arithmetic (cb_traffic mode 3),
+        # on the same views; c = 0 leaves every value as it is
+        shapes = [(1, 0), (1, 10), (1, 12), (1, 14), (1, 16), (2, 0), (2, 8), (2, 10), (2, 12),
+                  (2, 14)]
+        best, shape, rates = best_traffic(3, (p, gr, mb, vb), mask, 0.0, shapes, per_elem,
+                                          launches)
+        out["traffic_ceiling"] = {"GBs": best, "shape": shape,
+                                  "update_shape_GBs": rates[(2, 12)],
+                                  "update_of_ceiling": round(gbs / best, 4)}
+    torch.cuda.empty_cache()
+    return out
 
 
 def other_ops_timing(adam_args, launches: int):
@@ -547,6 +727,47 @@ def lds_for_residency(n: int, lds_per_cu: int = 160 * 1024) -> int:
     return x
 
 
+def traffic_rate(mode, bufs, mask, c, packs, cap, per_elem, launches) -> float:
+    """GB/s of one cb_traffic pattern (churten_amd/lib/libchurten_bench.so)
+    over the active rows of `bufs` (p, g, m, v), `packs` per thread under a
+    residency cap of `cap` one-wave workgroups per CU (0: none), timed over
+    `launches` back-to-back launches between two HIP events."""
+    import ctypes
+
+    import torch
+
+    lib = ctypes.CDLL(str(ROOT / "churten_amd" / "lib" / "libchurten_bench.so"))
+    p = bufs[0]
+    R, T = p.shape
+    active = int(mask.sum().item())
+    stream = torch.cuda.current_stream()
+    sink = torch.zeros(1, device=p.device)
+    vp = lambda t: ctypes.c_void_p(t.data_ptr())  # noqa: E731
+    lds = lds_for_residency(cap) if cap else 0
+    call = lambda: lib.cb_traffic(  # noqa: E731
+        ctypes.c_int(mode), *[vp(t) for t in bufs], vp(mask), ctypes.c_int64(R),
+        ctypes.c_int64(T), ctypes.c_float(c), ctypes.c_uint32(lds), ctypes.c_int(packs),
+        vp(sink), ctypes.c_void_p(stream.cuda_stream))
+    for _ in range(3):
+        assert call() == 0
+    e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    e0.record(stream)
+    for _ in range(launches):
+        call()
+    e1.record(stream)
+    torch.cuda.synchronize()
+    ms = e0.elapsed_time(e1) / launches
+    return round(active * T * per_elem / (ms * 1e-3) / 1e9, 1)
+
+
+def best_traffic(mode, bufs, mask, c, shapes, per_elem, launches):
+    """The best `traffic_rate` over (packs, cap) shapes: (GB/s, its shape, all rates)."""
+    rates = {(k, cap): traffic_rate(mode, bufs, mask, c, k, cap, per_elem, launches)
+             for k, cap in shapes}
+    (k, cap), r = max(rates.items(), key=lambda kv: kv[1])
+    return r, f"{k} pack{'s' if k > 1 else ''}, " + (f"cap {cap}" if cap else "uncapped"), rates
+
+
 def ceiling_timing(adam_args, launches: int):
     """The Adam step's traffic without its arithmetic on the same config-5
     buffers (churten_amd/lib/libchurten_bench.so), each kind at the best of a
@@ -556,42 +777,15 @@ def ceiling_timing(adam_args, launches: int):
     a 16 B read + 12 B write element reaches if reads and writes each ran at
     their own best rate, one after the other. Runs last: the write-only passes
     overwrite the buffers."""
-    import ctypes
-
     import torch
 
-    lib = ctypes.CDLL(str(ROOT / "churten_amd" / "lib" / "libchurten_bench.so"))
     p, gr, m, v = adam_args[:4]
     mask = adam_args[11]
     assert all(t.is_contiguous() and t.shape == p.shape and t.dtype == torch.float32
                for t in (p, gr, m, v))
-    R, T = p.shape
-    active = int(mask.sum().item())
-    stream = torch.cuda.current_stream()
-    sink = torch.zeros(1, device=p.device)
-    vp = lambda t: ctypes.c_void_p(t.data_ptr())  # noqa: E731
-
-    def rate(mode, c, packs, cap, per_elem):
-        lds = lds_for_residency(cap) if cap else 0
-        call = lambda: lib.cb_traffic(  # noqa: E731
-            ctypes.c_int(mode), vp(p), vp(gr), vp(m), vp(v), vp(mask), ctypes.c_int64(R),
-            ctypes.c_int64(T), ctypes.c_float(c), ctypes.c_uint32(lds), ctypes.c_int(packs),
-            vp(sink), ctypes.c_void_p(stream.cuda_stream))
-        for _ in range(3):
-            assert call() == 0
-        e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
-        e0.record(stream)
-        for _ in range(launches):
-            call()
-        e1.record(stream)
-        torch.cuda.synchronize()
-        ms = e0.elapsed_time(e1) / launches
-        return round(active * T * per_elem / (ms * 1e-3) / 1e9, 1)
 
     def best(mode, c, shapes, per_elem):
-        rates = {(k, cap): rate(mode, c, k, cap, per_elem) for k, cap in shapes}
-        (k, cap), r = max(rates.items(), key=lambda kv: kv[1])
-        return r, f"{k} pack{'s' if k > 1 else ''}, " + (f"cap {cap}" if cap else "uncapped"), rates
+        return best_traffic(mode, (p, gr, m, v), mask, c, shapes, per_elem, launches)
 
     mix, mix_shape, mix_rates = best(
         0, 0.0, [(1, 4), (1, 6), (1, 8), (1, 10), (1, 12), (1, 14), (2, 3), (2, 4), (2, 10)], 28)
@@ -830,6 +1024,15 @@ def main():
                     help="skip the replica-minor (column driver) timing")
     ap.add_argument("--no-grad-scatter", action="store_true",
                     help="skip the scatter-then-update vs fused segmented timing")
+    ap.add_argument("--no-mall", action="store_true",
+                    help="skip the warm-vs-evicted MALL timing (configs 1-4)")
+    ap.add_argument("--size-sweep", default="",
+                    help="comma-separated replica counts: time the config's update at each "
+                         "and fit a fixed cost plus a streaming rate (e.g. 50,100,150,200 "
+                         "for config 2)")
+    ap.add_argument("--geometry", type=int, default=0, metavar="ROWS",
+                    help="time config 2's update at ROWS replicas with ragged and 256-byte "
+                         "rows, with its mask and all replicas active (e.g. 800)")
     ap.add_argument("--calibrate-copy", action="store_true",
                     help="run only a plain 1 GiB device copy (reads and writes 2^30 B "
                          "each), to scale rocprofv3 FETCH_SIZE / WRITE_SIZE counters")
@@ -890,6 +1093,8 @@ def main():
     median_ms = per_step[len(per_step) // 2]
 
     kern_ms = kernel_only_timing(op_name, op_args, kw, max(10, args.steps))
+    mall = (mall_residency_timing(op_name, op_args, kw, nbytes, max(10, args.steps))
+            if args.config != 5 and not args.no_mall else None)
     # the same update through the entry points without a workspace (every
     # workgroup derives its replica's constants): what the workspace buys
     nows_ms = (kernel_only_timing(op_name, op_args, kw, max(10, args.steps), workspace=False)
@@ -902,7 +1107,8 @@ def main():
     low_prec = None
     if args.config == 5:
         if not args.no_bf16_state:
-            bf16 = bf16_state_shared_timing(op_args, max(10, args.steps // 2))
+            bf16 = bf16_state_shared_timing(op_args, max(10, args.steps // 2),
+                                            ceiling=not args.no_ceiling)
         if not args.no_low_precision:
             low_prec = low_precision_timing(op_args, max(10, args.steps // 2))
     ceiling = (ceiling_timing(op_args, max(10, args.steps // 2))
@@ -951,6 +1157,13 @@ def main():
     minor = None if args.no_replica_minor else replica_minor_timing(args.config,
                                                                     max(10, args.steps // 2))
 
+    sweep = None
+    if args.size_sweep:
+        sweep = size_sweep_timing(args.config, [int(x) for x in args.size_sweep.split(",")],
+                                  max(10, args.steps))
+
+    geometry = geometry_timing(args.geometry, max(10, args.steps // 5)) if args.geometry else None
+
     scatter = None
     if not args.no_grad_scatter and op_name == "adam":
         scatter = grad_scatter_timing(args.config, max(5, args.steps // 2))
@@ -986,6 +1199,7 @@ def main():
                                f"N={c['N']} x T={padded_width(c['layout'])}",
                    "N": c["N"], "T": padded_width(c["layout"]),
                    "active_bytes_per_step": nbytes, "bytes_per_elem": bytes_per_elem(args.config),
+                   "first_call_bytes": first_step_bytes(args.config),
                    "parallelism": "single GPU"},
         "roofline": {"bound": "hbm", "kernel": kernel, "achieved": round(achieved, 1),
                      "peak": HBM_PEAK_GBS, "unit": "GB/s",
@@ -1008,6 +1222,9 @@ def main():
         "fp64_roofline": fp64_roofline,
         "snapshot": snapshot,
         "graph_replay": graphed,
+        "mall_residency": mall,
+        "size_sweep": sweep,
+        "geometry": geometry,
         "speedup_vs_python_loop": ({k: round(v / step_ms, 2) for k, v in loop.items()}
                                    if loop else None),
         "python_loop_note": ("torch.optim per replica, own hyperparameters, active replicas "

@@ -19,7 +19,13 @@
 //      exp_avg_sq (28 B per active element, the Adam step's traffic)
 //   1  the four reads only (16 B)
 //   2  the three writes only (12 B; the written values are `c`)
-// Mode 0 writes x + g * c, so with c = 0 it leaves finite values unchanged.
+//   3  mode 0 with bfloat16 moments next to float32 params and grads, as
+//      Adam with TS_STATE_BF16 moves them: `m` and `v` point at (R, T)
+//      bfloat16 buffers, read and written 8 bytes (4 values) per thread per
+//      pack, params and grads 16 bytes (20 B per active element)
+// Mode 0 writes x + g * c, so with c = 0 it leaves finite values unchanged;
+// mode 3 writes params likewise and flips the lowest bit of every moment
+// value when c != 0.
 
 #include <hip/hip_runtime.h>
 
@@ -87,6 +93,53 @@ __global__ __launch_bounds__(kThreads) void traffic_kernel(float* p, const float
   if constexpr (MODE == 1) {
     // keeps the reads: the host passes a `c` no sum of the data reaches
     if (acc.x + acc.y + acc.z + acc.w == c) sink[0] = acc.x;
+  }
+}
+
+using U2 = uint32_t __attribute__((ext_vector_type(2)));
+
+__device__ __forceinline__ U2 ld(const U2* p) { return __builtin_nontemporal_load(p); }
+__device__ __forceinline__ void st(U2* p, U2 v) { __builtin_nontemporal_store(v, p); }
+
+// Mode 3 of cb_traffic: tiles as traffic_kernel's, moments as 4-value
+// bfloat16 packs.
+template <int kUnroll>
+__global__ __launch_bounds__(kThreads) void traffic_bf16_kernel(float* p, const float* g,
+                                                                uint16_t* m, uint16_t* v,
+                                                                const uint8_t* mask, int64_t T,
+                                                                uint32_t tiles, float c) {
+  constexpr int64_t kTile = int64_t(kThreads) * 4 * kUnroll;
+  const uint32_t b = blockIdx.x;
+  const uint32_t r = b / tiles;
+  const int64_t t0 = int64_t(b - r * tiles) * kTile;
+  if (!mask[r]) return;
+  const int64_t base = int64_t(r) * T + t0;
+  F4* const P = reinterpret_cast<F4*>(p + base);
+  const F4* const G = reinterpret_cast<const F4*>(g + base);
+  U2* const M = reinterpret_cast<U2*>(m + base);
+  U2* const V = reinterpret_cast<U2*>(v + base);
+  const int64_t left = (T - t0) / 4;
+  const uint32_t flip = c != 0.0f ? 0x00010001u : 0u;  // the lowest bit of both values
+  F4 a[kUnroll], bb[kUnroll];
+  U2 cc[kUnroll], d[kUnroll];
+#pragma unroll
+  for (int u = 0; u < kUnroll; ++u) {
+    const int64_t i = int64_t(u) * kThreads + threadIdx.x;
+    if (i < left) {
+      a[u] = ld(P + i);
+      bb[u] = ld(G + i);
+      cc[u] = ld(M + i);
+      d[u] = ld(V + i);
+    }
+  }
+#pragma unroll
+  for (int u = 0; u < kUnroll; ++u) {
+    const int64_t i = int64_t(u) * kThreads + threadIdx.x;
+    if (i < left) {
+      st(P + i, a[u] + bb[u] * c);
+      st(M + i, cc[u] ^ flip);
+      st(V + i, d[u] ^ flip);
+    }
   }
 }
 
@@ -180,15 +233,15 @@ extern "C" int cb_div_bc2s(const float* x, const float* b, int64_t b_stride, flo
   return static_cast<int>(hipGetLastError());
 }
 
-// The pattern over the active rows of four row-major (R, T) float32 buffers:
-// T a multiple of 4, every base 16-byte aligned, `mask` R bytes, `packs` 1 or
-// 2 per thread. `lds` is the dynamic LDS per workgroup (a residency cap, as
-// the streaming driver's). Returns 0, 1 on bad arguments, or the HIP error
-// code.
+// The pattern over the active rows of four row-major (R, T) buffers (float32;
+// in mode 3 `m` and `v` hold bfloat16): T a multiple of 4, every base 16-byte
+// aligned, `mask` R bytes, `packs` 1 or 2 per thread. `lds` is the dynamic LDS
+// per workgroup (a residency cap, as the streaming driver's). Returns 0, 1 on
+// bad arguments, or the HIP error code.
 extern "C" int cb_traffic(int mode, float* p, const float* g, float* m, float* v,
                           const uint8_t* mask, int64_t R, int64_t T, float c, uint32_t lds,
                           int packs, float* sink, hipStream_t stream) {
-  if (R <= 0 || T <= 0 || T % 4 != 0 || mode < 0 || mode > 2 || packs < 1 || packs > 2) return 1;
+  if (R <= 0 || T <= 0 || T % 4 != 0 || mode < 0 || mode > 3 || packs < 1 || packs > 2) return 1;
   for (const void* q : {static_cast<const void*>(p), static_cast<const void*>(g),
                         static_cast<const void*>(m), static_cast<const void*>(v)}) {
     if (reinterpret_cast<uintptr_t>(q) % 16 != 0) return 1;
@@ -198,6 +251,18 @@ extern "C" int cb_traffic(int mode, float* p, const float* g, float* m, float* v
   if (tiles > INT32_MAX || R > INT32_MAX / tiles) return 1;
   const dim3 grid(static_cast<uint32_t>(R * tiles)), block(kThreads);
   const uint32_t t32 = static_cast<uint32_t>(tiles);
+  if (mode == 3) {
+    uint16_t* const mb = reinterpret_cast<uint16_t*>(m);
+    uint16_t* const vb = reinterpret_cast<uint16_t*>(v);
+    if (packs == 1) {
+      hipLaunchKernelGGL(traffic_bf16_kernel<1>, grid, block, lds, stream, p, g, mb, vb, mask,
+                         T, t32, c);
+    } else {
+      hipLaunchKernelGGL(traffic_bf16_kernel<2>, grid, block, lds, stream, p, g, mb, vb, mask,
+                         T, t32, c);
+    }
+    return static_cast<int>(hipGetLastError());
+  }
   using K = void (*)(float*, const float*, float*, float*, const uint8_t*, int64_t, uint32_t,
                      float, float*);
   const K kernels[3][2] = {{traffic_kernel<0, 1>, traffic_kernel<0, 2>},

@@ -49,12 +49,41 @@ def test_traffic_modes(T, packs):
     assert torch.equal(ts[1], before[1])                # the gradient is only read
 
 
+@pytest.mark.parametrize("packs", [1, 2])
+@pytest.mark.parametrize("T", [4, 1000, 1028, 4096])
+def test_traffic_bf16_moments_mode(T, packs):
+    """Mode 3: float32 params and grads, bfloat16 moments. With c = 0 nothing
+    changes; with c != 0 the active rows' params become p + g * c and their
+    moments' bits flip in the lowest bit, frozen rows and the gradient stay."""
+    lib = ctypes.CDLL(str(LIB))
+    R = 3
+    g = torch.Generator(device="cuda").manual_seed(T + 1)
+    p, gr = (torch.randn(R, T, device="cuda", generator=g) for _ in range(2))
+    m, v = (torch.randn(R, T, device="cuda", generator=g).to(torch.bfloat16) for _ in range(2))
+    ts = [p, gr, m, v]
+    before = [t.clone() for t in ts]
+    mask = torch.tensor([True, False, True], device="cuda")
+    sink = torch.zeros(1, device="cuda")
+    assert call(lib, 3, ts, mask, 0.0, sink, packs=packs) == 0
+    torch.cuda.synchronize()
+    for a, b in zip(ts, before):
+        assert torch.equal(a.view(torch.int32 if a.dtype == torch.float32 else torch.int16),
+                           b.view(torch.int32 if b.dtype == torch.float32 else torch.int16))
+    assert call(lib, 3, ts, mask, 0.5, sink, packs=packs) == 0
+    torch.cuda.synchronize()
+    assert torch.equal(p[mask], before[0][mask] + before[1][mask] * 0.5)
+    assert torch.equal(p[~mask], before[0][~mask]) and torch.equal(gr, before[1])
+    for t, b in ((m, before[2]), (v, before[3])):
+        ti, bi = t.view(torch.int16), b.view(torch.int16)
+        assert torch.equal(ti[mask], bi[mask] ^ 1) and torch.equal(ti[~mask], bi[~mask])
+
+
 def test_traffic_rejects_bad_arguments():
     lib = ctypes.CDLL(str(LIB))
     ts = [torch.zeros(2, 8, device="cuda") for _ in range(4)]
     mask = torch.ones(2, dtype=torch.bool, device="cuda")
     sink = torch.zeros(1, device="cuda")
-    assert call(lib, 3, ts, mask, 0.0, sink) == 1                 # no such mode
+    assert call(lib, 4, ts, mask, 0.0, sink) == 1                 # no such mode
     assert call(lib, 0, ts, mask, 0.0, sink, packs=3) == 1        # 1 or 2 packs only
     assert call(lib, 0, ts, mask, 0.0, sink, T=6) == 1            # T not a multiple of 4
     odd = [t.view(-1)[1:9].view(1, 8) for t in ts]               # 4-byte aligned only
