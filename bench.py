@@ -449,18 +449,22 @@ def size_sweep_timing(cfg: int, ns, launches: int):
     fits = {}
     for cls in ("small", "mid", "large"):
         sel = [p for p in pts if p["class"] == cls]
-        if len(sel) < 3:
-            continue
-        xs = [p["bytes"] for p in sel]
-        ys = [p["kernel_avg_us"] for p in sel]
-        mx, my = sum(xs) / len(xs), sum(ys) / len(ys)
-        slope = (sum((x - mx) * (y - my) for x, y in zip(xs, ys))
-                 / sum((x - mx) ** 2 for x in xs))  # us per byte
-        t0 = my - slope * mx
-        fits[cls] = {"t0_us": round(t0, 2), "rate_GBs": round(1e-3 / slope, 1),
-                     "max_residual_us": round(max(abs(y - t0 - slope * x)
-                                                  for x, y in zip(xs, ys)), 2)}
+        if len(sel) >= 3:
+            fits[cls] = fit_fixed_and_rate([p["bytes"] for p in sel],
+                                           [p["kernel_avg_us"] for p in sel])
     return {"points": pts, "fits": fits}
+
+
+def fit_fixed_and_rate(nbytes, us):
+    """Least-squares t = t0 + bytes / rate over (bytes, microseconds) points:
+    t0 in microseconds, rate in GB/s, and the largest residual."""
+    n = len(nbytes)
+    mx, my = sum(nbytes) / n, sum(us) / n
+    slope = (sum((x - mx) * (y - my) for x, y in zip(nbytes, us))
+             / sum((x - mx) ** 2 for x in nbytes))  # us per byte
+    t0 = my - slope * mx
+    return {"t0_us": round(t0, 2), "rate_GBs": round(1e-3 / slope, 1),
+            "max_residual_us": round(max(abs(y - t0 - slope * x) for x, y in zip(nbytes, us)), 2)}
 
 
 def loop_baseline(cfg: int, steps: int, fused: bool, hyper):
