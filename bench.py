@@ -13,6 +13,10 @@ one update launch / its average duration, measured with HIP events on the
 launch stream), the reference CPU kernel timed on this host, the N-instance
 torch.optim Python-loop baseline on the same GPU, and the training step's
 gradient hand-off (per-parameter scatter then update, vs the fused segmented update).
+Configs 1-4 add `mall_residency` (each launch warm vs after a MALL-evicting
+read); `--size-sweep N1,N2,...` fits a fixed cost and a streaming rate over
+replica counts, and `--geometry ROWS` times config 2's update with ragged and
+256-byte rows, with and without frozen replicas.
 
     python bench.py [--gpus 1] [--steps K] [--warmup W] [--config 5]
 """
