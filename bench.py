@@ -414,9 +414,9 @@ def geometry_timing(rows: int, launches: int, rounds: int = 3):
             e1.record(stream)
             torch.cuda.synchronize()
             res[k].append(nb / (e0.elapsed_time(e1) / launches * 1e-3) / 1e9)
-    for k, v in res.items():
-        out[k] = {"active": int(cases[k][2][-1].sum().item()), "best_GBs": round(max(v), 1),
-                  "mean_GBs": round(sum(v) / len(v), 1)}
+    for k, rates in res.items():
+        out[k] = {"active": int(cases[k][2][-1].sum().item()), "best_GBs": round(max(rates), 1),
+                  "mean_GBs": round(sum(rates) / len(rates), 1)}
     del cases
     torch.cuda.empty_cache()
     return out
