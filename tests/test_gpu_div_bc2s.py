@@ -106,7 +106,7 @@ def test_div_bc2s_random_pairs_and_sensitivity():
 
 
 # Divisors whose odd part is small, so that subnormal quotients can be exact
-# midpoints (b = 49 * 2^10 is the smallest of the advisor-style examples).
+# midpoints (b = 49 * 2^10 = 50176 gives one at x = 0x00012600).
 TIE_DIVISORS = [49.0 * 2.0 ** 10, 49.0 * 2.0 ** 52, 3.0 * 2.0 ** 60]
 
 
