@@ -152,6 +152,21 @@ def test_noalloc_equals_workspace_entry_point_on_successive_calls():
         assert za.item() == 0 and zb.item() == 0
 
 
+def test_noalloc_at_its_largest_replica_count():
+    """R = 65536, the scratch's capacity, every replica's constants in use
+    (the last entry at the array's end): equal to the workspace form."""
+    R, T = 65536, 8
+    bufs, steps, hyp, mask = _inputs(R, T, torch.float32, 11, False)
+    mask.fill_(1)
+    b_bufs, b_steps = [t.clone() for t in bufs], steps.clone()
+    za, zb = torch.ones(1, device=DEV), torch.ones(1, device=DEV)
+    assert _call(False, bufs, steps, hyp, mask, TS_ADAMW | TS_BUMP_STEPS, torch.float32, za) == 0
+    assert _call(True, b_bufs, b_steps, hyp, mask, TS_ADAMW | TS_BUMP_STEPS, torch.float32, zb) == 0
+    for k, (a, b) in enumerate(zip(bufs, b_bufs)):
+        assert torch.equal(a.view(torch.int32), b.view(torch.int32)), k
+    assert torch.equal(steps, b_steps) and za.item() == 0 and zb.item() == 0
+
+
 def test_noalloc_rejects_more_replicas_than_its_scratch_holds():
     R, T = 65537, 4
     bufs = [torch.zeros(R, T, device=DEV) for _ in range(4)]
