@@ -11,10 +11,11 @@
 //   stream_kernel   unit inner stride (the consolidated layout `State`
 //                   produces, and ragged or misaligned rows): one wavefront
 //                   per tile (1-4 packs of 4 or 8 elements per thread by
-//                   operand types), non-temporal 16-byte loads and stores
-//                   from each row's first 256-byte boundary (tiles never
-//                   share a cache line), the few head and tail elements of a
-//                   row one at a time;
+//                   operand types), non-temporal 16-byte loads and stores,
+//                   tiles on the row's boundaries of the tile size (tiles
+//                   never share a cache line) and one head tile per row for
+//                   what lies before the first, the few elements off the
+//                   pack grid one at a time;
 //                   large launches cap residency per CU. Operands at another
 //                   16-byte phase than the parameters take element-aligned
 //                   packs (the ANY variant).
@@ -102,6 +103,16 @@ constexpr uint32_t kAlignBytes = 256;
 template <typename T>
 constexpr uint32_t align_elems() {
   return kAlignBytes / sizeof(T);
+}
+
+// Rows' phases (res0 / rmod) are kept modulo this many bytes: a multiple of
+// every alignment the drivers use (256 bytes for the segmented and scatter
+// walks, the streaming driver's tile size: 1-8 KB). All are powers of two, so
+// a phase product res0 + r * rmod that wraps in 32 bits keeps its residue.
+constexpr uint32_t kPhaseBytes = 16384;
+template <typename T>
+constexpr uint32_t phase_elems() {
+  return kPhaseBytes / sizeof(T);
 }
 
 // N consecutive elements of one operand: 4 in the drivers' usual pack (16 B
@@ -246,17 +257,22 @@ __device__ __forceinline__ bool ilp_row(uint32_t rule, uint32_t r) {
 // Doubles per replica in a workspace of per-replica constants.
 constexpr int kPreStride = 2;
 
-// Tiles of a driver's tile size per row. For the streaming driver, row r's first
-// 256-byte boundary lies head(r) = (A - (res0 + r * rmod) % A) % A elements in
-// (A: 256 bytes in elements of the parameter type; res0: the parameter base's
-// element offset modulo A, rmod: its row stride modulo A); packs stream from
-// there and the head and the at most three tail elements of each row go one at
-// a time. Where every operand shares the parameter's phase modulo the pack, the
-// packs are aligned in all of them (else the ANY variants run).
+// Tiles of a driver's tile size per row. res0 is the parameter base's element
+// offset and rmod its row stride, both modulo kPhaseBytes in elements of the
+// parameter type. For the streaming driver, row r's first boundary of the tile
+// size (TILE elements) lies head(r) = (TILE - (res0 + r * rmod) % TILE) % TILE
+// elements in; its tiles k >= 1 start there, and its tile 0 takes the head
+// (packs from the first pack boundary, fewer than a pack before it one element
+// at a time) and the row's fewer than a pack of tail elements. Where every
+// operand shares the parameter's phase modulo the pack, the packs are aligned
+// in all of them (else the ANY variants run).
 struct Grid {
   int64_t T;
   uint32_t tiles_per_row;
   uint32_t res0, rmod;
+  // Workgroups at the start of the grid that take each row's tile 0 (the
+  // streaming driver's head tiles: one per row), before the rows' other tiles.
+  uint32_t heads;
 };
 
 // Integer minimum for tile bounds (a plain compare-and-select; HIP's generic
@@ -269,6 +285,23 @@ __device__ __forceinline__ void tile_of_block(const Grid& g, uint32_t& r,
   const uint32_t tile = blockIdx.x;
   r = tile / g.tiles_per_row;
   t0 = int64_t(tile - r * g.tiles_per_row) * TILE;
+}
+
+// The streaming driver's grid: workgroup b < heads takes row b's tile 0;
+// the others take row r's tile k + 1 (t0 = (k + 1) * TILE) in row-major order,
+// the same order as a grid without head tiles, shifted by `heads`.
+template <int64_t TILE>
+__device__ __forceinline__ void stream_tile_of_block(const Grid& g, uint32_t& r,
+                                                     int64_t& t0) {
+  const uint32_t b = blockIdx.x;
+  if (b < g.heads) {
+    r = b;
+    t0 = 0;
+    return;
+  }
+  const uint32_t m = b - g.heads;
+  r = m / g.tiles_per_row;
+  t0 = int64_t(m - r * g.tiles_per_row + 1) * TILE;
 }
 
 template <typename T>
@@ -968,115 +1001,141 @@ __global__ __launch_bounds__((stream_threads<P, SMALL>())) void stream_kernel(KA
   constexpr int KP = P::kStreamPack;
   constexpr int U = stream_unroll_of<P, PRE, SMALL>();
   constexpr int64_t kStreamTile = stream_tile<P, PRE, SMALL>();
+  static_assert((kStreamTile & (kStreamTile - 1)) == 0 &&
+                    phase_elems<T>() % kStreamTile == 0,
+                "streaming tiles align to their own size, a divisor of the phase modulus");
   uint32_t r;
   int64_t t0;
-  tile_of_block<kStreamTile>(a.g, r, t0);
+  stream_tile_of_block<kStreamTile>(a.g, r, t0);
   if (!a.vec.mask[r]) {
     return;
   }
-  const bool load_state = P::reads_state(a.vec, r);
 
-  constexpr uint32_t A = align_elems<T>();
+  // A row's tiles k >= 1 start at its first kStreamTile-element boundary, so
+  // no tile straddles one (tiles aligned to 256 bytes only ran 1.5-2% slower).
+  // Tile 0 takes what lies before that boundary: packs from the first pack
+  // boundary, the fewer than KP elements before it one at a time, and the
+  // row's fewer than KP tail elements. The two kinds branch apart here, so a
+  // main tile computes no more addresses than a plain row-major tile.
   const int64_t width = a.g.T;
-  const int64_t head = imin(width, (A - (a.g.res0 + r * a.g.rmod) % A) % A);
-  const int64_t packs_row = (width - head) / KP;
-  T* const pbase = pg_row<P>(a.x, 0, r);
-  const T* const gbase = pg_row<P>(a.x, 1, r);
-  S* sbase[SS];
-#pragma unroll
-  for (int b = 0; b < NS; ++b) sbase[b] = state_row<P>(a.x, 2 + b, r);
+  const uint32_t phase = (a.g.res0 + r * a.g.rmod) % uint32_t(kStreamTile);
+  const int64_t head = imin(width, (kStreamTile - phase) % kStreamTile);
 
-  // The parameters' packs are aligned by construction (a row's packs start at
-  // its first 256-byte boundary); with ANY the other operands sit at another
-  // phase and use element-aligned packs.
-  Pack<T, KP>* prow = reinterpret_cast<Pack<T, KP>*>(pbase + head) + t0 / KP;
-  const Packs<ANY, T, NT, KP> grow(const_cast<T*>(gbase) + head + t0);
-  Packs<ANY, S, NT, KP> srow[SS];
+  // The packs [first, first + packs_left * KP) of row r, then (head tile)
+  // the single elements [0, pre) and [body_end, width).
+  const auto run = [&](auto head_tile, int64_t first, int64_t packs_left, int64_t pre,
+                       int64_t body_end) __attribute__((always_inline)) {
+    const bool load_state = P::reads_state(a.vec, r);
+    T* const pbase = pg_row<P>(a.x, 0, r);
+    const T* const gbase = pg_row<P>(a.x, 1, r);
+    S* sbase[SS];
 #pragma unroll
-  for (int b = 0; b < NS; ++b) srow[b] = Packs<ANY, S, NT, KP>(sbase[b] + head + t0);
-  const int64_t packs_left = packs_row - t0 / KP;
+    for (int b = 0; b < NS; ++b) sbase[b] = state_row<P>(a.x, 2 + b, r);
 
-  Pack<T, KP> vp[U], vg[U];
-  Pack<S, KP> vs[SS][U];
+    // The parameters' packs are aligned by construction (`first` lies on a
+    // pack boundary of the row); with ANY the other operands sit at another
+    // phase and use element-aligned packs.
+    Pack<T, KP>* prow = reinterpret_cast<Pack<T, KP>*>(pbase + first);
+    const Packs<ANY, T, NT, KP> grow(const_cast<T*>(gbase) + first);
+    Packs<ANY, S, NT, KP> srow[SS];
 #pragma unroll
-  for (int u = 0; u < U; ++u) {
-    const int64_t i = int64_t(u) * NTH + threadIdx.x;
-    if (i < packs_left) {
-      vp[u] = load_stream<NT>(prow + i);
-      vg[u] = grow.load(i);
-      if (load_state) {
-#pragma unroll
-        for (int b = 0; b < NS; ++b) {
-          vs[b][u] = srow[b].load(i);
-        }
-      }
-    }
-  }
-  typename P::Rep rep;
-  P::template prologue<PRE>(a.vec, r, rep);
-  const auto store_packs = [&](int u, int64_t i) {
-    store_stream<NT>(prow + i, vp[u]);
-#pragma unroll
-    for (int b = 0; b < NS; ++b) {
-      srow[b].store(i, vs[b][u]);
-    }
-  };
-  const auto compute = [&](const typename P::Rep& rp, bool maximize)
-                           __attribute__((always_inline)) {
+    for (int b = 0; b < NS; ++b) srow[b] = Packs<ANY, S, NT, KP>(sbase[b] + first);
+
+    Pack<T, KP> vp[U], vg[U];
+    Pack<S, KP> vs[SS][U];
 #pragma unroll
     for (int u = 0; u < U; ++u) {
       const int64_t i = int64_t(u) * NTH + threadIdx.x;
       if (i < packs_left) {
-        Pack<S, KP> st[SS];
+        vp[u] = load_stream<NT>(prow + i);
+        vg[u] = grow.load(i);
+        if (load_state) {
 #pragma unroll
-        for (int b = 0; b < NS; ++b) st[b] = vs[b][u];
-        apply_pack<P, KP>(vp[u], vg[u], st, load_state, rp, maximize);
-#pragma unroll
-        for (int b = 0; b < NS; ++b) vs[b][u] = st[b];
-        if constexpr (!P::kLateStores) store_packs(u, i);
+          for (int b = 0; b < NS; ++b) {
+            vs[b][u] = srow[b].load(i);
+          }
+        }
       }
     }
-  };
-  // The replica's weight decay and `maximize` are uniform over the workgroup:
-  // branch on them once instead of evaluating the decay term per element and
-  // selecting (what the compiler makes of the per-element test). The common
-  // case, neither, runs the math with both as constants.
-  if (!a.maximize && !P::decays(rep)) {
-    typename P::Rep plain = rep;
-    P::drop_decay(plain);
-    with_variant<P>(plain, [&](const typename P::Rep& rp) { compute(rp, false); });
-  } else {
-    with_variant<P>(rep, [&](const typename P::Rep& rp) {
-      with_maximize<P>(a.maximize, [&](bool mx) { compute(rp, mx); });
-    });
-  }
-  if constexpr (P::kLateStores) {
+    typename P::Rep rep;
+    P::template prologue<PRE>(a.vec, r, rep);
+    const auto store_packs = [&](int u, int64_t i) {
+      store_stream<NT>(prow + i, vp[u]);
 #pragma unroll
-    for (int u = 0; u < U; ++u) {
-      const int64_t i = int64_t(u) * NTH + threadIdx.x;
-      if (i < packs_left) store_packs(u, i);
+      for (int b = 0; b < NS; ++b) {
+        srow[b].store(i, vs[b][u]);
+      }
+    };
+    const auto compute = [&](const typename P::Rep& rp, bool maximize)
+                             __attribute__((always_inline)) {
+#pragma unroll
+      for (int u = 0; u < U; ++u) {
+        const int64_t i = int64_t(u) * NTH + threadIdx.x;
+        if (i < packs_left) {
+          Pack<S, KP> st[SS];
+#pragma unroll
+          for (int b = 0; b < NS; ++b) st[b] = vs[b][u];
+          apply_pack<P, KP>(vp[u], vg[u], st, load_state, rp, maximize);
+#pragma unroll
+          for (int b = 0; b < NS; ++b) vs[b][u] = st[b];
+          if constexpr (!P::kLateStores) store_packs(u, i);
+        }
+      }
+    };
+    // The replica's weight decay and `maximize` are uniform over the workgroup:
+    // branch on them once instead of evaluating the decay term per element and
+    // selecting (what the compiler makes of the per-element test). The common
+    // case, neither, runs the math with both as constants.
+    if (!a.maximize && !P::decays(rep)) {
+      typename P::Rep plain = rep;
+      P::drop_decay(plain);
+      with_variant<P>(plain, [&](const typename P::Rep& rp) { compute(rp, false); });
+    } else {
+      with_variant<P>(rep, [&](const typename P::Rep& rp) {
+        with_maximize<P>(a.maximize, [&](bool mx) { compute(rp, mx); });
+      });
     }
-  }
+    if constexpr (P::kLateStores) {
+#pragma unroll
+      for (int u = 0; u < U; ++u) {
+        const int64_t i = int64_t(u) * NTH + threadIdx.x;
+        if (i < packs_left) store_packs(u, i);
+      }
+    }
 
-  // The row's head before its first 256-byte boundary (tile 0) and its fewer
-  // than KP tail elements (last tile), one element per access.
-  const auto one = [&](int64_t j) {
-    T pe = pbase[j];
-    S st[SS];
-    if (load_state) {
+    if constexpr (decltype(head_tile)::value) {
+      // The elements before the row's first pack boundary and its fewer than
+      // KP tail elements, one element per access.
+      const auto one = [&](int64_t j) {
+        T pe = pbase[j];
+        S st[SS];
+        if (load_state) {
 #pragma unroll
-      for (int b = 0; b < NS; ++b) st[b] = sbase[b][j];
+          for (int b = 0; b < NS; ++b) st[b] = sbase[b][j];
+        }
+        apply_element<P>(pe, gbase[j], st, load_state, rep, a.maximize);
+        pbase[j] = pe;
+#pragma unroll
+        for (int b = 0; b < NS; ++b) sbase[b][j] = st[b];
+      };
+      for (int64_t j = threadIdx.x; j < pre; j += NTH) one(j);
+      for (int64_t j = body_end + threadIdx.x; j < width; j += NTH) one(j);
     }
-    apply_element<P>(pe, gbase[j], st, load_state, rep, a.maximize);
-    pbase[j] = pe;
-#pragma unroll
-    for (int b = 0; b < NS; ++b) sbase[b][j] = st[b];
   };
-  if (t0 == 0) {
-    for (int64_t j = threadIdx.x; j < head; j += NTH) one(j);
+
+  if (t0 != 0) {
+    const int64_t packs_left = (width - head) / KP - (t0 - kStreamTile) / KP;
+    if (packs_left > 0) {
+      run(std::false_type{}, head + (t0 - kStreamTile), packs_left, 0, width);
+    }
+    return;
   }
-  if (t0 + kStreamTile >= width) {
-    for (int64_t j = head + packs_row * KP + threadIdx.x; j < width; j += NTH) one(j);
+  const int64_t pre = imin(head, (KP - phase % KP) % KP);
+  const int64_t head_packs = (head - pre) / KP;
+  const int64_t body_end =
+      head < width ? head + (width - head) / KP * KP : pre + head_packs * KP;
+  if (head_packs > 0 || pre > 0 || body_end < width) {
+    run(std::true_type{}, pre, head_packs, pre, body_end);
   }
 }
 
@@ -1325,7 +1384,7 @@ struct Segments {
 template <typename P>
 struct SegArgs {
   KArgs<P> k;  // k.x.data[1]: consolidated gradient to write, or null;
-               // k.g.res0 / rmod: the params rows' 256-byte phase
+               // k.g.res0 / rmod: the params rows' phase
   Segments<typename P::T> seg;
 };
 
@@ -1646,12 +1705,12 @@ bool fill_operands(const ts_rt_buf* bufs, int n, Operands<T>& x, bool grad_optio
 }
 
 // The streaming drivers take any operands with unit inner stride and
-// element-aligned bases. The walk follows the parameters' 256-byte boundaries
-// (res0 / rmod: their phase modulo 256 bytes, for the grid); operands at
-// another phase use element-aligned packs.
+// element-aligned bases. The walk follows the parameters' boundaries (res0 /
+// rmod: their phase modulo kPhaseBytes, for the grid); operands at another
+// phase use element-aligned packs.
 template <typename P>
 bool rows_streamable(const Operands<typename P::T>& x, int n, uint32_t& res0, uint32_t& rmod) {
-  constexpr uint32_t A = align_elems<typename P::T>();
+  constexpr uint32_t A = phase_elems<typename P::T>();
   for (int b = 0; b < n; ++b) {
     if (x.data[b] == nullptr) continue;
     const size_t elem = b < 2 ? sizeof(typename P::T) : sizeof(typename P::S);
@@ -1733,15 +1792,21 @@ bool col_lines_private(const Operands<typename P::T>& x, int n, const ColGrid& g
   return true;
 }
 
-inline bool make_grid(int64_t R, int64_t T, int64_t tile, Grid& g, uint32_t& blocks) {
-  const int64_t tiles = (T + tile - 1) / tile;
+// The (replica, tile) grid of a row driver. With head_tiles (the streaming
+// driver) every row also gets its tile 0, the first R workgroups; its
+// ceil(T / tile) other tiles cover [head, head + ceil(T / tile) * tile) ⊇
+// [head, T), the last of them empty where the head and the tail fit in one.
+inline bool make_grid(int64_t R, int64_t T, int64_t tile, Grid& g, uint32_t& blocks,
+                      bool head_tiles = false) {
+  const int64_t tiles = (T + tile - 1) / tile + (head_tiles ? 1 : 0);
   if (R <= 0 || T <= 0 || tiles > INT32_MAX || R > INT32_MAX / tiles) {
     return false;
   }
   g.T = T;
-  g.tiles_per_row = static_cast<uint32_t>(tiles);
+  g.tiles_per_row = static_cast<uint32_t>(head_tiles ? tiles - 1 : tiles);
   g.res0 = 0;
   g.rmod = 0;
+  g.heads = head_tiles ? static_cast<uint32_t>(R) : 0u;
   blocks = static_cast<uint32_t>(R * tiles);
   return true;
 }
@@ -2017,7 +2082,8 @@ int launch_dense(const Call& c, int nbufs) {
                          : small     ? stream_tile<P, false, true>()
                          : pre       ? stream_tile<P, true, false>()
                                      : stream_tile<P, false, false>();
-    if (!make_grid(c.R, c.T, tile, a.g, blocks)) return false;
+    // The streaming driver adds each row's tile 0 (its head and tail).
+    if (!make_grid(c.R, c.T, tile, a.g, blocks, streamable)) return false;
     a.g.res0 = res0;
     a.g.rmod = rmod;
     return true;
@@ -2087,7 +2153,7 @@ int launch_segments(const Call& c, int nbufs, const ts_segment* segs, int n_segs
     if (!fill_kargs<P>(c, nbufs, a.k, true) || !segments_valid(segs, n_segs, c.T)) {
       return false;
     }
-    a.k.g = Grid{c.T, 0, 0, 0};
+    a.k.g = Grid{c.T, 0, 0, 0, 0};
     vec_rows = rows_streamable<P>(a.k.x, nbufs, a.k.g.res0, a.k.g.rmod);
     return walk_fits<T>(walk, c.R, tile, vec_rows, a.seg);
   };

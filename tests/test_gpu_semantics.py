@@ -358,6 +358,61 @@ def test_misaligned_row_views_other_dtypes_bit_exact(dtype, offset):
         assert torch.equal(view[i], dense[i]), i
 
 
+@pytest.mark.parametrize("T", [3, 700, 1024, 1029, 4100])
+@pytest.mark.parametrize("offset", [0, 1, 255, 256, 1021, 1024, 2047, 3071, 4095])
+def test_views_at_every_tile_phase_match_oracle(offset, T):
+    """The streaming driver's tiles start on the row's boundaries of the tile
+    size (up to 4096 float32 elements); a head tile per row takes what lies
+    before the first one. Column views at offsets across that whole range,
+    rows whose widths are below, at and above a tile, with the row stride
+    moving every row to another phase: each element against the oracle."""
+    R = 4
+    big = adam_args(R, offset + T + 37, amsgrad=True, seed=offset * 7 + T)
+    view = [t[:, offset:offset + T] if t is not None and t.dim() == 2 else t for t in big]
+    mask = torch.tensor([True, True, False, True], device=DEV)
+    host = [t.contiguous().cpu().numpy().copy() if t is not None else None for t in view]
+    kw = dict(amsgrad=True, maximize=False, decoupled_weight_decay=True)
+    K.adam_step_(*view, mask, **kw)
+    torch.cuda.synchronize()
+    O.adam_step(O.DEVICE, *host[:11], mask.cpu().numpy(), **kw)
+    for i in (0, 2, 3, 4, 5):
+        got = view[i].contiguous().cpu().numpy()
+        assert np.array_equal(got.view(np.uint32), host[i].view(np.uint32)), i
+    untouched = big[0][:, :offset], big[0][:, offset + T:]
+    ref = adam_args(R, offset + T + 37, amsgrad=True, seed=offset * 7 + T)[0]
+    assert torch.equal(untouched[0], ref[:, :offset])
+    assert torch.equal(untouched[1], ref[:, offset + T:])
+
+
+@pytest.mark.parametrize("offset", [0, 3, 511, 4099, 8191])
+def test_bf16_views_at_every_tile_phase_bit_exact_to_aten(offset):
+    """As above for bfloat16 parameters (8 elements per pack, tiles of up to
+    8192 elements), against torch's fused Adam on each active row, with
+    hyperparameters exact in 16 bits."""
+    R, T = 3, 5000
+    dtype = torch.bfloat16
+    g = torch.Generator(device=DEV).manual_seed(offset)
+    W = offset + T + 13
+    rnd = lambda: torch.randn(R, W, device=DEV, generator=g).to(dtype)  # noqa: E731
+    big = [rnd(), rnd(), rnd().abs(), rnd().abs()]
+    p, gr, m, v = (t[:, offset:offset + T] for t in big)
+    lr, b1, b2, eps, wd = 2.0**-7, 0.875, 1 - 2.0**-7, 2.0**-14, 2.0**-6
+    mask = torch.tensor([True, False, True], device=DEV)
+    ref = [[t[r].clone() for t in (p, m, v)] for r in range(R)]
+    steps = torch.zeros(R, device=DEV, dtype=dtype)
+    for r in (0, 2):
+        torch._fused_adam_([ref[r][0]], [gr[r].clone()], [ref[r][1]], [ref[r][2]], [],
+                           [torch.tensor(1.0, device=DEV)], lr=lr, beta1=b1, beta2=b2,
+                           weight_decay=wd, eps=eps, amsgrad=False, maximize=False,
+                           grad_scale=None, found_inf=None)
+    K.adam_step_(p, gr, m, v, None, steps, *(full(R, x, dtype) for x in (lr, b1, b2, eps, wd)),
+                 mask, amsgrad=False, maximize=False, decoupled_weight_decay=False)
+    torch.cuda.synchronize()
+    for r in range(R):
+        for got, want in zip((p[r], m[r], v[r]), ref[r]):
+            assert torch.equal(got, want), r
+
+
 @pytest.mark.parametrize("op", ["sgd", "adagrad", "adam-bf16"])
 def test_ragged_rows_other_policies_bit_exact(op):
     """Rows of width T = 4k + 3 in one contiguous (R, T) allocation (every row
