@@ -94,11 +94,13 @@ constexpr int kPer = kPack * kUnroll;  // elements per thread per tile
 constexpr int64_t kTile = int64_t(kThreads) * kPer;
 constexpr int kStreamThreads = 64;
 
-// Tile boundaries sit on 256-byte boundaries of the (R, T) rows. Consecutive
-// tiles run on different XCDs (each with its own L2); a 128-byte line split
-// between two of them is fetched twice and written back as two partial lines.
-// Measured on the MI355X with the same buffers viewed 16 / 64 / 128 / 0 bytes
-// off a 256-byte boundary: the Adam step took 19% / 8% / 1% / 0% longer.
+// Tile boundaries sit on 256-byte boundaries of the (R, T) rows (the
+// streaming driver's on boundaries of its own tile size, a multiple of 256
+// bytes). Consecutive tiles run on different XCDs (each with its own L2); a
+// 128-byte line split between two of them is fetched twice and written back
+// as two partial lines. Measured on the MI355X with the same buffers viewed
+// 16 / 64 / 128 / 0 bytes off a 256-byte boundary: the Adam step took
+// 19% / 8% / 1% / 0% longer.
 constexpr uint32_t kAlignBytes = 256;
 template <typename T>
 constexpr uint32_t align_elems() {

@@ -2,8 +2,8 @@
 buffers.
 
 The drivers pick their access pattern from the operands' strides and
-alignment (streaming rows with a per-row head before the first 256-byte
-boundary, replica-minor columns, element-wise otherwise; per-parameter
+alignment (streaming rows with a per-row head tile before the first boundary
+of the tile size, replica-minor columns, element-wise otherwise; per-parameter
 gradients at any column offset). Every choice must give the bits the
 contiguous layout gives, since all drivers share one element update. These
 cases draw the layout at random -- row width, column offset inside a wider

@@ -343,8 +343,8 @@ def test_misaligned_row_views_bit_exact(offset, extra, T):
 @pytest.mark.parametrize("dtype", [torch.float64, torch.float16, torch.bfloat16])
 @pytest.mark.parametrize("offset", [1, 6, 31, 127])
 def test_misaligned_row_views_other_dtypes_bit_exact(dtype, offset):
-    """As above for the other parameter types (256 bytes = 32 / 128 elements):
-    heads of up to 127 elements per row."""
+    """As above for the other parameter types: rows start at offsets of up to
+    127 elements from a 256-byte boundary."""
     R, T = 5, 1500
     big = adam_args(R, T + offset + 3, seed=offset, dtype=dtype)
     view = [t[:, offset:offset + T] if t is not None and t.dim() == 2 else t for t in big]
