@@ -1755,6 +1755,14 @@ bool replica_minor(const Operands<T>& x, int n) {
   return true;
 }
 
+// Whether a 1-D grid of `blocks` workgroups of `threads` threads can launch:
+// at most INT32_MAX workgroups, and at most 2^32 - 1 work-items (the dispatch
+// packet counts work-items in 32 bits; HIP refuses a larger launch, which would
+// leave a call's preparation launch run and its update not).
+inline bool grid_fits(uint64_t blocks, int threads) {
+  return blocks <= INT32_MAX && blocks * static_cast<uint64_t>(threads) <= UINT32_MAX;
+}
+
 inline bool make_col_grid(int64_t R, int64_t T, ColGrid& g, uint32_t& blocks) {
   if (R <= 1 || R > INT32_MAX || T <= 0) return false;
   g.R = R;
@@ -1771,7 +1779,10 @@ inline bool make_col_grid(int64_t R, int64_t T, ColGrid& g, uint32_t& blocks) {
   const int64_t n_rblocks = (R + g.rb - 1) / g.rb;
   const int64_t cols_per_block = int64_t(g.cpi) * kColIters;
   const int64_t n_cblocks = (T + cols_per_block - 1) / cols_per_block;
-  if (n_rblocks > INT32_MAX / n_cblocks) return false;
+  if (n_rblocks > INT32_MAX / n_cblocks ||
+      !grid_fits(static_cast<uint64_t>(n_rblocks * n_cblocks), g.threads)) {
+    return false;  // the element driver takes it
+  }
   g.n_rblocks = static_cast<uint32_t>(n_rblocks);
   blocks = static_cast<uint32_t>(n_rblocks * n_cblocks);
   return true;
@@ -1794,14 +1805,16 @@ bool col_lines_private(const Operands<typename P::T>& x, int n, const ColGrid& g
   return true;
 }
 
-// The (replica, tile) grid of a row driver. With head_tiles (the streaming
-// driver) every row also gets its tile 0, the first R workgroups; its
-// ceil(T / tile) other tiles cover [head, head + ceil(T / tile) * tile) ⊇
-// [head, T), the last of them empty where the head and the tail fit in one.
+// The (replica, tile) grid of a row driver, in `threads`-thread workgroups.
+// With head_tiles (the streaming driver) every row also gets its tile 0, the
+// first R workgroups; its ceil(T / tile) other tiles cover
+// [head, head + ceil(T / tile) * tile) ⊇ [head, T), the last of them empty
+// where the head and the tail fit in one.
 inline bool make_grid(int64_t R, int64_t T, int64_t tile, Grid& g, uint32_t& blocks,
-                      bool head_tiles = false) {
+                      int threads, bool head_tiles = false) {
   const int64_t tiles = (T + tile - 1) / tile + (head_tiles ? 1 : 0);
-  if (R <= 0 || T <= 0 || tiles > INT32_MAX || R > INT32_MAX / tiles) {
+  if (R <= 0 || T <= 0 || tiles > INT32_MAX || R > INT32_MAX / tiles ||
+      !grid_fits(static_cast<uint64_t>(R) * static_cast<uint64_t>(tiles), threads)) {
     return false;
   }
   g.T = T;
@@ -1869,9 +1882,11 @@ struct SegmentWalk {
 
 // Fills the next launch's table, up to kMaxSegments entries, from the walk;
 // returns the grid size (0 when the walk is done, -1 when it exceeds the 1-D
-// grid). `vec_rows` says whether the (R, T) operands allow vector access.
+// grid of `threads`-thread workgroups). `vec_rows` says whether the (R, T)
+// operands allow vector access.
 template <typename T>
-int64_t next_chunk(SegmentWalk& w, int64_t R, int64_t tile, bool vec_rows, Segments<T>& out) {
+int64_t next_chunk(SegmentWalk& w, int64_t R, int64_t tile, bool vec_rows, Segments<T>& out,
+                   int threads) {
   out.n = 0;
   out.vec_ok = 0;
   uint64_t tiles = 0;
@@ -1890,14 +1905,15 @@ int64_t next_chunk(SegmentWalk& w, int64_t R, int64_t tile, bool vec_rows, Segme
   }
   out.tile0[out.n] = static_cast<uint32_t>(tiles);
   const uint64_t blocks = tiles * static_cast<uint64_t>(R);
-  return blocks > INT32_MAX ? -1 : static_cast<int64_t>(blocks);
+  return grid_fits(blocks, threads) ? static_cast<int64_t>(blocks) : -1;
 }
 
 // Checks that every launch of a walk fits the grid, without launching.
 template <typename T>
-bool walk_fits(SegmentWalk w, int64_t R, int64_t tile, bool vec_rows, Segments<T>& scratch) {
+bool walk_fits(SegmentWalk w, int64_t R, int64_t tile, bool vec_rows, Segments<T>& scratch,
+               int threads = kThreads) {
   int64_t blocks;
-  while ((blocks = next_chunk<T>(w, R, tile, vec_rows, scratch)) != 0 || scratch.n > 0) {
+  while ((blocks = next_chunk<T>(w, R, tile, vec_rows, scratch, threads)) != 0 || scratch.n > 0) {
     if (blocks < 0) return false;
   }
   return true;
@@ -1908,7 +1924,7 @@ template <typename T, typename Args, typename Kernel>
 int launch_walk(SegmentWalk w, int64_t R, int64_t tile, bool vec_rows, Args& a, Segments<T>& seg,
                 Kernel kernel, hipStream_t stream, uint32_t lds = 0, int threads = kThreads) {
   int64_t blocks;
-  while ((blocks = next_chunk<T>(w, R, tile, vec_rows, seg)) != 0 || seg.n > 0) {
+  while ((blocks = next_chunk<T>(w, R, tile, vec_rows, seg, threads)) != 0 || seg.n > 0) {
     if (blocks < 0) return kInvalid;
     if (blocks == 0) continue;
     hipLaunchKernelGGL(kernel, dim3(static_cast<uint32_t>(blocks)), dim3(threads), lds, stream,
@@ -2084,8 +2100,11 @@ int launch_dense(const Call& c, int nbufs) {
                          : small     ? stream_tile<P, false, true>()
                          : pre       ? stream_tile<P, true, false>()
                                      : stream_tile<P, false, false>();
+    const int threads = !streamable ? kThreads
+                        : small     ? stream_threads<P, true>()
+                                    : stream_threads<P, false>();
     // The streaming driver adds each row's tile 0 (its head and tail).
-    if (!make_grid(c.R, c.T, tile, a.g, blocks, streamable)) return false;
+    if (!make_grid(c.R, c.T, tile, a.g, blocks, threads, streamable)) return false;
     a.g.res0 = res0;
     a.g.rmod = rmod;
     return true;
@@ -2157,7 +2176,8 @@ int launch_segments(const Call& c, int nbufs, const ts_segment* segs, int n_segs
     }
     a.k.g = Grid{c.T, 0, 0, 0, 0};
     vec_rows = rows_streamable<P>(a.k.x, nbufs, a.k.g.res0, a.k.g.rmod);
-    return walk_fits<T>(walk, c.R, tile, vec_rows, a.seg);
+    const int nth = pre ? segment_threads<P, true>() : segment_threads<P, false>();
+    return walk_fits<T>(walk, c.R, tile, vec_rows, a.seg, nth);
   };
   return run_step<P>(c, a.k.vec, prepare, [&]() -> int {
     const bool same_phase = rows_same_phase<P>(a.k.x, nbufs);

@@ -110,6 +110,33 @@ def test_workspace_size_and_bad_workspaces_rejected_before_any_launch():
                                     ctypes.c_int64(65537), T, flags, None, None) == 1
 
 
+def test_grids_past_the_dispatch_limit_rejected_before_any_launch():
+    """A launch counts its work-items in 32 bits, and HIP refuses a larger one.
+    A call whose update grid would pass 2^32 - 1 work-items is an invalid
+    argument before anything is enqueued (otherwise its preparation launch
+    would bump the steps and the update would not run). 16 rows of 2^32
+    float32 elements: 2^28 one-wavefront streaming tiles of 256 elements."""
+    lib = ctypes.CDLL(str(LIB))
+    R, T = 16, 2**32
+    fake = ctypes.c_void_p(0x10000)
+    bufs = (RTBuf * 5)(*[RTBuf(0x10000 * (i + 1), T, 1) for i in range(5)])
+    ws = ctypes.c_void_p(0x80000)
+    flags = ctypes.c_uint32(0x10)
+    i64, sz = ctypes.c_int64, ctypes.c_size_t
+    assert lib.ts_adam_step(bufs, 0, fake, fake, fake, fake, fake, fake, fake, i64(R), i64(T),
+                            flags, None, None) == 1
+    assert lib.ts_adam_step_ws(bufs, 0, fake, fake, fake, fake, fake, fake, fake, i64(R),
+                               i64(T), flags, None, ws, sz(16 * R), None) == 1
+    assert lib.ts_adagrad_step_ws(bufs, 0, fake, fake, fake, fake, fake, fake, i64(R), i64(T),
+                                  flags, None, ws, sz(16 * R), None) == 1
+    assert lib.ts_sgd_step(bufs, 0, fake, fake, fake, fake, fake, fake, i64(R), i64(T), flags,
+                           None, None) == 1
+    seg = (Segment * 1)(Segment(0x90000, T, 0, T))
+    assert lib.ts_adam_step_segments(bufs, seg, 1, 0, fake, fake, fake, fake, fake, fake, fake,
+                                     i64(R), i64(T), flags, None, None) == 1
+    assert lib.ts_scatter_segments(seg, 1, 0, fake, i64(T), i64(T), i64(R), None) == 1
+
+
 class Segment(ctypes.Structure):
     _fields_ = [("data", ctypes.c_void_p), ("stride_r", ctypes.c_int64),
                 ("col", ctypes.c_int64), ("numel", ctypes.c_int64)]
