@@ -362,7 +362,9 @@ constexpr int64_t kMallBytes = int64_t(256) << 20;
 // 75% active; three runs on two boxes): float32 Adam at cap 20 5.85-5.94 TB/s
 // against 5.66-5.74 at its cap of 14, and with amsgrad 5.83-5.91 against
 // 5.73-5.79 at its cap of 12. From 2 GB of operands on (R = 128, T = 1M to
-// 8M) the large-launch caps were best or within 0.3%.
+// 8M) the large-launch caps were best or within 0.3%. (With the active flag
+// read through the scalar cache the mid-size caps moved to 14, 12 with
+// amsgrad; see the policies.)
 constexpr int64_t kMidBytes = int64_t(1) << 30;
 
 // Packs per thread of the streaming driver, by operand types: float32
@@ -460,6 +462,36 @@ constexpr int stream_unroll(int fp32, int bf16_state, int narrow, int wide) {
 // each shape in 2-3 processes): float16 Adam moved to one pack under a cap
 // of 20 and bfloat16 SGD to two packs under a cap of 20 (at the policies);
 // float16 SGD and 16-bit Adagrad kept their shapes.
+// Retuned with the active flag read through the scalar cache (kScalarMask):
+// a workgroup then issues its loads sooner, and the best caps moved down.
+// Sweep per policy (packs 1/2/4 x caps 8-24 and uncapped, both flag reads,
+// config-5 buffers unless noted, 3 interleaved rounds, mean GB/s; old shape
+// with the vector read -> new):
+//   Adam                   1 pack, cap 14 -> cap 12: 6432 -> 6601
+//   Adam, mid size         1 pack, cap 20 -> cap 14 (config-2 rows without
+//                          amsgrad): 5876 -> 6118
+//   Adam + amsgrad, mid    1 pack, cap 20 -> cap 12 (config 2): 5905 -> 6054
+//   Adam, no workspace     2 packs, cap 14 -> cap 10: 6266 -> 6340
+//   Adam, bf16 moments     2 packs, cap 12 -> 1 pack, cap 16: 6184 -> 6462
+//   Adam, 16-bit params,   1 pack, uncapped -> 4 packs: half 4559 -> 6258,
+//   no workspace           bfloat16 4555 -> 6097
+//   Adam, bf16 params      1 pack, uncapped -> cap 16: 6136 -> 6237
+//   Adam, half params      1 pack, cap 20 (kept): 6181 -> 6248
+//   Adagrad                1 pack, cap 20 -> cap 14: 6445 -> 6605 (config 4,
+//                          mid size, cap 24 -> 14: 6587)
+//   Adagrad, no workspace  2 packs, cap 16 -> 1 pack: 6347 (cap 14) -> 6524
+//   Adagrad, bf16 state    1 pack, uncapped -> cap 20: 6331 -> 6531
+//   SGD with momentum      1 pack, cap 20 (kept): 6518 -> 6608
+// Adam with amsgrad (large launches) and bfloat16-state SGD stayed within
+// 0.5% either way and kept their shapes. 16-bit SGD and Adagrad ran slower
+// with the scalar read (bfloat16 SGD -5% at its shape) and keep the vector
+// read, as do float64 and the float32-math Adagrad (not swept). Same-process
+// A/B of the whole change against the previous build (6 rounds): config 5
+// +2.7%, config 2 +2.1%, config 3 +1.3% (SGD's MALL-resident launches read
+// it scalar too), config 4 +0.4%, bfloat16 moments +5.1%, Adagrad on the
+// config-5 buffers +2.3%, half / bfloat16 params +2.6% / +0.6%; config 1 is
+// unchanged (Adam's MALL-resident launches keep the vector read: -1.3% with
+// the scalar one).
 
 // Adam / AdamW: h = {lr, beta1, beta2, eps, weight_decay}.
 template <typename T_, bool ADAMW, bool AMSGRAD, typename S_ = T_>
@@ -468,8 +500,8 @@ struct AdamPolicy {
   using S = S_;
   using M = op_t<T>;
   static constexpr int NS = AMSGRAD ? 3 : 2;
-  static constexpr uint32_t kStreamLds = residency_lds<T, S>(AMSGRAD ? 12 : 14);
-  static constexpr int kStreamUnroll = stream_unroll<T, S>(2, 4, 1, 2);
+  static constexpr uint32_t kStreamLds = residency_lds<T, S>(AMSGRAD ? 12 : 10);
+  static constexpr int kStreamUnroll = stream_unroll<T, S>(2, 4, 4, 2);
   // float16 Adam (no amsgrad): one 8-element pack under a cap of 20. Three
   // boxes, config-5 shape: 6.16-6.38 TB/s on synthetic moments and
   // 6.37 on moments that start at zero and underflow (the bench's data),
@@ -477,13 +509,17 @@ struct AdamPolicy {
   // between processes; four packs under a cap of 12 matched it on synthetic
   // moments (6.26-6.40) and lost 1.5% on the zeroed ones.
   static constexpr bool kHalfShape = kHalfAll<T, S> && !AMSGRAD;
+  static constexpr bool kBf16ParamShape =
+      std::is_same<T, bf16_t>::value && std::is_same<S, bf16_t>::value && !AMSGRAD;
   static constexpr uint32_t kStreamLdsPre =
-      kBf16State<T, S> ? lds_for_residency(12)
-      : kHalfShape     ? lds_for_residency(20)
-                       : kStreamLds;
+      kBf16State<T, S>  ? lds_for_residency(16)
+      : kHalfShape      ? lds_for_residency(20)
+      : kBf16ParamShape ? lds_for_residency(16)
+                        : residency_lds<T, S>(12);
   static constexpr uint32_t kStreamLdsMid =
-      kFp32State<T, S> ? lds_for_residency(20) : kStreamLdsPre;
-  static constexpr int kStreamUnrollPre = stream_unroll<T, S>(1, 2, 1, 2);
+      kFp32State<T, S> ? lds_for_residency(AMSGRAD ? 12 : 14) : kStreamLdsPre;
+  static constexpr int kStreamUnrollPre = stream_unroll<T, S>(1, 1, 1, 2);
+  static constexpr bool kScalarMask = !std::is_same<T, double>::value;
   static constexpr int kStreamUnrollSmall = stream_unroll<T, S>(2, 4, 4, 2);
   static constexpr int64_t kStreamSmallBytes = kMallBytes;
   static constexpr int kStreamPack = stream_pack<T, S>();
@@ -560,6 +596,8 @@ struct SgdPolicy {
   static constexpr uint32_t kStreamLdsMid = kStreamLdsPre;
   static constexpr int kStreamUnrollPre = kStreamUnroll;
   static constexpr int kStreamUnrollSmall = stream_unroll<T, S>(1, 1, 4, 2);
+  static constexpr bool kScalarMask = HAS_BUF && std::is_same<T, float>::value;
+  static constexpr bool kScalarMaskSmall = kScalarMask;
   // float32 launches that fit the MALL: two-wavefront workgroups. Config 3's
   // shape (32 x 545100, 80% active), two calls, 2-3 processes: 6.87-6.91
   // TB/s against 6.77-6.79 for one wavefront (256 threads: 6.88-6.93).
@@ -609,12 +647,12 @@ struct AdagradPolicy {
   using M = op_t<T>;
   static constexpr int NS = 1;
   static constexpr uint32_t kStreamLds = residency_lds<T, S>(16);
-  static constexpr int kStreamUnroll = stream_unroll<T, S>(2, 1, 1, 2);
-  static constexpr uint32_t kStreamLdsPre = residency_lds<T, S>(20);
-  // Mid-size launches (config 4's 419 MB): cap 24, 6.37-6.39 TB/s against
-  // 6.28-6.30 at 20 (four processes, two calls).
-  static constexpr uint32_t kStreamLdsMid = residency_lds<T, S>(24);
+  static constexpr int kStreamUnroll = stream_unroll<T, S>(1, 1, 1, 2);
+  static constexpr uint32_t kStreamLdsPre =
+      kBf16State<T, S> ? lds_for_residency(20) : residency_lds<T, S>(14);
+  static constexpr uint32_t kStreamLdsMid = kStreamLdsPre;
   static constexpr int kStreamUnrollPre = stream_unroll<T, S>(1, 1, 4, 2);
+  static constexpr bool kScalarMask = std::is_same<T, float>::value;
   static constexpr int kStreamUnrollSmall = stream_unroll<T, S>(2, 1, 4, 2);
   static constexpr int64_t kStreamSmallBytes = kMallBytes;
   static constexpr int kStreamPack = stream_pack<T, S>();
@@ -724,6 +762,7 @@ struct AdagradF32Policy {
   static constexpr uint32_t kStreamLdsPre = residency_lds<T, S>(20);
   static constexpr uint32_t kStreamLdsMid = kStreamLdsPre;
   static constexpr int kStreamUnrollPre = stream_unroll<T, S>(1, 1, 1, 2);
+  static constexpr bool kScalarMask = false;
   static constexpr int kStreamUnrollSmall = stream_unroll<T, S>(2, 1, 4, 2);
   static constexpr int64_t kStreamSmallBytes = kMallBytes;
   static constexpr int kStreamPack = stream_pack<T, S>();
@@ -804,6 +843,46 @@ struct stream_block_small_of<P, std::void_t<decltype(P::kStreamBlockSmall)>> {
 template <typename P, bool SMALL>
 constexpr int stream_threads() {
   return SMALL ? stream_block_small_of<P>::value : stream_block_of<P>::value;
+}
+
+// How a streaming workgroup reads its replica's active flag: through the
+// scalar cache (mask_byte_scalar) or with a vector load. The scalar read skips
+// the vector memory pipeline, which the streaming loads keep queued, so a
+// workgroup starts its loads sooner and a frozen replica's workgroup exits
+// sooner; the residency caps below are tuned with it. By default launches
+// beyond the MALL read it scalar and SMALL ones as a vector load
+// (kScalarMask / kScalarMaskSmall override).
+template <typename P, typename = void>
+struct scalar_mask_of {
+  static constexpr bool value = true;
+};
+template <typename P>
+struct scalar_mask_of<P, std::void_t<decltype(P::kScalarMask)>> {
+  static constexpr bool value = P::kScalarMask;
+};
+template <typename P, typename = void>
+struct scalar_mask_small_of {
+  static constexpr bool value = false;
+};
+template <typename P>
+struct scalar_mask_small_of<P, std::void_t<decltype(P::kScalarMaskSmall)>> {
+  static constexpr bool value = P::kScalarMaskSmall;
+};
+template <typename P, bool SMALL>
+constexpr bool stream_scalar_mask() {
+  return SMALL ? scalar_mask_small_of<P>::value : scalar_mask_of<P>::value;
+}
+
+// Replica r's active flag through the scalar cache: one s_load_dword of the
+// aligned dword that holds byte r (that dword never leaves the page the byte
+// is on), then the byte. The address is uniform over the workgroup. The
+// scalar and vector L1 caches are invalidated between kernel dispatches, so a
+// mask written before the launch is what the load sees.
+__device__ __forceinline__ bool mask_byte_scalar(const uint8_t* mask, uint32_t r) {
+  const uintptr_t at = reinterpret_cast<uintptr_t>(mask) + r;
+  const auto* word =
+      reinterpret_cast<const __attribute__((address_space(4))) uint32_t*>(at & ~uintptr_t(3));
+  return ((*word >> (8 * (at & 3))) & 0xFFu) != 0;
 }
 
 // Elements per streaming tile: the workgroup's threads x the policy's packs
@@ -1009,8 +1088,10 @@ __global__ __launch_bounds__((stream_threads<P, SMALL>())) void stream_kernel(KA
   uint32_t r;
   int64_t t0;
   stream_tile_of_block<kStreamTile>(a.g, r, t0);
-  if (!a.vec.mask[r]) {
-    return;
+  if constexpr (stream_scalar_mask<P, SMALL>()) {
+    if (!mask_byte_scalar(a.vec.mask, r)) return;
+  } else {
+    if (!a.vec.mask[r]) return;
   }
 
   // A row's tiles k >= 1 start at its first kStreamTile-element boundary, so
