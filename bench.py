@@ -696,7 +696,7 @@ def bf16_state_shared_timing(adam_args, launches: int, ceiling: bool = True):
         best, shape, rates = best_traffic(3, (p, gr, mb, vb), mask, 0.0, shapes, per_elem,
                                           launches)
         out["traffic_ceiling"] = {"GBs": best, "shape": shape,
-                                  "update_shape_GBs": rates[(2, 12)],
+                                  "update_shape_GBs": rates[(1, 16)],
                                   "update_of_ceiling": round(gbs / best, 4)}
     torch.cuda.empty_cache()
     return out
@@ -781,7 +781,7 @@ def ceiling_timing(adam_args, launches: int):
     buffers (churten_amd/lib/libchurten_bench.so), each kind at the best of a
     few launch shapes (one-wave workgroups, 1 or 2 packs per thread, residency
     caps): 4 reads + 3 writes, also at the update kernel's own shape (1 pack,
-    14 per CU); the 4 reads alone; the 3 writes alone. `mix_bound` is the rate
+    12 per CU); the 4 reads alone; the 3 writes alone. `mix_bound` is the rate
     a 16 B read + 12 B write element reaches if reads and writes each ran at
     their own best rate, one after the other. Runs last: the write-only passes
     overwrite the buffers."""
@@ -801,7 +801,7 @@ def ceiling_timing(adam_args, launches: int):
     writes, write_shape, _ = best(
         2, 0.0, [(1, 4), (1, 6), (1, 8), (1, 10), (1, 12), (2, 4), (2, 8)], 12)
     out = {"mix_4r3w_GBs": mix, "mix_4r3w_shape": mix_shape,
-           "mix_4r3w_update_shape_GBs": mix_rates[(1, 14)],
+           "mix_4r3w_update_shape_GBs": mix_rates[(1, 12)],
            "read_4_GBs": reads, "read_4_shape": read_shape,
            "write_3_GBs": writes, "write_3_shape": write_shape}
     out["mix_bound_GBs"] = round(28 / (16 / reads + 12 / writes), 1)
