@@ -413,6 +413,58 @@ def test_bf16_views_at_every_tile_phase_bit_exact_to_aten(offset):
             assert torch.equal(got, want), r
 
 
+@pytest.mark.parametrize("large", [False, True], ids=["small", "large"])
+@pytest.mark.parametrize("op", ["adam", "sgd", "adagrad"])
+@pytest.mark.parametrize("offset", [0, 1, 2, 3, 5])
+def test_mask_views_at_every_byte_offset(offset, op, large):
+    """The streaming driver reads a replica's active byte as part of the
+    aligned 4-byte word that holds it (Adam and Adagrad beyond the MALL, SGD
+    with momentum at every size; Adam's MALL-resident shape keeps a vector
+    load). Masks that are views starting 0-3 bytes into such a word, with rows
+    of every residue mod 4, must give each replica its own byte: frozen rows
+    bit-identical, active rows equal to the oracle's."""
+    R = 11
+    bytes_per_elem = 16 if op == "adam" else 12  # params, grads and state, float32
+    T = (300 * 2**20) // (bytes_per_elem * R) // 4 * 4 + 4 if large else 1030
+    g = torch.Generator(device=DEV).manual_seed(offset + 31)
+    rnd = lambda: torch.randn(R, T, device=DEV, generator=g)  # noqa: E731
+    pattern = [True, False, True, True, False, False, True, False, True, True, False]
+    big = torch.zeros(R + 8, dtype=torch.bool, device=DEV)
+    big[offset:offset + R] = torch.tensor(pattern, device=DEV)
+    mask = big[offset:offset + R]
+    assert mask.data_ptr() % 4 == offset % 4
+    if op == "adam":
+        a = [rnd(), rnd(), rnd().abs(), rnd().abs(), None, full(R, 2.0), full(R, 1e-2),
+             full(R, 0.9), full(R, 0.999), full(R, 1e-8), full(R, 1e-2)]
+        kw = dict(amsgrad=False, maximize=False, decoupled_weight_decay=True)
+        state, n_in, run, ref = (0, 2, 3), 11, K.adam_step_, O.adam_step
+    elif op == "sgd":
+        a = [rnd(), rnd(), rnd(), full(R, 3.0), full(R, 1e-2), full(R, 0.9), full(R, 0.1),
+             full(R, 1e-3)]
+        kw = dict(nesterov=True, maximize=False)
+        state, n_in, run, ref = (0, 2), 8, K.sgd_step_, O.sgd_step
+    else:
+        a = [rnd(), rnd(), rnd().abs(), full(R, 2.0), full(R, 1e-2), full(R, 1e-3),
+             full(R, 1e-3), full(R, 1e-10)]
+        kw = dict(maximize=False)
+        state, n_in, run, ref = (0, 2), 8, K.adagrad_step_, O.adagrad_step
+    steps = 5 if op == "adam" else 3
+    rows = [0, 1, 2, 3, 4, 7, 10]
+    host = [t[rows].cpu().numpy().copy() if t is not None else None for t in a]
+    before = [t.clone() if t is not None else None for t in a]
+    run(*a, mask, **kw)
+    torch.cuda.synchronize()
+    ref(O.DEVICE, *host[:n_in], np.array([pattern[r] for r in rows]), **kw)
+    for i in state:
+        for k, r in enumerate(rows):
+            if pattern[r]:
+                got = a[i][r].cpu().numpy()
+                assert np.array_equal(got.view(np.uint32), host[i][k].view(np.uint32)), (i, r)
+            else:
+                assert torch.equal(a[i][r], before[i][r]), (i, r)
+    assert torch.equal(a[steps], before[steps] + mask.float())
+
+
 @pytest.mark.parametrize("op", ["sgd", "adagrad", "adam-bf16"])
 def test_ragged_rows_other_policies_bit_exact(op):
     """Rows of width T = 4k + 3 in one contiguous (R, T) allocation (every row
