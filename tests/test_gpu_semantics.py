@@ -413,6 +413,34 @@ def test_bf16_views_at_every_tile_phase_bit_exact_to_aten(offset):
             assert torch.equal(got, want), r
 
 
+@pytest.mark.parametrize("R,T", [(2500, 300), (2500, 600), (2500, 1100), (2500, 1700),
+                                 (1500, 4100), (700, 110_000)])
+def test_many_rows_land_on_their_own_tiles(R, T):
+    """A streaming workgroup finds its row by dividing its index by the tiles
+    per row (a multiply and shifts with host-computed constants). Many rows and
+    1, 2, 3, 4, 9 and 430 tiles per row (the last a launch beyond the MALL):
+    sampled rows, the first and last included, equal the oracle's, and frozen
+    ones stay bit-identical."""
+    a = adam_args(R, T, seed=R + T)
+    mask = torch.arange(R, device=DEV) % 7 != 3
+    rows = sorted({0, 1, 2, 3, R // 2, R // 2 + 1, R - 2, R - 1, 10, 17})
+    host = [t[rows].cpu().numpy().copy() if t is not None else None for t in a]
+    before = [t[rows].clone() if t is not None else None for t in a]
+    kw = dict(amsgrad=False, maximize=False, decoupled_weight_decay=True)
+    K.adam_step_(*a, mask, **kw)
+    torch.cuda.synchronize()
+    m = mask[rows].cpu().numpy()
+    O.adam_step(O.DEVICE, *host[:11], m, **kw)
+    for i in (0, 2, 3):
+        got = a[i][rows]
+        for k in range(len(rows)):
+            if m[k]:
+                assert np.array_equal(got[k].cpu().numpy().view(np.uint32),
+                                      host[i][k].view(np.uint32)), (i, rows[k])
+            else:
+                assert torch.equal(got[k], before[i][k]), (i, rows[k])
+
+
 @pytest.mark.parametrize("large", [False, True], ids=["small", "large"])
 @pytest.mark.parametrize("op", ["adam", "sgd", "adagrad"])
 @pytest.mark.parametrize("offset", [0, 1, 2, 3, 5])
