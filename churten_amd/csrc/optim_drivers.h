@@ -628,10 +628,12 @@ struct SgdPolicy {
   static constexpr int kStreamUnrollSmall = stream_unroll<T, S>(1, 1, 4, 2);
   static constexpr bool kScalarMask = HAS_BUF && std::is_same<T, float>::value;
   static constexpr bool kScalarMaskSmall = kScalarMask;
-  // float32 launches that fit the MALL: two-wavefront workgroups. Config 3's
-  // shape (32 x 545100, 80% active), two calls, 2-3 processes: 6.87-6.91
-  // TB/s against 6.77-6.79 for one wavefront (256 threads: 6.88-6.93).
-  static constexpr int kStreamBlockSmall = kFp32State<T, S> ? 128 : kStreamThreads;
+  // float32 launches that fit the MALL: four-wavefront workgroups. Config 3's
+  // shape (32 x 545100, 80% active) with the vector flag read, two calls, 2-3
+  // processes: 128 threads 6.87-6.91 TB/s against 6.77-6.79 for one wavefront
+  // and 6.88-6.93 for 256; with the scalar read 256 threads ran 2.2% ahead of
+  // 128 (same-process A/B, 10 rounds).
+  static constexpr int kStreamBlockSmall = kFp32State<T, S> ? 256 : kStreamThreads;
   static constexpr int64_t kStreamSmallBytes = kMallBytes;
   static constexpr int kStreamPack = stream_pack<T, S>();
   static constexpr int kSegmentUnroll = 2;
