@@ -509,7 +509,7 @@ constexpr int stream_unroll(int fp32, int bf16_state, int narrow, int wide) {
 // Adam with amsgrad (large launches) and bfloat16-state SGD stayed within
 // 0.5% either way and kept their shapes. 16-bit SGD and Adagrad ran slower
 // with the scalar read (bfloat16 SGD -5% at its shape) and keep the vector
-// read, as do float64 and the float32-math Adagrad (not swept). Same-process
+// read, as does float64 (not swept). Same-process
 // A/B of the whole change against the previous build (6 rounds): config 5
 // +2.7%, config 2 +2.1%, config 3 +1.3% (SGD's MALL-resident launches read
 // it scalar too), config 4 +0.4%, bfloat16 moments +5.1%, Adagrad on the
@@ -789,12 +789,16 @@ struct AdagradF32Policy {
   using S = S_;
   using M = float;
   static constexpr int NS = 1;
+  // With the scalar flag read, as the fp64-math Adagrad: one pack under cap
+  // 14 with a workspace, one pack under 16 without (same-process A/B against
+  // the vector read at cap 20 / two packs, 6 rounds: config 4 +1.8%, config-5
+  // buffers +1.8%, without a workspace +5.7-7.0%).
   static constexpr uint32_t kStreamLds = residency_lds<T, S>(16);
-  static constexpr int kStreamUnroll = stream_unroll<T, S>(2, 1, 1, 2);
-  static constexpr uint32_t kStreamLdsPre = residency_lds<T, S>(20);
+  static constexpr int kStreamUnroll = stream_unroll<T, S>(1, 1, 1, 2);
+  static constexpr uint32_t kStreamLdsPre = residency_lds<T, S>(14);
   static constexpr uint32_t kStreamLdsMid = kStreamLdsPre;
   static constexpr int kStreamUnrollPre = stream_unroll<T, S>(1, 1, 1, 2);
-  static constexpr bool kScalarMask = false;
+  static constexpr bool kScalarMask = std::is_same<T, float>::value;
   static constexpr int kStreamUnrollSmall = stream_unroll<T, S>(2, 1, 4, 2);
   static constexpr int64_t kStreamSmallBytes = kMallBytes;
   static constexpr int kStreamPack = stream_pack<T, S>();
