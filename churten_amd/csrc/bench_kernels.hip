@@ -9,6 +9,8 @@
 // an array, for the test that checks it against torch's. cb_div_bc2s: Adam's sqrt(v) /
 // bias_correction2_sqrt as the float update computes it (a multiply by the
 // divisor's double reciprocal), for the tests that check it against a true
+// division. cb_div_tiles: the streaming driver's division of a workgroup
+// index by the tiles per row, for the test that checks it against integer
 // division.
 //
 // Same decomposition as the streaming driver at float32: one-wave workgroups,
@@ -31,6 +33,7 @@
 
 #include <stdint.h>
 
+#include "optim_drivers.h"
 #include "optim_math.h"
 
 namespace {
@@ -171,6 +174,12 @@ __global__ __launch_bounds__(256) void div_bc2s_kernel(const float* x, const flo
   }
 }
 
+__global__ __launch_bounds__(256) void div_tiles_kernel(churten::Grid g, const uint32_t* m,
+                                                        uint32_t* q, int64_t n) {
+  const int64_t i = int64_t(blockIdx.x) * 256 + threadIdx.x;
+  if (i < n) q[i] = churten::div_tiles(g, m[i]);
+}
+
 __global__ __launch_bounds__(256) void narrow_f16_kernel(const float* in, uint16_t* out,
                                                          int64_t n) {
   const int64_t i = int64_t(blockIdx.x) * 256 + threadIdx.x;
@@ -178,6 +187,20 @@ __global__ __launch_bounds__(256) void narrow_f16_kernel(const float* in, uint16
 }
 
 }  // namespace
+
+// q[i] = m[i] / d as the streaming driver divides a workgroup index by the
+// tiles per row (the constants from set_div_tiles, the quotient from
+// div_tiles). Returns 0, 1 on bad arguments, or the HIP error code.
+extern "C" int cb_div_tiles(uint32_t d, const uint32_t* m, uint32_t* q, int64_t n,
+                            hipStream_t stream) {
+  if (d == 0 || n <= 0 || n > int64_t(UINT32_MAX) * 256) return 1;
+  churten::Grid g{};
+  g.tiles_per_row = d;
+  churten::set_div_tiles(g);
+  const uint32_t blocks = static_cast<uint32_t>((n + 255) / 256);
+  hipLaunchKernelGGL(div_tiles_kernel, dim3(blocks), dim3(256), 0, stream, g, m, q, n);
+  return static_cast<int>(hipGetLastError());
+}
 
 // out[i] = the half bits the update kernels store for the float in[i].
 extern "C" int cb_narrow_f16(const float* in, uint16_t* out, int64_t n, hipStream_t stream) {

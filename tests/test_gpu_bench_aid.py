@@ -88,3 +88,35 @@ def test_traffic_rejects_bad_arguments():
     assert call(lib, 0, ts, mask, 0.0, sink, T=6) == 1            # T not a multiple of 4
     odd = [t.view(-1)[1:9].view(1, 8) for t in ts]               # 4-byte aligned only
     assert call(lib, 0, odd, mask, 0.0, sink, R=1) == 1
+
+
+DIVISORS = [1, 2, 3, 5, 7, 64, 255, 256, 257, 430, 1037, 4099, 98_328, 8_388_625,
+            2**20 - 1, 2**24 + 1, 2**31 - 1, 2**31, 2**31 + 1, 2**32 - 1]
+
+
+@pytest.mark.parametrize("d", DIVISORS)
+def test_div_tiles_is_integer_division(d):
+    """The streaming driver finds a workgroup's row as index / tiles-per-row
+    with a multiply and shifts (Granlund-Montgomery constants set on the host).
+    Against integer division: 2^20 random 32-bit indices plus the edges (0,
+    d - 1, d, d + 1, multiples of d and their neighbours, 2^32 - 1)."""
+    lib = ctypes.CDLL(str(LIB))
+    g = torch.Generator().manual_seed(d % 1_000_003)
+    rnd = torch.randint(0, 2**32, (1 << 20,), generator=g, dtype=torch.int64)
+    edges = [0, 1, d - 1, d, d + 1, 2 * d - 1, 2 * d, 2**32 - 1, 2**32 - 2, 2**31, 2**31 - 1]
+    k = (2**32 - 1) // d
+    edges += [k * d, k * d - 1, (k // 2) * d, (k // 2) * d - 1, (k // 2) * d + 1]
+    m = torch.cat([rnd, torch.tensor([e % 2**32 for e in edges], dtype=torch.int64)])
+    dev_m = m.to(torch.uint32).cuda()
+    q = torch.empty_like(dev_m)
+    assert lib.cb_div_tiles(ctypes.c_uint32(d), ctypes.c_void_p(dev_m.data_ptr()),
+                            ctypes.c_void_p(q.data_ptr()), ctypes.c_int64(m.numel()),
+                            None) == 0
+    torch.cuda.synchronize()
+    got = q.cpu().view(torch.int32).to(torch.int64) & 0xFFFFFFFF
+    assert torch.equal(got, m // d)
+
+
+def test_div_tiles_rejects_a_zero_divisor():
+    lib = ctypes.CDLL(str(LIB))
+    assert lib.cb_div_tiles(ctypes.c_uint32(0), None, None, ctypes.c_int64(4), None) == 1
