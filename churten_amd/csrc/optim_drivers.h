@@ -163,6 +163,18 @@ __device__ __forceinline__ void store_stream(Pack<T, N>* p, const Pack<T, N>& v)
   store_bits<NT>(reinterpret_cast<PackBits<T, N>*>(p), __builtin_bit_cast(PackBits<T, N>, v));
 }
 
+// A pack whose value the compiler cannot know, at no cost (no instruction):
+// the value a pack can hold where a thread has nothing to load. Left undefined
+// there, a pack lets the compiler fold the conversion of a loaded 16-bit pack
+// into the branch that loads it, and the wavefront then waits for that load
+// right there, before it issues the next loads or its other work.
+template <typename T, int N>
+__device__ __forceinline__ void opaque(Pack<T, N>& x) {
+  PackBits<T, N> b;
+  asm volatile("" : "=v"(b));
+  x = __builtin_bit_cast(Pack<T, N>, b);
+}
+
 // Packs at addresses that are only element-aligned: operands whose 16-byte
 // boundaries do not line up with the parameters' (a column view at another
 // offset, a per-parameter gradient's rows). gfx950 code runs in unaligned
@@ -333,6 +345,14 @@ __device__ __forceinline__ void stream_tile_of_block(const Grid& g, uint32_t& r,
 template <typename T>
 __device__ __forceinline__ double hyper_at(const T* h, uint32_t r) {
   return static_cast<double>(widen(h[r]));
+}
+
+// Lane `lane`'s x, for every lane of the wavefront (that lane must be active).
+__device__ __forceinline__ double wave_lane(double x, int lane) {
+  const uint64_t b = __builtin_bit_cast(uint64_t, x);
+  const uint32_t lo = __builtin_amdgcn_readlane(static_cast<uint32_t>(b), lane);
+  const uint32_t hi = __builtin_amdgcn_readlane(static_cast<uint32_t>(b >> 32), lane);
+  return __builtin_bit_cast(double, (uint64_t(hi) << 32) | lo);
 }
 
 // ---------------------------------------------------------------------------
@@ -517,6 +537,20 @@ constexpr int stream_unroll(int fp32, int bf16_state, int narrow, int wide) {
 // unchanged (Adam's MALL-resident launches keep the vector read: -1.3% with
 // the scalar one).
 
+// Without a workspace, float32 Adam derives its constants once per wavefront
+// (wave_prologue: the two pow and two divides spread over even and odd lanes,
+// 280 VALU instructions per workgroup instead of 425), and with it amsgrad
+// moved to one pack per thread. Same-process A/B against the per-lane form
+// (3 rounds, one box): config 1 +22%, config 2 +8.9%, config-5 buffers +2.5%,
+// with amsgrad +4.2% (800 x 265,484 rows: +4.2%); two packs for amsgrad gave
+// +2.4% at config 2 and -0.7% on the config-5 buffers. The wavefront form lost
+// 1-9% for 16-bit parameters and bfloat16 moments (their load schedules moved),
+// so only float32 state takes it.
+// Opaque packs (kOpaquePacks / kOpaquePacksPre) in the same A/B: bfloat16
+// Adam with a workspace +1.2%, bfloat16 Adagrad with one +0.7-1.0%, float16
+// Adagrad without one +5.8%; other combinations of the 16-bit policies moved
+// -3% to +1% with them (float32 -3% at configs 1 and 2) and do without.
+
 // Adam / AdamW: h = {lr, beta1, beta2, eps, weight_decay}.
 template <typename T_, bool ADAMW, bool AMSGRAD, typename S_ = T_>
 struct AdamPolicy {
@@ -525,7 +559,7 @@ struct AdamPolicy {
   using M = op_t<T>;
   static constexpr int NS = AMSGRAD ? 3 : 2;
   static constexpr uint32_t kStreamLds = residency_lds<T, S>(AMSGRAD ? 12 : 10);
-  static constexpr int kStreamUnroll = stream_unroll<T, S>(2, 4, 4, 2);
+  static constexpr int kStreamUnroll = stream_unroll<T, S>(AMSGRAD ? 1 : 2, 4, 4, 2);
   // float16 Adam (no amsgrad): one 8-element pack under a cap of 20. Three
   // boxes, config-5 shape: 6.16-6.38 TB/s on synthetic moments and
   // 6.37 on moments that start at zero and underflow (the bench's data),
@@ -544,6 +578,8 @@ struct AdamPolicy {
       kFp32State<T, S> ? lds_for_residency(AMSGRAD ? 12 : 14) : kStreamLdsPre;
   static constexpr int kStreamUnrollPre = stream_unroll<T, S>(1, 1, 1, 2);
   static constexpr bool kScalarMask = !std::is_same<T, double>::value;
+  static constexpr bool kWavePrologue = kFp32State<T, S>;
+  static constexpr bool kOpaquePacksPre = kBf16ParamShape;
   static constexpr int kStreamUnrollSmall = stream_unroll<T, S>(2, 4, 4, 2);
   static constexpr int64_t kStreamSmallBytes = kMallBytes;
   static constexpr int kStreamPack = stream_pack<T, S>();
@@ -578,17 +614,45 @@ struct AdamPolicy {
   }
   template <bool PRE>
   __device__ static void prologue(const Vectors<T>& v, uint32_t r, Rep& rep) {
-    rep.h.lr = hyper_at(v.h[0], r);
-    rep.h.beta1 = hyper_at(v.h[1], r);
-    rep.h.beta2 = hyper_at(v.h[2], r);
-    rep.h.eps = hyper_at(v.h[3], r);
-    rep.h.weight_decay = hyper_at(v.h[4], r);
+    hypers(v, r, rep);
     if constexpr (PRE) {
       rep.c.step_size = static_cast<M>(v.pre[kPreStride * r]);
       rep.c.bc2s_div = v.pre[kPreStride * r + 1];
     } else {
       rep.c = consts(v, r);
     }
+  }
+  // prologue<false> for a replica that every lane of the wavefront shares.
+  // The two bias corrections' pow run as one, beta1's on even lanes and
+  // beta2's on odd ones, and so do the step size's divide and (float math)
+  // the divide that gives sqrt(v)'s divisor; lanes 0 and 1 then hand their
+  // values to the whole wavefront. Each value comes from the same operations
+  // on the same operands as in consts(), so the bits are the same, at about
+  // half of consts()'s fp64 instructions.
+  __device__ static void wave_prologue(const Vectors<T>& v, uint32_t r, Rep& rep) {
+    hypers(v, r, rep);
+    const bool odd = (__lane_id() & 1) != 0;
+    const double bc = adam_bias_correction(odd ? rep.h.beta2 : rep.h.beta1,
+                                           static_cast<float>(hyper_at(v.steps, r)));
+    if constexpr (std::is_same<M, float>::value) {
+      // Even lanes: lr / bias_correction1; odd lanes: 1 / bias_correction2_sqrt,
+      // each correction narrowed to float first (adam_consts).
+      const double den = static_cast<double>(static_cast<float>(odd ? std::sqrt(bc) : bc));
+      const double q = (odd ? 1.0 : rep.h.lr) / den;
+      rep.c.step_size = static_cast<float>(wave_lane(q, 0));
+      rep.c.bc2s_div = wave_lane(q, 1);
+    } else {
+      const double x = odd ? std::sqrt(bc) : rep.h.lr / bc;
+      rep.c.step_size = wave_lane(x, 0);
+      rep.c.bc2s_div = wave_lane(x, 1);
+    }
+  }
+  __device__ static void hypers(const Vectors<T>& v, uint32_t r, Rep& rep) {
+    rep.h.lr = hyper_at(v.h[0], r);
+    rep.h.beta1 = hyper_at(v.h[1], r);
+    rep.h.beta2 = hyper_at(v.h[2], r);
+    rep.h.eps = hyper_at(v.h[3], r);
+    rep.h.weight_decay = hyper_at(v.h[4], r);
   }
   __device__ static bool reads_state(const Vectors<T>&, uint32_t) { return true; }
   __device__ static bool decays(const Rep& rep) { return rep.h.weight_decay != 0; }
@@ -685,6 +749,9 @@ struct AdagradPolicy {
   static constexpr uint32_t kStreamLdsMid = kStreamLdsPre;
   static constexpr int kStreamUnrollPre = stream_unroll<T, S>(1, 1, 4, 2);
   static constexpr bool kScalarMask = std::is_same<T, float>::value;
+  static constexpr bool kOpaquePacks = kHalfAll<T, S>;
+  static constexpr bool kOpaquePacksPre =
+      std::is_same<T, bf16_t>::value && std::is_same<S, bf16_t>::value;
   static constexpr int kStreamUnrollSmall = stream_unroll<T, S>(2, 1, 4, 2);
   static constexpr int64_t kStreamSmallBytes = kMallBytes;
   static constexpr int kStreamPack = stream_pack<T, S>();
@@ -907,6 +974,54 @@ struct scalar_mask_small_of<P, std::void_t<decltype(P::kScalarMaskSmall)>> {
 template <typename P, bool SMALL>
 constexpr bool stream_scalar_mask() {
   return SMALL ? scalar_mask_small_of<P>::value : scalar_mask_of<P>::value;
+}
+
+// A policy's constants for a replica that a whole workgroup works on: its
+// `wave_prologue` (derived once per wavefront, the work spread over lanes)
+// where it sets kWavePrologue and the constants are derived, else
+// `prologue<PRE>`. Every lane of the wavefront must be active.
+template <typename P, typename = void>
+struct wave_prologue_of {
+  static constexpr bool value = false;
+};
+template <typename P>
+struct wave_prologue_of<P, std::void_t<decltype(P::kWavePrologue)>> {
+  static constexpr bool value = P::kWavePrologue;
+};
+template <typename P, bool PRE>
+__device__ __forceinline__ void uniform_prologue(const Vectors<typename P::T>& v, uint32_t r,
+                                                 typename P::Rep& rep) {
+  if constexpr (!PRE && wave_prologue_of<P>::value) {
+    P::wave_prologue(v, r, rep);
+  } else {
+    P::template prologue<PRE>(v, r, rep);
+  }
+}
+
+// Whether the streaming driver's large launches start a thread's packs from
+// opaque values (opaque()) rather than undefined ones: P::kOpaquePacks without
+// a workspace, P::kOpaquePacksPre with one; by default not. It changes the
+// compiler's schedule of the loads, and that pays for some 16-bit policies and
+// costs others (the policies say which).
+template <typename P, typename = void>
+struct opaque_packs_of {
+  static constexpr bool value = false;
+};
+template <typename P>
+struct opaque_packs_of<P, std::void_t<decltype(P::kOpaquePacks)>> {
+  static constexpr bool value = P::kOpaquePacks;
+};
+template <typename P, typename = void>
+struct opaque_packs_pre_of {
+  static constexpr bool value = false;
+};
+template <typename P>
+struct opaque_packs_pre_of<P, std::void_t<decltype(P::kOpaquePacksPre)>> {
+  static constexpr bool value = P::kOpaquePacksPre;
+};
+template <typename P, bool PRE, bool SMALL>
+constexpr bool stream_opaque_packs() {
+  return !SMALL && (PRE ? opaque_packs_pre_of<P>::value : opaque_packs_of<P>::value);
 }
 
 // The segmented driver's flag read and residency reservation with a
@@ -1186,6 +1301,12 @@ __global__ __launch_bounds__((stream_threads<P, SMALL>())) void stream_kernel(KA
 #pragma unroll
     for (int u = 0; u < U; ++u) {
       const int64_t i = int64_t(u) * NTH + threadIdx.x;
+      if constexpr (stream_opaque_packs<P, PRE, SMALL>()) {
+        opaque(vp[u]);
+        opaque(vg[u]);
+#pragma unroll
+        for (int b = 0; b < SS; ++b) opaque(vs[b][u]);
+      }
       if (i < packs_left) {
         vp[u] = load_stream<NT>(prow + i);
         vg[u] = grow.load(i);
@@ -1198,7 +1319,7 @@ __global__ __launch_bounds__((stream_threads<P, SMALL>())) void stream_kernel(KA
       }
     }
     typename P::Rep rep;
-    P::template prologue<PRE>(a.vec, r, rep);
+    uniform_prologue<P, PRE>(a.vec, r, rep);
     const auto store_packs = [&](int u, int64_t i) {
       store_stream<NT>(prow + i, vp[u]);
 #pragma unroll

@@ -301,14 +301,19 @@ __device__ __forceinline__ void adam_element(
   adam_finish(param, exp_avg, sqrt_rn<ZEROS>(v), h, c);
 }
 
+// 1 - beta^step in double, with pow(double, double) from the float step.
+__device__ __forceinline__ double adam_bias_correction(const double beta, const float step) {
+  return 1 - ::pow(beta, static_cast<double>(step));
+}
+
 // Per-replica bias corrections from the (bumped) step count: computed in double
-// with pow(double, double) from the float step, then narrowed to the math type.
+// (adam_bias_correction), then narrowed to the math type.
 template <typename opmath_t>
 __device__ __forceinline__ void adam_bias_corrections(
     const double beta1, const double beta2, const float step,
     opmath_t& bias_correction1, opmath_t& bias_correction2_sqrt) {
-  const double bc1 = 1 - ::pow(beta1, static_cast<double>(step));
-  const double bc2 = 1 - ::pow(beta2, static_cast<double>(step));
+  const double bc1 = adam_bias_correction(beta1, step);
+  const double bc2 = adam_bias_correction(beta2, step);
   bias_correction1 = static_cast<opmath_t>(bc1);
   bias_correction2_sqrt = static_cast<opmath_t>(std::sqrt(bc2));
 }

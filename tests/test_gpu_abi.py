@@ -14,12 +14,15 @@ for bit with the oracle's device formulation:
   consolidated gradient written on the way, and with a gap column range;
 * the large-launch shapes (non-temporal, residency-capped) of every policy and
   dtype just above the size where the small, MALL-resident shape stops, against
-  torch's own fused kernels row by row (and the oracle for float32).
+  torch's own fused kernels row by row (and the oracle for float32);
+* Adam's per-replica constants derived without a workspace (once per
+  wavefront) against those of the workspace form, replica by replica.
 """
 
 from __future__ import annotations
 
 import ctypes
+import math
 from pathlib import Path
 
 import numpy as np
@@ -456,6 +459,46 @@ def test_large_adam_rows_bit_identical_to_aten(dtype, amsgrad, adamw, maximize, 
             _same(f"{name}[{r}]", got[r], w[r])
     for t, f in zip((p, m, v), frozen):
         _same("frozen row", t[1], f)
+
+
+@pytest.mark.parametrize("large", [False, True], ids=["small", "large"])
+@pytest.mark.parametrize("dtype,amsgrad", [
+    (torch.float32, False), (torch.float32, True), (torch.float16, False),
+    (torch.bfloat16, False), (torch.float64, False)], ids=str)
+def test_adam_constants_per_wavefront_match_workspace(dtype, amsgrad, large):
+    """Without a workspace the streaming driver derives a replica's step size
+    and sqrt(v) divisor once per wavefront, the two pow and the two divides
+    spread over even and odd lanes; with one, the preparation launch derives
+    them one thread per replica. Both must give the same bits for every
+    replica: 512 replicas, each with its own lr, betas (up to 1 - 1e-7) and
+    step count (1 to 2^24 - 1), in MALL-resident and large launches."""
+    R = 512
+    bpe = torch.finfo(dtype).bits // 8 * (5 if amsgrad else 4)
+    T = _large_T(R, bpe) if large else 1003
+    g = torch.Generator(device=DEV).manual_seed(R + T)
+    rnd = lambda: torch.randn(R, T, device=DEV, generator=g, dtype=dtype)  # noqa: E731
+    ops = [rnd(), rnd(), rnd(), rnd().abs()] + ([rnd().abs()] if amsgrad else [])
+    u = lambda: torch.rand(R, device=DEV, generator=g, dtype=torch.float64)  # noqa: E731
+    steps = torch.floor(torch.exp(u() * math.log(2.0 ** 24 - 1))).clamp_(1, 2 ** 24 - 1)
+    steps[:4] = torch.tensor([1.0, 2.0, 3.0, 2.0 ** 24 - 1], dtype=torch.float64)
+    beta1 = 1 - torch.exp(u() * math.log(1e-7) * 0.5 - 0.1)
+    beta2 = 1 - torch.exp(u() * math.log(1e-7))
+    lr = torch.exp(math.log(1e-5) + u() * math.log(1e4))
+    eps = torch.full((R,), 1e-4 if dtype == torch.float16 else 1e-8, dtype=torch.float64,
+                     device=DEV)
+    wd = u() * 1e-2
+    hyp = [h.to(dtype) for h in (lr, beta1, beta2, eps, wd)]
+    steps = steps.to(dtype)
+    mask = (torch.rand(R, device=DEV, generator=g) < 0.9).to(torch.uint8)
+    flags = TS_AMSGRAD if amsgrad else 0
+    got = [t.clone() for t in ops]
+    assert abi_step("adam", got, steps, hyp, mask, flags, dtype=dtype, workspace=False) == 0
+    want = [t.clone() for t in ops]
+    assert abi_step("adam", want, steps, hyp, mask, flags, dtype=dtype, workspace=True) == 0
+    for name, a, b in zip(("params", "grads", "exp_avgs", "exp_avg_sqs", "max_exp_avg_sqs"),
+                          got, want):
+        _same(name, a, b)
+    assert not torch.equal(got[0], ops[0])
 
 
 @pytest.mark.filterwarnings("ignore:`is_first_step` argument has no effect")
