@@ -1414,8 +1414,12 @@ __global__ __launch_bounds__(kThreads) void element_kernel(KArgs<P> a) {
   if (!a.vec.mask[r]) {
     return;
   }
+  // The workgroup's replica is every lane's: float32 Adam without a workspace
+  // derives its constants once per wavefront (+4.0% on strided float32
+  // parameters, same-process A/B; the segmented driver lost 1.2% with it at
+  // config 5 and keeps the per-lane form).
   typename P::Rep rep;
-  P::template prologue<PRE>(a.vec, r, rep);
+  uniform_prologue<P, PRE>(a.vec, r, rep);
   const bool load_state = P::reads_state(a.vec, r);
 
   T* const prow = pg_row<P>(a.x, 0, r);

@@ -461,23 +461,34 @@ def test_large_adam_rows_bit_identical_to_aten(dtype, amsgrad, adamw, maximize, 
         _same("frozen row", t[1], f)
 
 
-@pytest.mark.parametrize("large", [False, True], ids=["small", "large"])
+@pytest.mark.parametrize("layout", ["small", "large", "strided"])
 @pytest.mark.parametrize("dtype,amsgrad", [
     (torch.float32, False), (torch.float32, True), (torch.float16, False),
     (torch.bfloat16, False), (torch.float64, False)], ids=str)
-def test_adam_constants_per_wavefront_match_workspace(dtype, amsgrad, large):
-    """Without a workspace the streaming driver derives a replica's step size
-    and sqrt(v) divisor once per wavefront, the two pow and the two divides
-    spread over even and odd lanes; with one, the preparation launch derives
-    them one thread per replica. Both must give the same bits for every
-    replica: 512 replicas, each with its own lr, betas (up to 1 - 1e-7) and
-    step count (1 to 2^24 - 1), in MALL-resident and large launches."""
+def test_adam_constants_per_wavefront_match_workspace(dtype, amsgrad, layout):
+    """Without a workspace the streaming and element drivers derive a
+    replica's step size and sqrt(v) divisor once per wavefront, the two pow and
+    the two divides spread over even and odd lanes; with one, the preparation
+    launch derives them one thread per replica. Both must give the same bits
+    for every replica: 512 replicas, each with its own lr, betas (up to
+    1 - 1e-7) and step count (1 to 2^24 - 1), in MALL-resident and large
+    streaming launches and with strided parameters (the element driver)."""
     R = 512
     bpe = torch.finfo(dtype).bits // 8 * (5 if amsgrad else 4)
-    T = _large_T(R, bpe) if large else 1003
+    T = _large_T(R, bpe) if layout == "large" else 1003
     g = torch.Generator(device=DEV).manual_seed(R + T)
     rnd = lambda: torch.randn(R, T, device=DEV, generator=g, dtype=dtype)  # noqa: E731
     ops = [rnd(), rnd(), rnd(), rnd().abs()] + ([rnd().abs()] if amsgrad else [])
+    # strided: the parameters every other element of a (R, 2T) buffer (a
+    # clone of such a view would be contiguous, so copies re-take the view)
+    base = None
+    if layout == "strided":
+        base = torch.randn(R, 2 * T, device=DEV, generator=g, dtype=dtype)
+        ops[0] = base[:, ::2]
+
+    def copy(t, i):
+        return base.clone()[:, ::2] if base is not None and i == 0 else t.clone()
+
     u = lambda: torch.rand(R, device=DEV, generator=g, dtype=torch.float64)  # noqa: E731
     steps = torch.floor(torch.exp(u() * math.log(2.0 ** 24 - 1))).clamp_(1, 2 ** 24 - 1)
     steps[:4] = torch.tensor([1.0, 2.0, 3.0, 2.0 ** 24 - 1], dtype=torch.float64)
@@ -491,10 +502,11 @@ def test_adam_constants_per_wavefront_match_workspace(dtype, amsgrad, large):
     steps = steps.to(dtype)
     mask = (torch.rand(R, device=DEV, generator=g) < 0.9).to(torch.uint8)
     flags = TS_AMSGRAD if amsgrad else 0
-    got = [t.clone() for t in ops]
+    got = [copy(t, i) for i, t in enumerate(ops)]
     assert abi_step("adam", got, steps, hyp, mask, flags, dtype=dtype, workspace=False) == 0
-    want = [t.clone() for t in ops]
+    want = [copy(t, i) for i, t in enumerate(ops)]
     assert abi_step("adam", want, steps, hyp, mask, flags, dtype=dtype, workspace=True) == 0
+    assert got[0].stride(1) == (2 if layout == "strided" else 1)
     for name, a, b in zip(("params", "grads", "exp_avgs", "exp_avg_sqs", "max_exp_avg_sqs"),
                           got, want):
         _same(name, a, b)
