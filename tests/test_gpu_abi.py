@@ -431,7 +431,7 @@ def _fused_rows_adam(p, g, m, v, mx, steps, hyp, mask, amsgrad, adamw, maximize)
 @pytest.mark.parametrize("dtype,amsgrad,adamw,maximize", [
     (torch.float32, False, False, False), (torch.float32, True, True, True),
     (torch.float16, False, True, False), (torch.bfloat16, True, False, False),
-    (torch.float64, False, True, True)], ids=str)
+    (torch.bfloat16, False, False, False), (torch.float64, False, True, True)], ids=str)
 def test_large_adam_rows_bit_identical_to_aten(dtype, amsgrad, adamw, maximize, workspace):
     R = 3
     bpe = torch.finfo(dtype).bits // 8 * (5 if amsgrad else 4)
@@ -546,10 +546,16 @@ def test_large_sgd_rows_bit_identical_to_aten(dtype, has_buf, nesterov):
 
 
 @pytest.mark.parametrize("workspace", [False, True], ids=["no_ws", "ws"])
-@pytest.mark.parametrize("dtype", [torch.float32, torch.float64, torch.bfloat16], ids=str)
-def test_large_adagrad_rows_bit_identical_to_aten(dtype, workspace):
+@pytest.mark.parametrize("dtype,extra", [
+    (torch.float32, 3), (torch.float64, 3), (torch.bfloat16, 3), (torch.float16, 3),
+    (torch.float16, 4)], ids=str)
+def test_large_adagrad_rows_bit_identical_to_aten(dtype, extra, workspace):
+    """float16 twice: with ragged rows (torch's element path, the state sum
+    rounded twice) and with rows a multiple of 4 long (its vector path,
+    rounded once)."""
     R = 3
-    T = _large_T(R, torch.finfo(dtype).bits // 8 * 3)
+    T = _large_T(R, torch.finfo(dtype).bits // 8 * 3, extra)
+    assert dtype != torch.float16 or (T % 4 == 0) == (extra == 4)
     g = torch.Generator(device=DEV).manual_seed(T + 2)
     rnd = lambda: torch.randn(R, T, device=DEV, generator=g, dtype=dtype)  # noqa: E731
     p, gr, s = rnd(), rnd(), rnd().abs()
