@@ -529,7 +529,8 @@ constexpr int stream_unroll(int fp32, int bf16_state, int narrow, int wide) {
 // Adam with amsgrad (large launches) and bfloat16-state SGD stayed within
 // 0.5% either way and kept their shapes. 16-bit SGD and Adagrad ran slower
 // with the scalar read (bfloat16 SGD -5% at its shape) and keep the vector
-// read, as does float64 (not swept). Same-process
+// read; float64 kept it too until swept on its own (float64 Adam without
+// amsgrad now reads it scalar, at the policy). Same-process
 // A/B of the whole change against the previous build (6 rounds): config 5
 // +2.7%, config 2 +2.1%, config 3 +1.3% (SGD's MALL-resident launches read
 // it scalar too), config 4 +0.4%, bfloat16 moments +5.1%, Adagrad on the
@@ -569,15 +570,22 @@ struct AdamPolicy {
   static constexpr bool kHalfShape = kHalfAll<T, S> && !AMSGRAD;
   static constexpr bool kBf16ParamShape =
       std::is_same<T, bf16_t>::value && std::is_same<S, bf16_t>::value && !AMSGRAD;
+  // float64 Adam (no amsgrad) with a workspace: one 4-element pack under a cap
+  // of 12, the flag read through the scalar cache. Same-process A/B, 64 x 4M
+  // doubles, 4 rounds: 5.33 TB/s against 5.15 for two packs uncapped with the
+  // vector read (one pack uncapped 5.28, under 16 5.26; two packs under 12
+  // 5.13; four uncapped 5.09). Without a workspace the scalar read: +1%.
+  static constexpr bool kWideShape = std::is_same<T, double>::value && !AMSGRAD;
   static constexpr uint32_t kStreamLdsPre =
       kBf16State<T, S>  ? lds_for_residency(16)
       : kHalfShape      ? lds_for_residency(20)
       : kBf16ParamShape ? lds_for_residency(16)
+      : kWideShape      ? lds_for_residency(12)
                         : residency_lds<T, S>(12);
   static constexpr uint32_t kStreamLdsMid =
       kFp32State<T, S> ? lds_for_residency(AMSGRAD ? 12 : 14) : kStreamLdsPre;
-  static constexpr int kStreamUnrollPre = stream_unroll<T, S>(1, 1, 1, 2);
-  static constexpr bool kScalarMask = !std::is_same<T, double>::value;
+  static constexpr int kStreamUnrollPre = stream_unroll<T, S>(1, 1, 1, kWideShape ? 1 : 2);
+  static constexpr bool kScalarMask = !std::is_same<T, double>::value || !AMSGRAD;
   static constexpr bool kWavePrologue = kFp32State<T, S>;
   static constexpr bool kOpaquePacksPre = kBf16ParamShape;
   static constexpr int kStreamUnrollSmall = stream_unroll<T, S>(2, 4, 4, 2);
