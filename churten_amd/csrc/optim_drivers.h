@@ -695,14 +695,19 @@ struct SgdPolicy {
   // float64 with momentum: one 4-element pack, uncapped, the flag read
   // through the scalar cache (same-process A/B on 64 x 4M doubles: +3.4%
   // against two packs with the vector read; under a cap of 12: -5%).
+  // float32 without momentum: one pack, uncapped, the scalar read (same-process
+  // A/B, 4 rounds, config-5 buffers: 6.46 TB/s against 5.38 for two packs with
+  // the vector read; two packs with the scalar read 5.59, four 6.07, one pack
+  // under a cap of 20 6.06; its MALL-resident launches +2.3% with the scalar
+  // read at config 3's size).
   static constexpr int kStreamUnroll =
-      kBf16Shape ? 2 : stream_unroll<T, S>(HAS_BUF ? 1 : 2, 1, 1, HAS_BUF ? 1 : 2);
+      kBf16Shape ? 2 : stream_unroll<T, S>(1, 1, 1, HAS_BUF ? 1 : 2);
   static constexpr uint32_t kStreamLdsPre = kStreamLds;
   static constexpr uint32_t kStreamLdsMid = kStreamLdsPre;
   static constexpr int kStreamUnrollPre = kStreamUnroll;
   static constexpr int kStreamUnrollSmall = stream_unroll<T, S>(1, 1, 4, 2);
   static constexpr bool kScalarMask =
-      HAS_BUF && (std::is_same<T, float>::value || std::is_same<T, double>::value);
+      std::is_same<T, float>::value || (HAS_BUF && std::is_same<T, double>::value);
   static constexpr bool kScalarMaskSmall = kScalarMask;
   // float32 launches that fit the MALL: four-wavefront workgroups. Config 3's
   // shape (32 x 545100, 80% active) with the vector flag read, two calls, 2-3
