@@ -570,12 +570,14 @@ struct AdamPolicy {
   static constexpr bool kHalfShape = kHalfAll<T, S> && !AMSGRAD;
   static constexpr bool kBf16ParamShape =
       std::is_same<T, bf16_t>::value && std::is_same<S, bf16_t>::value && !AMSGRAD;
-  // float64 Adam (no amsgrad) with a workspace: one 4-element pack under a cap
-  // of 12, the flag read through the scalar cache. Same-process A/B, 64 x 4M
-  // doubles, 4 rounds: 5.33 TB/s against 5.15 for two packs uncapped with the
-  // vector read (one pack uncapped 5.28, under 16 5.26; two packs under 12
-  // 5.13; four uncapped 5.09). Without a workspace the scalar read: +1%.
-  static constexpr bool kWideShape = std::is_same<T, double>::value && !AMSGRAD;
+  // float64 Adam with a workspace: one 4-element pack under a cap of 12, the
+  // flag read through the scalar cache. Same-process A/B, 64 x 4M doubles, 4
+  // rounds: 5.33 TB/s against 5.15 for two packs uncapped with the vector read
+  // (one pack uncapped 5.28, under 16 5.26; two packs under 12 5.13; four
+  // uncapped 5.09); with amsgrad (64 x 3M) +1.7%. Without a workspace the
+  // scalar read: +1%. 16-bit Adam with amsgrad kept its uncapped pack (caps
+  // 16 / 20 within 0.8%).
+  static constexpr bool kWideShape = std::is_same<T, double>::value;
   static constexpr uint32_t kStreamLdsPre =
       kBf16State<T, S>  ? lds_for_residency(16)
       : kHalfShape      ? lds_for_residency(20)
@@ -585,7 +587,7 @@ struct AdamPolicy {
   static constexpr uint32_t kStreamLdsMid =
       kFp32State<T, S> ? lds_for_residency(AMSGRAD ? 12 : 14) : kStreamLdsPre;
   static constexpr int kStreamUnrollPre = stream_unroll<T, S>(1, 1, 1, kWideShape ? 1 : 2);
-  static constexpr bool kScalarMask = !std::is_same<T, double>::value || !AMSGRAD;
+  static constexpr bool kScalarMask = true;
   static constexpr bool kWavePrologue = kFp32State<T, S>;
   static constexpr bool kOpaquePacksPre = kBf16ParamShape;
   static constexpr int kStreamUnrollSmall = stream_unroll<T, S>(2, 4, 4, 2);

@@ -431,7 +431,8 @@ def _fused_rows_adam(p, g, m, v, mx, steps, hyp, mask, amsgrad, adamw, maximize)
 @pytest.mark.parametrize("dtype,amsgrad,adamw,maximize", [
     (torch.float32, False, False, False), (torch.float32, True, True, True),
     (torch.float16, False, True, False), (torch.bfloat16, True, False, False),
-    (torch.bfloat16, False, False, False), (torch.float64, False, True, True)], ids=str)
+    (torch.bfloat16, False, False, False), (torch.float64, False, True, True),
+    (torch.float64, True, False, False)], ids=str)
 def test_large_adam_rows_bit_identical_to_aten(dtype, amsgrad, adamw, maximize, workspace):
     R = 3
     bpe = torch.finfo(dtype).bits // 8 * (5 if amsgrad else 4)
