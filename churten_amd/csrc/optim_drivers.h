@@ -1905,34 +1905,45 @@ struct ScatterArgs {
   Segments<T> seg;
 };
 
+// The scatter's workgroup shape: kScatterThreads threads x kScatterUnroll
+// packs of 4 elements per tile, under a residency cap of kScatterLds bytes of
+// dynamic LDS (0: none). Same-process A/B on config 5's twelve per-parameter
+// gradients (23.6 GB moved, 4 rounds): one wavefront x 1 pack 6.71 TB/s;
+// 128 x 2 6.48, 256 x 1 6.54, 128 x 1 6.44, 64 x 4 6.29, 64 x 2 5.95; caps of
+// 12-16 workgroups per CU 4.7-4.9.
+constexpr int kScatterThreads = 64;
+constexpr int kScatterUnroll = 1;
+constexpr uint32_t kScatterLds = 0;
+constexpr int64_t kScatterTile = int64_t(kScatterThreads) * kPack * kScatterUnroll;
+
 template <typename T>
-__global__ __launch_bounds__(kThreads) void scatter_kernel(ScatterArgs<T> a) {
+__global__ __launch_bounds__(kScatterThreads) void scatter_kernel(ScatterArgs<T> a) {
   const uint32_t tiles_per_row = a.seg.tile0[a.seg.n];
   const uint32_t r = blockIdx.x / tiles_per_row;
   const uint32_t local = blockIdx.x - r * tiles_per_row;
   const int s = segment_of_tile(a.seg.tile0, a.seg.n, local);
   const int64_t numel = a.seg.numel[s];
-  const int64_t j0 = int64_t(local - a.seg.tile0[s]) * kTile;
+  const int64_t j0 = int64_t(local - a.seg.tile0[s]) * kScatterTile;
   const T* src = a.seg.data[s] + int64_t(r) * a.seg.stride_r[s];
   T* dst = a.dst + int64_t(r) * a.dst_stride_r + a.seg.col[s];
   if ((a.seg.vec_ok >> s) & 1u) {
-    const SegTile t = seg_tile<T, kTile>(a.res0, a.rmod, r, a.seg.col[s], numel, j0);
-    Pack<T> v[kUnroll];
+    const SegTile t = seg_tile<T, kScatterTile>(a.res0, a.rmod, r, a.seg.col[s], numel, j0);
+    Pack<T> v[kScatterUnroll];
 #pragma unroll
-    for (int u = 0; u < kUnroll; ++u) {
-      const int64_t i = int64_t(u) * kThreads + threadIdx.x;
+    for (int u = 0; u < kScatterUnroll; ++u) {
+      const int64_t i = int64_t(u) * kScatterThreads + threadIdx.x;
       if (i < t.packs) v[u] = load_stream_any(src + t.first + i * kPack);
     }
 #pragma unroll
-    for (int u = 0; u < kUnroll; ++u) {
-      const int64_t i = int64_t(u) * kThreads + threadIdx.x;
+    for (int u = 0; u < kScatterUnroll; ++u) {
+      const int64_t i = int64_t(u) * kScatterThreads + threadIdx.x;
       if (i < t.packs) store_stream(reinterpret_cast<Pack<T>*>(dst + t.first) + i, v[u]);
     }
-    seg_singles<kThreads>(t, numel, [&](int64_t j) { dst[j] = src[j]; });
+    seg_singles<kScatterThreads>(t, numel, [&](int64_t j) { dst[j] = src[j]; });
     return;
   }
-  const int64_t cnt = imin(kTile, numel - j0);
-  for (int64_t j = j0 + threadIdx.x; j < j0 + cnt; j += kThreads) {
+  const int64_t cnt = imin(kScatterTile, numel - j0);
+  for (int64_t j = j0 + threadIdx.x; j < j0 + cnt; j += kScatterThreads) {
     dst[j] = src[j];
   }
 }

@@ -33,8 +33,12 @@ int scatter(const ts_segment* segs, int n_segs, void* dst, int64_t dst_stride_r,
   const bool any = std::any_of(segs, segs + n_segs, [](const ts_segment& s) {
     return s.numel > 0;
   });
-  if ((any && dst == nullptr) || !walk_fits<T>(walk, R, kTile, vec_rows, a.seg)) return kInvalid;
-  return launch_walk<T>(walk, R, kTile, vec_rows, a, a.seg, scatter_kernel<T>, stream);
+  if ((any && dst == nullptr) ||
+      !walk_fits<T>(walk, R, kScatterTile, vec_rows, a.seg, kScatterThreads)) {
+    return kInvalid;
+  }
+  return launch_walk<T>(walk, R, kScatterTile, vec_rows, a, a.seg, scatter_kernel<T>, stream,
+                        kScatterLds, kScatterThreads);
 }
 
 }  // namespace
