@@ -48,7 +48,9 @@
 // workgroup-uniform early exit, so its rows are never read or written (they stay
 // bit-identical, and a replica frozen at step 0 never evaluates 1 - beta^0 = 0).
 // Active workgroups read the replica's hyperparameters once (uniform address:
-// scalar loads) and derive the per-replica constants, then stream their tile.
+// scalar loads) and read the per-replica constants from the call's workspace
+// or derive them (float32 Adam: once per wavefront, the work spread over its
+// lanes), then stream their tile.
 // All drivers inline the same per-element update, so the same element gives
 // the same bits whichever driver processed it.
 //
