@@ -597,13 +597,23 @@ struct AdamPolicy {
   static constexpr int kStreamPack = stream_pack<T, S>();
   static constexpr int kSegmentUnroll = stream_unroll<T, S>(2, 4, 8, 2);
   static constexpr int kSegmentThreads = kThreads;
-  static constexpr int kSegmentThreadsPre = kFp32State<T, S> ? kStreamThreads : kThreads;
-  static constexpr int kSegmentUnrollPre = kFp32State<T, S> ? 1 : kSegmentUnroll;
+  // With a workspace, every type but float64 runs one-wavefront workgroups:
+  // one pack of 4 for float32 and bfloat16 moments, two for 16-bit params.
+  // Same-process A/B on config 5's twelve per-parameter gradients, 4 rounds,
+  // against 128 threads x 4 / 8 packs with the vector flag read: bfloat16
+  // moments 6.20 TB/s against 5.54, float16 / bfloat16 params 5.93 / 6.18
+  // against 5.68 / 5.66 (128 threads x 2 / 4: 5.87 / 6.07 and 5.88 / 5.82).
+  static constexpr int kSegmentThreadsPre =
+      std::is_same<T, double>::value ? kThreads : kStreamThreads;
+  static constexpr int kSegmentUnrollPre = sizeof(T) == 2 ? 2 : std::is_same<T, double>::value
+                                                                   ? kSegmentUnroll
+                                                                   : 1;
   // float32 Adam's segmented update with a workspace: the flag read through
   // the scalar cache under a cap of 20 (config 5, twelve per-parameter
   // gradients, 3 rounds: 6.35 TB/s against 6.13 for the vector read
-  // uncapped; the vector read under cap 20: 6.28).
-  static constexpr bool kSegmentScalarMask = kFp32State<T, S>;
+  // uncapped; the vector read under cap 20: 6.28). The other types but
+  // float64 read it scalar too.
+  static constexpr bool kSegmentScalarMask = !std::is_same<T, double>::value;
   static constexpr uint32_t kSegmentLdsPre = kFp32State<T, S> ? lds_for_residency(20) : 0u;
   static constexpr bool kLateStores = !AMSGRAD && std::is_same<T_, float>::value;
   static constexpr bool kVariant = false;
