@@ -734,12 +734,15 @@ struct SgdPolicy {
   // Segmented float32 updates: one-wavefront workgroups, one pack, the flag
   // read through the scalar cache (same-process A/B on config 5's twelve
   // per-parameter gradients, 4 rounds: 6.28 TB/s against 5.95 for 128 threads
-  // x 2 packs with the vector read; 128 x 1: 6.19).
+  // x 2 packs with the vector read; 128 x 1: 6.19). 16-bit: one wavefront x 2
+  // packs of 4, scalar read (float16 / bfloat16 6.33 / 6.29 against 5.76 /
+  // 5.71; one pack 5.46 / 5.37, four 5.92 / 5.91).
   static constexpr int kSegmentUnroll = kFp32State<T, S> ? 1 : 2;
-  static constexpr int kSegmentThreads = kFp32State<T, S> ? kStreamThreads : kThreads;
+  static constexpr int kSegmentThreads =
+      kFp32State<T, S> || sizeof(T) == 2 ? kStreamThreads : kThreads;
   static constexpr int kSegmentThreadsPre = kThreads;
   static constexpr int kSegmentUnrollPre = kSegmentUnroll;
-  static constexpr bool kSegmentScalarMask = kFp32State<T, S>;
+  static constexpr bool kSegmentScalarMask = kFp32State<T, S> || sizeof(T) == 2;
   static constexpr bool kLateStores = std::is_same<T_, float>::value;
   static constexpr bool kVariant = false;
   static constexpr int kPreWords = 0;
@@ -799,12 +802,15 @@ struct AdagradPolicy {
   // pack, the scalar flag read, uncapped (same-process A/B on config 5's
   // twelve per-parameter gradients, 4 rounds: 6.34 TB/s against 5.97 for 128
   // threads x 2 packs with the vector read; under a cap of 20: 6.13). Without
-  // a workspace the shape stays; the scalar read costs it 0.5%.
+  // a workspace the shape stays; the scalar read costs it 0.5%. 16-bit with a
+  // workspace: one wavefront x 4 packs of 4, scalar read (float16 / bfloat16
+  // 5.76 / 5.73 against 5.39 / 5.46; two packs 5.49 / 5.62, one 4.70 / 4.95).
   static constexpr int kSegmentUnroll = 2;
   static constexpr int kSegmentThreads = kThreads;
-  static constexpr int kSegmentThreadsPre = kFp32State<T, S> ? kStreamThreads : kThreads;
-  static constexpr int kSegmentUnrollPre = kFp32State<T, S> ? 1 : kSegmentUnroll;
-  static constexpr bool kSegmentScalarMask = kFp32State<T, S>;
+  static constexpr int kSegmentThreadsPre =
+      kFp32State<T, S> || sizeof(T) == 2 ? kStreamThreads : kThreads;
+  static constexpr int kSegmentUnrollPre = kFp32State<T, S> ? 1 : sizeof(T) == 2 ? 4 : kSegmentUnroll;
+  static constexpr bool kSegmentScalarMask = kFp32State<T, S> || sizeof(T) == 2;
   static constexpr bool kLateStores = false;
   static constexpr bool kVariant = std::is_same_v<T, _Float16> && std::is_same_v<S, _Float16>;
   static constexpr int kPreWords = 1;
