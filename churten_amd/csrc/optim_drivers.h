@@ -597,23 +597,22 @@ struct AdamPolicy {
   static constexpr int kStreamPack = stream_pack<T, S>();
   static constexpr int kSegmentUnroll = stream_unroll<T, S>(2, 4, 8, 2);
   static constexpr int kSegmentThreads = kThreads;
-  // With a workspace, every type but float64 runs one-wavefront workgroups:
-  // one pack of 4 for float32 and bfloat16 moments, two for 16-bit params.
+  // With a workspace, every type runs one-wavefront workgroups: one pack of
+  // 4 for float32 and bfloat16 moments, two for 16-bit params and float64.
   // Same-process A/B on config 5's twelve per-parameter gradients, 4 rounds,
   // against 128 threads x 4 / 8 packs with the vector flag read: bfloat16
   // moments 6.20 TB/s against 5.54, float16 / bfloat16 params 5.93 / 6.18
   // against 5.68 / 5.66 (128 threads x 2 / 4: 5.87 / 6.07 and 5.88 / 5.82).
-  static constexpr int kSegmentThreadsPre =
-      std::is_same<T, double>::value ? kThreads : kStreamThreads;
-  static constexpr int kSegmentUnrollPre = sizeof(T) == 2 ? 2 : std::is_same<T, double>::value
-                                                                   ? kSegmentUnroll
-                                                                   : 1;
+  // float64: two packs of 4, +1.6% against 128 threads x 2.
+  static constexpr int kSegmentThreadsPre = kStreamThreads;
+  static constexpr int kSegmentUnrollPre =
+      sizeof(T) == 2 || std::is_same<T, double>::value ? 2 : 1;
   // float32 Adam's segmented update with a workspace: the flag read through
   // the scalar cache under a cap of 20 (config 5, twelve per-parameter
   // gradients, 3 rounds: 6.35 TB/s against 6.13 for the vector read
-  // uncapped; the vector read under cap 20: 6.28). The other types but
-  // float64 read it scalar too.
-  static constexpr bool kSegmentScalarMask = !std::is_same<T, double>::value;
+  // uncapped; the vector read under cap 20: 6.28). The other types read it
+  // scalar too.
+  static constexpr bool kSegmentScalarMask = true;
   static constexpr uint32_t kSegmentLdsPre = kFp32State<T, S> ? lds_for_residency(20) : 0u;
   static constexpr bool kLateStores = !AMSGRAD && std::is_same<T_, float>::value;
   static constexpr bool kVariant = false;
@@ -736,13 +735,13 @@ struct SgdPolicy {
   // per-parameter gradients, 4 rounds: 6.28 TB/s against 5.95 for 128 threads
   // x 2 packs with the vector read; 128 x 1: 6.19). 16-bit: one wavefront x 2
   // packs of 4, scalar read (float16 / bfloat16 6.33 / 6.29 against 5.76 /
-  // 5.71; one pack 5.46 / 5.37, four 5.92 / 5.91).
-  static constexpr int kSegmentUnroll = kFp32State<T, S> ? 1 : 2;
-  static constexpr int kSegmentThreads =
-      kFp32State<T, S> || sizeof(T) == 2 ? kStreamThreads : kThreads;
+  // 5.71; one pack 5.46 / 5.37, four 5.92 / 5.91). bfloat16 state: one pack,
+  // +2.5% (two: -10%); float64: two packs, +0.9%.
+  static constexpr int kSegmentUnroll = kFp32State<T, S> || kBf16State<T, S> ? 1 : 2;
+  static constexpr int kSegmentThreads = kStreamThreads;
   static constexpr int kSegmentThreadsPre = kThreads;
   static constexpr int kSegmentUnrollPre = kSegmentUnroll;
-  static constexpr bool kSegmentScalarMask = kFp32State<T, S> || sizeof(T) == 2;
+  static constexpr bool kSegmentScalarMask = true;
   static constexpr bool kLateStores = std::is_same<T_, float>::value;
   static constexpr bool kVariant = false;
   static constexpr int kPreWords = 0;
@@ -805,12 +804,13 @@ struct AdagradPolicy {
   // a workspace the shape stays; the scalar read costs it 0.5%. 16-bit with a
   // workspace: one wavefront x 4 packs of 4, scalar read (float16 / bfloat16
   // 5.76 / 5.73 against 5.39 / 5.46; two packs 5.49 / 5.62, one 4.70 / 4.95).
+  // bfloat16 state: one pack, +2.4% (two: -10%); float64: two packs, +1.7%.
   static constexpr int kSegmentUnroll = 2;
   static constexpr int kSegmentThreads = kThreads;
-  static constexpr int kSegmentThreadsPre =
-      kFp32State<T, S> || sizeof(T) == 2 ? kStreamThreads : kThreads;
-  static constexpr int kSegmentUnrollPre = kFp32State<T, S> ? 1 : sizeof(T) == 2 ? 4 : kSegmentUnroll;
-  static constexpr bool kSegmentScalarMask = kFp32State<T, S> || sizeof(T) == 2;
+  static constexpr int kSegmentThreadsPre = kStreamThreads;
+  static constexpr int kSegmentUnrollPre =
+      kFp32State<T, S> || kBf16State<T, S> ? 1 : sizeof(T) == 2 ? 4 : kSegmentUnroll;
+  static constexpr bool kSegmentScalarMask = true;
   static constexpr bool kLateStores = false;
   static constexpr bool kVariant = std::is_same_v<T, _Float16> && std::is_same_v<S, _Float16>;
   static constexpr int kPreWords = 1;
