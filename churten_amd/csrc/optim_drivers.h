@@ -1535,7 +1535,10 @@ __global__ __launch_bounds__(kThreads) void element_kernel(KArgs<P> a) {
 // 0.1-0.9 TB/s slower at every R.)
 constexpr int kColThreads = 256;
 constexpr int kColThreadsNarrow = 128;
-constexpr int kColIters = 32;  // columns per thread per workgroup
+// Columns per thread per workgroup: 16 (config 5 as transposed views, R =
+// 128, same-process A/B, two runs of 3-4 rounds: +2.2-2.6% against 32; 8:
+// -1% to +2.5%, 24 and 64: -0.6% to -1.2%).
+constexpr int kColIters = 16;
 constexpr int kColUnroll = 4;
 constexpr uint32_t kLineBytes = 128;
 constexpr uint32_t kXcds = 8;
