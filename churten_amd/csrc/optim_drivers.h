@@ -1537,7 +1537,8 @@ constexpr int kColThreads = 256;
 constexpr int kColThreadsNarrow = 128;
 // Columns per thread per workgroup: 16 (config 5 as transposed views, R =
 // 128, same-process A/B, two runs of 3-4 rounds: +2.2-2.6% against 32; 8:
-// -1% to +2.5%, 24 and 64: -0.6% to -1.2%).
+// -1% to +2.5%, 24 and 64: -0.6% to -1.2%; against 32 at R = 64 ... 4096 on
+// 2^28-element buffers: +0.7% to +1.9%).
 constexpr int kColIters = 16;
 constexpr int kColUnroll = 4;
 constexpr uint32_t kLineBytes = 128;
