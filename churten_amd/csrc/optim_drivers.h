@@ -531,8 +531,8 @@ constexpr int stream_unroll(int fp32, int bf16_state, int narrow, int wide) {
 // Adam with amsgrad (large launches) and bfloat16-state SGD stayed within
 // 0.5% either way and kept their shapes. 16-bit SGD and Adagrad ran slower
 // with the scalar read (bfloat16 SGD -5% at its shape) and keep the vector
-// read; float64 kept it too until swept on its own (float64 Adam without
-// amsgrad now reads it scalar, at the policy). Same-process
+// read; float64 kept it too until swept on its own (float64 Adam, SGD with
+// momentum and Adagrad now read it scalar, at the policies). Same-process
 // A/B of the whole change against the previous build (6 rounds): config 5
 // +2.7%, config 2 +2.1%, config 3 +1.3% (SGD's MALL-resident launches read
 // it scalar too), config 4 +0.4%, bfloat16 moments +5.1%, Adagrad on the
