@@ -801,9 +801,9 @@ struct AdagradPolicy {
   static constexpr bool kOpaquePacks = kHalfAll<T, S>;
   static constexpr bool kOpaquePacksPre =
       std::is_same<T, bf16_t>::value && std::is_same<S, bf16_t>::value;
-  // MALL-resident 16-bit launches: one pack, the scalar flag read (bfloat16
-  // at config 4's shape: +12% against four packs with the vector read; two
-  // packs +5%).
+  // MALL-resident 16-bit launches: one pack, the scalar flag read (at config
+  // 4's shape against four packs with the vector read: bfloat16 +12%, float16
+  // +9%; two packs +5%).
   static constexpr int kStreamUnrollSmall = stream_unroll<T, S>(2, 1, 1, 2);
   static constexpr bool kScalarMaskSmall = sizeof(T) == 2;
   static constexpr int64_t kStreamSmallBytes = kMallBytes;
