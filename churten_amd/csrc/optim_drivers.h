@@ -93,7 +93,6 @@ constexpr int kThreads = 128;
 constexpr int kPack = 4;
 constexpr int kUnroll = 2;
 constexpr int kPer = kPack * kUnroll;  // elements per thread per tile
-constexpr int64_t kTile = int64_t(kThreads) * kPer;
 constexpr int kStreamThreads = 64;
 
 // Tile boundaries sit on 256-byte boundaries of the (R, T) rows (the
@@ -1463,17 +1462,26 @@ __global__ __launch_bounds__((stream_threads<P, SMALL>())) void stream_kernel(KA
   }
 }
 
-// Any strides: kPer elements per thread, one element per access. PRE: the
+// The element driver's shape: kElemThreads threads x kElemPer elements per
+// thread per tile. 128 x 4: float32 Adam with stride-2 parameters (64 x 4M),
+// same-process A/B, 4 rounds, against 128 x 8: +15% with a workspace, +12%
+// without (256 x 4 +13% / +11%, 64 x 4 +10%, 128 x 16 -36%); with every
+// operand at stride 2, -0.4%.
+constexpr int kElemThreads = kThreads;
+constexpr int kElemPer = 4;
+constexpr int64_t kElemTile = int64_t(kElemThreads) * kElemPer;
+
+// Any strides: kElemPer elements per thread, one element per access. PRE: the
 // replica's constants come from the call's workspace.
 template <typename P, bool PRE>
-__global__ __launch_bounds__(kThreads) void element_kernel(KArgs<P> a) {
+__global__ __launch_bounds__(kElemThreads) void element_kernel(KArgs<P> a) {
   using T = typename P::T;
   using S = typename P::S;
   constexpr int NS = P::NS;
   constexpr int SS = state_slots<P>();
   uint32_t r;
   int64_t t0;
-  tile_of_block<kTile>(a.g, r, t0);
+  tile_of_block<kElemTile>(a.g, r, t0);
   if (!a.vec.mask[r]) {
     return;
   }
@@ -1490,11 +1498,11 @@ __global__ __launch_bounds__(kThreads) void element_kernel(KArgs<P> a) {
   S* srow[SS];
 #pragma unroll
   for (int b = 0; b < NS; ++b) srow[b] = state_row<P>(a.x, 2 + b, r);
-  T vp[kPer], vg[kPer];
-  S vs[SS][kPer];
+  T vp[kElemPer], vg[kElemPer];
+  S vs[SS][kElemPer];
 #pragma unroll
-  for (int u = 0; u < kPer; ++u) {
-    const int64_t t = t0 + int64_t(u) * kThreads + threadIdx.x;
+  for (int u = 0; u < kElemPer; ++u) {
+    const int64_t t = t0 + int64_t(u) * kElemThreads + threadIdx.x;
     if (t < a.g.T) {
       vp[u] = prow[t * a.x.stride_t[0]];
       vg[u] = grow[t * a.x.stride_t[1]];
@@ -1507,8 +1515,8 @@ __global__ __launch_bounds__(kThreads) void element_kernel(KArgs<P> a) {
     }
   }
 #pragma unroll
-  for (int u = 0; u < kPer; ++u) {
-    const int64_t t = t0 + int64_t(u) * kThreads + threadIdx.x;
+  for (int u = 0; u < kElemPer; ++u) {
+    const int64_t t = t0 + int64_t(u) * kElemThreads + threadIdx.x;
     if (t < a.g.T) {
       S st[SS];
 #pragma unroll
@@ -2439,11 +2447,11 @@ int launch_dense(const Call& c, int nbufs) {
     if (!fill_kargs<P>(c, nbufs, a, false)) return false;
     uint32_t res0 = 0, rmod = 0;
     streamable = rows_streamable<P>(a.x, nbufs, res0, rmod);
-    const int64_t tile = !streamable ? kTile
+    const int64_t tile = !streamable ? kElemTile
                          : small     ? stream_tile<P, false, true>()
                          : pre       ? stream_tile<P, true, false>()
                                      : stream_tile<P, false, false>();
-    const int threads = !streamable ? kThreads
+    const int threads = !streamable ? kElemThreads
                         : small     ? stream_threads<P, true>()
                                     : stream_threads<P, false>();
     // The streaming driver adds each row's tile 0 (its head and tail).
@@ -2453,7 +2461,7 @@ int launch_dense(const Call& c, int nbufs) {
     return true;
   };
   return run_step<P>(c, a.vec, prepare, [&]() -> int {
-    const dim3 grid(blocks), block(kThreads);
+    const dim3 grid(blocks), block(kElemThreads);
     ColArgs<P> ca;
     uint32_t col_blocks = 0;
     if (streamable) {
