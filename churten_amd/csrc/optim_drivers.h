@@ -80,15 +80,16 @@
 namespace churten {
 namespace {
 
-// Launch shape, measured on the MI355X over the 52 GB north-star state: 2
-// packs of 4 elements per thread with non-temporal vector loads and stores
-// (non-temporal hints on both loads and stores were worth ~10% over plain
-// accesses, either alone nothing). The streaming driver runs one wavefront per
-// workgroup under a residency cap (below; 512-element tiles for float32): of
-// 64/128/256 threads x 1/2/4 packs x 8-24 resident waves per CU, that was
-// fastest, ahead of 128 x 2 with its best cap by 2-6% and uncapped 128 x 2 by
-// 6-10%. The other drivers keep 128 threads (1024-element tiles for float32),
-// where their own sweeps put them; packs per thread follow the policy.
+// Launch shape, measured on the MI355X over the 52 GB north-star state:
+// non-temporal vector loads and stores of 4-element packs (non-temporal hints
+// on both loads and stores were worth ~10% over plain accesses, either alone
+// nothing). The streaming driver runs one wavefront per workgroup under a
+// residency cap (each policy's shape below): of 64/128/256 threads x 1/2/4
+// packs x 8-24 resident waves per CU, that was fastest, ahead of 128 x 2 with
+// its best cap by 2-6% and uncapped 128 x 2 by 6-10%. The segmented driver
+// and the scatter mostly run one wavefront too; the element and column
+// drivers and a few segmented forms keep 128 or 256 threads, where their own
+// sweeps put them. kThreads / kPer are the defaults those start from.
 constexpr int kThreads = 128;
 constexpr int kPack = 4;
 constexpr int kUnroll = 2;
