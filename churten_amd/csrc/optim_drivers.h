@@ -437,14 +437,19 @@ constexpr int64_t kMidBytes = int64_t(1) << 30;
 // (with float32 or bfloat16 state) of Adam without amsgrad and of SGD store
 // late. The segmented driver keeps per-pack stores for every policy: late
 // ones lost 0.6-0.8% there.
-// Elements per pack of the streaming driver: 8 (16 B) where parameters and
-// state are 16-bit, else 4 (16 B for float32). With float32 parameters next to
+// Elements per pack of the streaming driver: 16 B per lane and access, so a
+// wavefront's access covers 1 KB of consecutive bytes. 8 where parameters and
+// state are 16-bit, 2 for float64, else 4. With float32 parameters next to
 // bfloat16 state a pack stays 4 elements (8 B of state): 8-element packs there
 // make the float32 operands' accesses 32 B apart per lane, measured 5-15%
-// slower on the config-5 buffers.
+// slower on the config-5 buffers. float64 had 4-element packs (32 B apart per
+// lane, two accesses each covering every other 16 B of 2 KB); 2-element packs
+// with the same packs per thread, same-process A/B on 64 x 4M doubles, 4
+// rounds: Adam +23% with a workspace (6.53 TB/s) and +13% without, SGD with
+// momentum +17%, Adagrad +17%, config 1's shape in float64 +5%.
 template <typename T, typename S>
 constexpr int stream_pack() {
-  return sizeof(T) == 2 && sizeof(S) == 2 ? 8 : kPack;
+  return sizeof(T) == 2 && sizeof(S) == 2 ? 8 : std::is_same<T, double>::value ? 2 : kPack;
 }
 
 template <typename T, typename S>
