@@ -607,7 +607,7 @@ struct AdamPolicy {
       !kFp32State<T, S> && !std::is_same<T, double>::value;
   static constexpr int64_t kStreamSmallBytes = kMallBytes;
   static constexpr int kStreamPack = stream_pack<T, S>();
-  static constexpr int kSegmentUnroll = stream_unroll<T, S>(2, 4, 8, 2);
+  static constexpr int kSegmentUnroll = stream_unroll<T, S>(2, 4, 4, 2);
   static constexpr int kSegmentThreads = kThreads;
   // With a workspace, every type runs one-wavefront workgroups: one pack of
   // 4 for float32 and bfloat16 moments, two for 16-bit params and float64.
@@ -617,8 +617,7 @@ struct AdamPolicy {
   // against 5.68 / 5.66 (128 threads x 2 / 4: 5.87 / 6.07 and 5.88 / 5.82).
   // float64: two packs of 4, +1.6% against 128 threads x 2.
   static constexpr int kSegmentThreadsPre = kStreamThreads;
-  static constexpr int kSegmentUnrollPre =
-      sizeof(T) == 2 || std::is_same<T, double>::value ? 2 : 1;
+  static constexpr int kSegmentUnrollPre = std::is_same<T, double>::value ? 2 : 1;
   // float32 Adam's segmented update with a workspace: the flag read through
   // the scalar cache under a cap of 20 (config 5, twelve per-parameter
   // gradients, 3 rounds: 6.35 TB/s against 6.13 for the vector read
@@ -749,7 +748,7 @@ struct SgdPolicy {
   // packs of 4, scalar read (float16 / bfloat16 6.33 / 6.29 against 5.76 /
   // 5.71; one pack 5.46 / 5.37, four 5.92 / 5.91). bfloat16 state: one pack,
   // +2.5% (two: -10%); float64: two packs, +0.9%.
-  static constexpr int kSegmentUnroll = kFp32State<T, S> || kBf16State<T, S> ? 1 : 2;
+  static constexpr int kSegmentUnroll = std::is_same<T, double>::value ? 2 : 1;
   static constexpr int kSegmentThreads = kStreamThreads;
   static constexpr int kSegmentThreadsPre = kThreads;
   static constexpr int kSegmentUnrollPre = kSegmentUnroll;
@@ -821,11 +820,11 @@ struct AdagradPolicy {
   // workspace: one wavefront x 4 packs of 4, scalar read (float16 / bfloat16
   // 5.76 / 5.73 against 5.39 / 5.46; two packs 5.49 / 5.62, one 4.70 / 4.95).
   // bfloat16 state: one pack, +2.4% (two: -10%); float64: two packs, +1.7%.
-  static constexpr int kSegmentUnroll = 2;
+  static constexpr int kSegmentUnroll = sizeof(T) == 2 ? 1 : 2;
   static constexpr int kSegmentThreads = kThreads;
   static constexpr int kSegmentThreadsPre = kStreamThreads;
   static constexpr int kSegmentUnrollPre =
-      kFp32State<T, S> || kBf16State<T, S> ? 1 : sizeof(T) == 2 ? 4 : kSegmentUnroll;
+      kFp32State<T, S> || kBf16State<T, S> ? 1 : 2;
   static constexpr bool kSegmentScalarMask = true;
   static constexpr bool kLateStores = false;
   static constexpr bool kVariant = std::is_same_v<T, _Float16> && std::is_same_v<S, _Float16>;
@@ -1162,7 +1161,8 @@ constexpr int segment_unroll() {
 }
 template <typename P, bool PRE>
 constexpr int64_t segment_tile() {
-  return int64_t(segment_threads<P, PRE>()) * kPack * segment_unroll<P, PRE>();
+  return int64_t(segment_threads<P, PRE>()) * stream_pack<typename P::T, typename P::S>() *
+         segment_unroll<P, PRE>();
 }
 
 template <typename P>
@@ -1759,17 +1759,17 @@ struct SegTile {
   bool has_head, has_tail;
 };
 
-template <typename T, int64_t TILE>
+template <typename T, int64_t TILE, int KP>
 __device__ __forceinline__ SegTile seg_tile(uint32_t res0, uint32_t rmod, uint32_t r,
                                             int64_t col, int64_t numel, int64_t j0) {
   constexpr uint32_t A = align_elems<T>();
   SegTile t;
   const uint32_t phase = (res0 + r * rmod + static_cast<uint32_t>(col % A)) % A;
   t.head = imin(numel, (A - phase) % A);
-  const int64_t packs_seg = (numel - t.head) / kPack;
+  const int64_t packs_seg = (numel - t.head) / KP;
   t.first = t.head + j0;
-  t.packs = packs_seg - j0 / kPack;
-  t.tail = t.head + packs_seg * kPack;
+  t.packs = packs_seg - j0 / KP;
+  t.tail = t.head + packs_seg * KP;
   t.has_head = j0 == 0;
   t.has_tail = j0 + TILE >= numel;
   return t;
@@ -1796,6 +1796,12 @@ __global__ __launch_bounds__((segment_threads<P, PRE>())) void segment_kernel(Se
   constexpr int U = segment_unroll<P, PRE>();
   constexpr int NTH = segment_threads<P, PRE>();
   constexpr int64_t kSegTile = segment_tile<P, PRE>();
+  // 16 B per lane and access, as in the streaming driver (4-element packs had
+  // given 16-bit operands 8 B per lane and float64 32 B, two accesses over
+  // every other 16 B: float64 +16% for Adam and SGD with 16-byte packs, 16-bit
+  // within -1.3% to +4% at half the packs per thread; same-process A/B on
+  // config 5's per-parameter gradients).
+  constexpr int KP = stream_pack<T, S>();
   const uint32_t tiles_per_row = a.seg.tile0[a.seg.n];
   const uint32_t r = blockIdx.x / tiles_per_row;
   const uint32_t local = blockIdx.x - r * tiles_per_row;
@@ -1830,12 +1836,13 @@ __global__ __launch_bounds__((segment_threads<P, PRE>())) void segment_kernel(Se
     // A frozen replica's optimizer state is not touched, but the consolidated
     // gradient is still filled, as the separate scatter would have filled it.
     if (vec) {
-      const SegTile t = seg_tile<T, kSegTile>(a.k.g.res0, a.k.g.rmod, r, col, numel, j0);
+      const SegTile t = seg_tile<T, kSegTile, KP>(a.k.g.res0, a.k.g.rmod, r, col, numel, j0);
 #pragma unroll
       for (int u = 0; u < U; ++u) {
         const int64_t i = int64_t(u) * NTH + threadIdx.x;
         if (i < t.packs) {
-          Packs<ANY, T>(g_dst + t.first).store(i, load_stream_any(g_src + t.first + i * kPack));
+          Packs<ANY, T, true, KP>(g_dst + t.first)
+              .store(i, load_stream_any<true, KP>(g_src + t.first + i * KP));
         }
       }
       seg_singles<NTH>(t, numel, [&](int64_t j) { g_dst[j] = g_src[j]; });
@@ -1886,14 +1893,14 @@ __global__ __launch_bounds__((segment_threads<P, PRE>())) void segment_kernel(Se
 
   // Vector walk (unit inner strides): the parameters' packs are aligned; with
   // ANY the other operands sit at another 16-byte phase (element-aligned packs).
-  const SegTile t = seg_tile<T, kSegTile>(a.k.g.res0, a.k.g.rmod, r, col, numel, j0);
-  Pack<T>* const pp = reinterpret_cast<Pack<T>*>(prow + t.first);
-  Packs<ANY, S> sp[SS];
+  const SegTile t = seg_tile<T, kSegTile, KP>(a.k.g.res0, a.k.g.rmod, r, col, numel, j0);
+  Pack<T, KP>* const pp = reinterpret_cast<Pack<T, KP>*>(prow + t.first);
+  Packs<ANY, S, true, KP> sp[SS];
 #pragma unroll
-  for (int b = 0; b < NS; ++b) sp[b] = Packs<ANY, S>(srow[b] + t.first);
-  const Packs<ANY, T> gout(g_dst != nullptr ? g_dst + t.first : nullptr);
-  Pack<T> vp[U], vg[U];
-  Pack<S> vs[SS][U];
+  for (int b = 0; b < NS; ++b) sp[b] = Packs<ANY, S, true, KP>(srow[b] + t.first);
+  const Packs<ANY, T, true, KP> gout(g_dst != nullptr ? g_dst + t.first : nullptr);
+  Pack<T, KP> vp[U], vg[U];
+  Pack<S, KP> vs[SS][U];
 #pragma unroll
   for (int u = 0; u < U; ++u) {
     const int64_t i = int64_t(u) * NTH + threadIdx.x;
@@ -1904,10 +1911,10 @@ __global__ __launch_bounds__((segment_threads<P, PRE>())) void segment_kernel(Se
           vg[u] = gout.load(i);  // a gap reads the consolidated gradient
         } else {
 #pragma unroll
-          for (int k = 0; k < kPack; ++k) vg[u].v[k] = zero;
+          for (int k = 0; k < KP; ++k) vg[u].v[k] = zero;
         }
       } else {
-        vg[u] = load_stream_any(g_src + t.first + i * kPack);
+        vg[u] = load_stream_any<true, KP>(g_src + t.first + i * KP);
       }
       if (load_state) {
 #pragma unroll
@@ -1924,10 +1931,10 @@ __global__ __launch_bounds__((segment_threads<P, PRE>())) void segment_kernel(Se
           if (store_grad) {
             gout.store(i, vg[u]);
           }
-          Pack<S> st[SS];
+          Pack<S, KP> st[SS];
 #pragma unroll
           for (int b = 0; b < NS; ++b) st[b] = vs[b][u];
-          apply_pack<P, kPack>(vp[u], vg[u], st, load_state, rp, mx);
+          apply_pack<P, KP>(vp[u], vg[u], st, load_state, rp, mx);
 #pragma unroll
           for (int b = 0; b < NS; ++b) vs[b][u] = st[b];
           store_stream(pp + i, vp[u]);
@@ -1961,10 +1968,22 @@ struct ScatterArgs {
 constexpr int kScatterThreads = 64;
 constexpr int kScatterUnroll = 1;
 constexpr uint32_t kScatterLds = 0;
-constexpr int64_t kScatterTile = int64_t(kScatterThreads) * kPack * kScatterUnroll;
+// Elements per pack of the scatter: 16 B per lane and access (config 5's
+// layout, same-process A/B against 4-element packs: float16 3.87 -> 6.71
+// TB/s, float64 3.30 -> 6.72).
+template <typename T>
+constexpr int scatter_pack() {
+  return static_cast<int>(16 / sizeof(T));
+}
+template <typename T>
+constexpr int64_t scatter_tile() {
+  return int64_t(kScatterThreads) * scatter_pack<T>() * kScatterUnroll;
+}
 
 template <typename T>
 __global__ __launch_bounds__(kScatterThreads) void scatter_kernel(ScatterArgs<T> a) {
+  constexpr int KP = scatter_pack<T>();
+  constexpr int64_t kScatterTile = scatter_tile<T>();
   const uint32_t tiles_per_row = a.seg.tile0[a.seg.n];
   const uint32_t r = blockIdx.x / tiles_per_row;
   const uint32_t local = blockIdx.x - r * tiles_per_row;
@@ -1974,17 +1993,17 @@ __global__ __launch_bounds__(kScatterThreads) void scatter_kernel(ScatterArgs<T>
   const T* src = a.seg.data[s] + int64_t(r) * a.seg.stride_r[s];
   T* dst = a.dst + int64_t(r) * a.dst_stride_r + a.seg.col[s];
   if ((a.seg.vec_ok >> s) & 1u) {
-    const SegTile t = seg_tile<T, kScatterTile>(a.res0, a.rmod, r, a.seg.col[s], numel, j0);
-    Pack<T> v[kScatterUnroll];
+    const SegTile t = seg_tile<T, kScatterTile, KP>(a.res0, a.rmod, r, a.seg.col[s], numel, j0);
+    Pack<T, KP> v[kScatterUnroll];
 #pragma unroll
     for (int u = 0; u < kScatterUnroll; ++u) {
       const int64_t i = int64_t(u) * kScatterThreads + threadIdx.x;
-      if (i < t.packs) v[u] = load_stream_any(src + t.first + i * kPack);
+      if (i < t.packs) v[u] = load_stream_any<true, KP>(src + t.first + i * KP);
     }
 #pragma unroll
     for (int u = 0; u < kScatterUnroll; ++u) {
       const int64_t i = int64_t(u) * kScatterThreads + threadIdx.x;
-      if (i < t.packs) store_stream(reinterpret_cast<Pack<T>*>(dst + t.first) + i, v[u]);
+      if (i < t.packs) store_stream(reinterpret_cast<Pack<T, KP>*>(dst + t.first) + i, v[u]);
     }
     seg_singles<kScatterThreads>(t, numel, [&](int64_t j) { dst[j] = src[j]; });
     return;
@@ -2537,7 +2556,8 @@ int launch_segments(const Call& c, int nbufs, const ts_segment* segs, int n_segs
     return walk_fits<T>(walk, c.R, tile, vec_rows, a.seg, nth);
   };
   return run_step<P>(c, a.k.vec, prepare, [&]() -> int {
-    const bool same_phase = rows_same_phase<P>(a.k.x, nbufs);
+    const bool same_phase =
+        rows_same_phase<P>(a.k.x, nbufs, stream_pack<typename P::T, typename P::S>());
     if constexpr (P::kPreWords > 0) {
       if (pre) {
         constexpr int nth = segment_threads<P, true>();

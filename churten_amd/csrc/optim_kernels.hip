@@ -34,10 +34,10 @@ int scatter(const ts_segment* segs, int n_segs, void* dst, int64_t dst_stride_r,
     return s.numel > 0;
   });
   if ((any && dst == nullptr) ||
-      !walk_fits<T>(walk, R, kScatterTile, vec_rows, a.seg, kScatterThreads)) {
+      !walk_fits<T>(walk, R, scatter_tile<T>(), vec_rows, a.seg, kScatterThreads)) {
     return kInvalid;
   }
-  return launch_walk<T>(walk, R, kScatterTile, vec_rows, a, a.seg, scatter_kernel<T>, stream,
+  return launch_walk<T>(walk, R, scatter_tile<T>(), vec_rows, a, a.seg, scatter_kernel<T>, stream,
                         kScatterLds, kScatterThreads);
 }
 
