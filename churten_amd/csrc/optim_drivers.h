@@ -609,13 +609,15 @@ struct AdamPolicy {
   static constexpr int kStreamPack = stream_pack<T, S>();
   static constexpr int kSegmentUnroll = stream_unroll<T, S>(2, 4, 4, 2);
   static constexpr int kSegmentThreads = kThreads;
-  // With a workspace, every type runs one-wavefront workgroups: one pack of
-  // 4 for float32 and bfloat16 moments, two for 16-bit params and float64.
-  // Same-process A/B on config 5's twelve per-parameter gradients, 4 rounds,
+  // With a workspace, every type runs one-wavefront workgroups: one 16-byte
+  // pack per thread (two for float64). Measured with 4-element packs (two for
+  // 16-bit params, the same bytes per thread as one 8-element pack now), in a
+  // same-process A/B on config 5's twelve per-parameter gradients, 4 rounds,
   // against 128 threads x 4 / 8 packs with the vector flag read: bfloat16
   // moments 6.20 TB/s against 5.54, float16 / bfloat16 params 5.93 / 6.18
-  // against 5.68 / 5.66 (128 threads x 2 / 4: 5.87 / 6.07 and 5.88 / 5.82).
-  // float64: two packs of 4, +1.6% against 128 threads x 2.
+  // against 5.68 / 5.66 (128 threads x 2 / 4: 5.87 / 6.07 and 5.88 / 5.82);
+  // the 8-element pack then +1.4% / +2.4%. float64: two 4-element packs +1.6%
+  // against 128 threads x 2, two 2-element packs +15.6% more.
   static constexpr int kSegmentThreadsPre = kStreamThreads;
   static constexpr int kSegmentUnrollPre = std::is_same<T, double>::value ? 2 : 1;
   // float32 Adam's segmented update with a workspace: the flag read through
@@ -744,10 +746,11 @@ struct SgdPolicy {
   // Segmented float32 updates: one-wavefront workgroups, one pack, the flag
   // read through the scalar cache (same-process A/B on config 5's twelve
   // per-parameter gradients, 4 rounds: 6.28 TB/s against 5.95 for 128 threads
-  // x 2 packs with the vector read; 128 x 1: 6.19). 16-bit: one wavefront x 2
-  // packs of 4, scalar read (float16 / bfloat16 6.33 / 6.29 against 5.76 /
-  // 5.71; one pack 5.46 / 5.37, four 5.92 / 5.91). bfloat16 state: one pack,
-  // +2.5% (two: -10%); float64: two packs, +0.9%.
+  // x 2 packs with the vector read; 128 x 1: 6.19). 16-bit: one wavefront x 8
+  // elements, scalar read (as two 4-element packs: float16 / bfloat16 6.33 /
+  // 6.29 against 5.76 / 5.71; 4 elements 5.46 / 5.37, 16 5.92 / 5.91).
+  // bfloat16 state: one pack, +2.5% (two: -10%); float64: two 2-element packs
+  // (+15.5% against two 4-element ones).
   static constexpr int kSegmentUnroll = std::is_same<T, double>::value ? 2 : 1;
   static constexpr int kSegmentThreads = kStreamThreads;
   static constexpr int kSegmentThreadsPre = kThreads;
@@ -817,9 +820,10 @@ struct AdagradPolicy {
   // twelve per-parameter gradients, 4 rounds: 6.34 TB/s against 5.97 for 128
   // threads x 2 packs with the vector read; under a cap of 20: 6.13). Without
   // a workspace the shape stays; the scalar read costs it 0.5%. 16-bit with a
-  // workspace: one wavefront x 4 packs of 4, scalar read (float16 / bfloat16
-  // 5.76 / 5.73 against 5.39 / 5.46; two packs 5.49 / 5.62, one 4.70 / 4.95).
-  // bfloat16 state: one pack, +2.4% (two: -10%); float64: two packs, +1.7%.
+  // workspace: one wavefront x 16 elements, scalar read (as four 4-element
+  // packs: float16 / bfloat16 5.76 / 5.73 against 5.39 / 5.46; 8 elements 5.49
+  // / 5.62, 4 4.70 / 4.95; as two 8-element packs +2.3% / +4% more).
+  // bfloat16 state: one pack, +2.4% (two: -10%); float64: two 2-element packs.
   static constexpr int kSegmentUnroll = sizeof(T) == 2 ? 1 : 2;
   static constexpr int kSegmentThreads = kThreads;
   static constexpr int kSegmentThreadsPre = kStreamThreads;
